@@ -1,0 +1,226 @@
+/*
+ * lisa_hip.h — C ABI of liblisa_hip.so, the MI355X replacement for the
+ * reference's Metal device bridge (src/device/metal.rs) and for the runner
+ * methods the speculative loop and the CLI call (src/model/runner.rs,
+ * src/speculative/mod.rs).
+ *
+ * Conventions (shared by every entry point):
+ *   - every call returns int: 0 on success, otherwise a negative LISA_E_* code
+ *     or a positive hipError_t value; lisa_last_error() gives the message of the
+ *     most recent failure on the calling thread. The reference panics on Metal
+ *     failures (metal.rs:153,195,240-245) and returns Result<_, String> from the
+ *     runner; a Rust binding maps non-zero returns to exactly those.
+ *   - handles are opaque; one stream per device handle, in-order, so a runner
+ *     or encoder may be driven by one thread at a time (the reference serializes
+ *     its Model behind a Mutex, src/serve/mod.rs:37-39).
+ *   - byte offsets are bytes (AGENTS.md:380-381 of the reference).
+ */
+#ifndef LISA_HIP_H
+#define LISA_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+  LISA_OK = 0,
+  LISA_E_ARG = -1,       /* invalid argument / shape */
+  LISA_E_STATE = -2,     /* call not valid in the current state */
+  LISA_E_CAPACITY = -3,  /* KV capacity exhausted */
+  LISA_E_VOCAB = -4,     /* token outside the vocabulary */
+  LISA_E_NOMODULE = -5,  /* kernel code object missing or unloadable */
+  LISA_E_NOMEM = -6
+};
+
+const char* lisa_last_error(void);
+
+/* ======================= device bridge (metal.rs) ======================== */
+typedef struct LisaDevice LisaDevice;
+typedef struct LisaBuffer LisaBuffer;
+typedef struct LisaModule LisaModule;
+typedef struct LisaFunction LisaFunction;
+typedef struct LisaEncoder LisaEncoder;
+typedef struct LisaGraph LisaGraph;
+typedef struct LisaEvent LisaEvent;
+
+/* MetalDevice::default (metal.rs:150-156): device `ordinal` with one stream. */
+int lisa_device_create(int ordinal, LisaDevice** out);
+void lisa_device_free(LisaDevice* dev);
+/* MetalDevice::name (metal.rs:159-167) */
+int lisa_device_name(LisaDevice* dev, char* buf, size_t len);
+/* recommendedMaxWorkingSetSize (metal.rs:169-173): total HBM bytes. */
+uint64_t lisa_device_max_working_set(LisaDevice* dev);
+/* new_buffer / new_untracked_buffer (metal.rs:175-197): hipMalloc'd,
+ * zero-filled. There is no hazard tracking: the stream is in order. */
+int lisa_buffer_alloc(LisaDevice* dev, size_t len, LisaBuffer** out);
+/* Drop for MetalBuffer (metal.rs:414-420). */
+void lisa_buffer_free(LisaBuffer* buf);
+uint64_t lisa_buffer_device_ptr(const LisaBuffer* buf);
+size_t lisa_buffer_len(const LisaBuffer* buf);
+/* write_bytes / read_bytes (metal.rs:396-409): synchronous with the stream. */
+int lisa_buffer_write(LisaBuffer* buf, size_t offset, const void* src, size_t len);
+int lisa_buffer_read(LisaBuffer* buf, size_t offset, void* dst, size_t len);
+/* Device-to-device copy on the stream (copy_bytes, norm.metal:118-130). */
+int lisa_buffer_copy(LisaBuffer* dst, size_t dst_off, const LisaBuffer* src, size_t src_off, size_t len);
+
+/* new_library + function_named (metal.rs:225-277): a gfx950 code object
+ * (.hsaco) by path or blob. lisa_module_load_default loads the kernels built
+ * with this library (lisa_kernels.hsaco next to liblisa_hip.so). */
+int lisa_module_load(LisaDevice* dev, const char* path, LisaModule** out);
+int lisa_module_load_data(LisaDevice* dev, const void* blob, size_t len, LisaModule** out);
+int lisa_module_load_default(LisaDevice* dev, LisaModule** out);
+void lisa_module_free(LisaModule* mod);
+int lisa_function_get(LisaModule* mod, const char* name, LisaFunction** out);
+
+/* Command buffer + compute encoder (metal.rs:297-381). Arguments are bound by
+ * index: set_buffer binds a device pointer (buffer + byte offset), set_bytes a
+ * value blob; a dispatch launches immediately on the device stream
+ * (hipModuleLaunchKernel), wait synchronizes the stream. */
+int lisa_encoder_begin(LisaDevice* dev, LisaEncoder** out);
+int lisa_encoder_set_function(LisaEncoder* enc, LisaFunction* fn);
+int lisa_encoder_set_buffer(LisaEncoder* enc, uint32_t index, const LisaBuffer* buf, uint64_t offset);
+int lisa_encoder_set_bytes(LisaEncoder* enc, uint32_t index, const void* bytes, size_t len);
+/* dispatch_thread_groups (metal.rs:366-376) */
+int lisa_encoder_dispatch_groups(LisaEncoder* enc, uint32_t gx, uint32_t gy, uint32_t gz, uint32_t tx,
+                                 uint32_t ty, uint32_t tz);
+/* dispatch_threads (metal.rs:354-364): total threads, ceil-divided into groups */
+int lisa_encoder_dispatch_threads(LisaEncoder* enc, uint32_t nx, uint32_t ny, uint32_t nz, uint32_t tx,
+                                  uint32_t ty, uint32_t tz);
+/* commit + wait_until_completed (metal.rs:314-320) and end. */
+int lisa_encoder_end(LisaEncoder* enc, int wait);
+
+/* hipGraph capture of everything dispatched between begin and end. */
+int lisa_capture_begin(LisaDevice* dev);
+int lisa_capture_end(LisaDevice* dev, LisaGraph** out);
+int lisa_graph_launch(LisaGraph* graph, LisaDevice* dev);
+void lisa_graph_free(LisaGraph* graph);
+int lisa_device_synchronize(LisaDevice* dev);
+
+/* Timing on the device stream (hipEvent). */
+int lisa_event_create(LisaEvent** out);
+void lisa_event_free(LisaEvent* ev);
+int lisa_event_record(LisaEvent* ev, LisaDevice* dev);
+int lisa_event_elapsed_ms(LisaEvent* start, LisaEvent* stop, float* ms);
+
+/* ============================ runner (runner.rs) ========================= */
+typedef struct LisaRunner LisaRunner;
+
+typedef struct LisaRunnerConfig {
+  int32_t layers;    /* multiple of 4; 64 for the 27B-shaped model */
+  int32_t vocab;     /* 248320 for the real vocabulary */
+  int32_t capacity;  /* KV capacity in positions (QwenRunner::load, runner.rs:337-417) */
+  int32_t with_mtp;  /* also build the 1-layer MTP drafter (MtpRunner::load, runner.rs:2443-2502) */
+  uint64_t seed;     /* synthetic checkpoint seed (lisa_synth.h) */
+  int32_t use_graph; /* capture the M=1 decode step into a hipGraph */
+  int32_t device;    /* device ordinal */
+} LisaRunnerConfig;
+
+/* Load: allocate the resident weight arena, generate the synthetic
+ * checkpoint in it, allocate state/KV/scratch, reset state. */
+int lisa_runner_create(const LisaRunnerConfig* cfg, LisaRunner** out);
+void lisa_runner_free(LisaRunner* r);
+LisaDevice* lisa_runner_device(LisaRunner* r);
+uint32_t lisa_runner_position(LisaRunner* r);
+uint64_t lisa_runner_weight_bytes(LisaRunner* r);
+
+/* reset_state (runner.rs:423-444): zero GDN/conv state and KV, position 0. */
+int lisa_runner_reset_state(LisaRunner* r);
+/* Synthetic context: GDN state N(0,0.01), conv history N(0,1), KV rows
+ * [0,filled) N(0,1) (target and drafter), position = filled. */
+int lisa_runner_fill_state(LisaRunner* r, uint32_t filled, uint64_t seed);
+
+/* forward_token_decode (runner.rs:555-591): one M=1 step; argmax (lowest
+ * index on ties) and optionally the bf16 hidden (before the final norm) as
+ * f32[5120]. */
+int lisa_runner_forward_token_decode(LisaRunner* r, uint32_t token, uint32_t* argmax, float* hidden);
+/* forward_token_with_hidden (runner.rs:510-550): also the f32 logits[vocab]. */
+int lisa_runner_forward_token_with_hidden(LisaRunner* r, uint32_t token, uint32_t* argmax, float* hidden,
+                                          float* logits);
+/* Greedy decode of `steps` tokens from `token` with device-side feedback
+ * (argmax -> next embed), replaying the captured step graph; tokens_out
+ * receives the `steps` generated tokens. The loop of src/cli/run.rs:69-73. */
+int lisa_runner_decode_greedy(LisaRunner* r, uint32_t token, int32_t steps, uint32_t* tokens_out);
+
+/* verify_block3_decode (runner.rs:734-909): M=3 pass with GDN/conv capture;
+ * argmax[3]; hidden (nullable) f32[3][5120]; logits (nullable) f32[3][vocab].
+ * position += 3 until commit. */
+int lisa_runner_verify_block3(LisaRunner* r, const uint32_t tokens[3], uint32_t argmax[3], float* hidden,
+                              float* logits);
+/* commit_verified_prefix (runner.rs:911-944): rows in 1..3. */
+int lisa_runner_commit_verified_prefix(LisaRunner* r, int32_t rows);
+
+/* checkpoint_state / restore_state (runner.rs:447-503). */
+typedef struct LisaCheckpoint LisaCheckpoint;
+int lisa_runner_checkpoint_state(LisaRunner* r, LisaCheckpoint** out);
+int lisa_runner_restore_state(LisaRunner* r, const LisaCheckpoint* ck);
+void lisa_checkpoint_free(LisaCheckpoint* ck);
+
+/* upload_hidden_device (runner.rs:850-858): host f32 hidden -> bf16
+ * (truncation, dtype.rs:42-47) into target hidden row `row`, the conditioning
+ * row the drafter reads with cond_source 0. */
+int lisa_runner_upload_hidden(LisaRunner* r, int32_t row, const float* hidden);
+int32_t lisa_runner_vocab(LisaRunner* r);
+
+/* Read back state for tests: GDN state of gdn layer `idx` (f32[48*128*128]),
+ * conv history (bf16[3*10240]). */
+int lisa_runner_read_gdn_state(LisaRunner* r, int32_t idx, float* out);
+int lisa_runner_read_conv_state(LisaRunner* r, int32_t idx, uint16_t* out);
+
+/* MtpRunner (runner.rs:2233-3701). cond_source: 0 = target hidden row
+ * `cond_row` (target.hidden_offset, runner.rs:846-848), 1 = the drafter's own
+ * last normalized hidden (draft chaining), 2 = the hidden uploaded with
+ * lisa_mtp_upload_cond. forward_position_decode_device (runner.rs:2711-2765). */
+int lisa_mtp_forward(LisaRunner* r, uint32_t token, int32_t cond_source, int32_t cond_row, uint32_t* argmax);
+/* upload_normalized_device (runner.rs:2685-2692): host f32 -> bf16 by
+ * truncation into the drafter's normalized-hidden slot (cond_source 1). */
+int lisa_mtp_upload_normalized(LisaRunner* r, const float* hidden);
+/* A free conditioning hidden (cond_source 2), bf16 bits. */
+int lisa_mtp_upload_cond(LisaRunner* r, const uint16_t* hidden);
+int lisa_mtp_read_normalized(LisaRunner* r, uint16_t* out);
+uint32_t lisa_mtp_position(LisaRunner* r);
+int lisa_mtp_trim_state(LisaRunner* r, int32_t count);
+
+/* ========================= speculative (speculative/mod.rs) ============== */
+typedef struct LisaAcceptance {
+  int32_t accepted_drafts;
+  int32_t emitted_count;
+  uint32_t emitted[3];
+  int32_t target_trim;
+} LisaAcceptance;
+/* accept_greedy (speculative/mod.rs:16-32); n_drafts <= 2. */
+int lisa_accept_greedy(const uint32_t* drafts, int32_t n_drafts, const uint32_t* target, LisaAcceptance* out);
+
+typedef struct LisaReconcilePlan {
+  int32_t trim;
+  int32_t replay_count;
+  int32_t replay[3]; /* draft index, or -1 for the replacement */
+} LisaReconcilePlan;
+/* mtp_reconcile_plan (speculative/mod.rs:49-65). */
+int lisa_mtp_reconcile_plan(int32_t draft_count, int32_t round_appended, int32_t accepted, LisaReconcilePlan* out);
+
+typedef struct LisaSpecStats {
+  int32_t rounds;
+  int32_t accepted_drafts;
+  int32_t drafted_tokens;
+  int32_t target_forwards;
+} LisaSpecStats;
+/* generate_greedy_block3_prefilled (speculative/mod.rs:384-413, loop
+ * :102-198). `bonus` and `target_hidden` (f32[5120]) come from the prefill;
+ * mtp_seed_token/mtp_seed_hidden (f32[5120]) seed the drafter. When
+ * force_truth is non-null, every draft is replaced before verification by
+ * force_truth[j] (the target-only greedy token at that output position) with
+ * probability p_accept under the seeded stream force_seed, else by a token
+ * that differs from it — a forced acceptance pattern exercising 1, 2 and 3
+ * accepted rows. tokens_out receives max_tokens tokens (bonus first). */
+int lisa_generate_greedy_block3(LisaRunner* r, uint32_t bonus, const float* target_hidden,
+                                uint32_t mtp_seed_token, const float* mtp_seed_hidden, int32_t max_tokens,
+                                const uint32_t* force_truth, int32_t force_len, uint64_t force_seed,
+                                float p_accept, uint32_t* tokens_out, LisaSpecStats* stats);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* LISA_HIP_H */

@@ -1,0 +1,160 @@
+/*
+ * lisa_kernels.h — argument blocks of the gfx950 kernels in lisa_kernels.hsaco.
+ *
+ * Every kernel takes exactly one by-value argument block, so a dispatch is
+ * `lisa_encoder_set_bytes(enc, 0, &params, sizeof params)` followed by
+ * `lisa_encoder_dispatch_groups` — the same set_bytes/dispatch_thread_groups
+ * pattern the reference's encoders use (src/device/metal.rs:342-376). Device
+ * addresses are plain 64-bit pointers (lisa_buffer_device_ptr + byte offset).
+ *
+ * Kernel names (hipModuleGetFunction) are listed next to each block.
+ */
+#ifndef LISA_KERNELS_H
+#define LISA_KERNELS_H
+
+#include <stdint.h>
+
+/* ---- q4 linear with fused prologue/epilogue -----------------------------
+ * Kernels: lisa_qmv_k{5120,6144,10240,17408}_m{1,3}
+ * Weights use the resident layout: W u32[N][K/8] (MLX, low nibble first) and
+ * SB u32[N][K/64] with SB = scale_bf16 | bias_bf16 << 16 (one load per group).
+ * One launch covers up to 4 matrices that share the input x; the virtual row
+ * space is split into 8-row tiles, each matrix owning a contiguous tile range
+ * [tile_start[e], tile_start[e+1]). ksplit is 4 when the launch has at most
+ * 8192 virtual rows (the N=5120 projections), else 1: a fixed rule, so the
+ * summation order of every output is a function of the launch shape. */
+#define LISA_QMV_MAX_MATS 4
+
+enum {
+  LISA_PRO_LOADX = 0,   /* x = bf16 x_in[M][K] */
+  LISA_PRO_RESNORM = 1, /* r = bf16(h_in + bf16(o_in)); x = RMSNorm(r, norm_w) */
+  LISA_PRO_EMBED = 2,   /* r = q4 embedding row of tokens[m]; x = RMSNorm(r) */
+  LISA_PRO_CAST = 3,    /* r = bf16(o_in); x = RMSNorm(r) */
+  LISA_PRO_NORM = 4,    /* r = h_in; x = RMSNorm(r) */
+  LISA_PRO_MTPFC = 5    /* x = [RMSNorm(embed(tok), norm_w) | RMSNorm(x_in, norm_w2)] */
+};
+
+enum {
+  LISA_EPI_STORE = 0,  /* out f32[M][rows] */
+  LISA_EPI_GATEUP = 1, /* rows j of (w, w2) -> out bf16[M][rows] = bf16(silu(g)*u) */
+  LISA_EPI_CONV = 2,   /* GDN qkv: causal conv + SiLU -> out f32[M][rows], conv state update */
+  LISA_EPI_ARGMAX = 3  /* out f32 logits[M][rows] + per-workgroup (max, idx) partials */
+};
+
+typedef struct LisaQ4Mat {
+  const uint32_t* w;
+  const uint32_t* sb;
+  const uint32_t* w2; /* GATEUP: up projection */
+  const uint32_t* sb2;
+  void* out;
+  uint32_t rows;
+  uint32_t kind;
+} LisaQ4Mat;
+
+typedef struct LisaQmvParams {
+  /* prologue */
+  const uint16_t* x_in;
+  const uint16_t* h_in;
+  const float* o_in;
+  const uint32_t* tokens;
+  const uint32_t* emb_w;
+  const uint32_t* emb_sb;
+  const uint16_t* norm_w;
+  const uint16_t* norm_w2;
+  uint16_t* r_out; /* written by workgroup 0: r rows bf16[M][5120] */
+  uint16_t* x_out; /* written by workgroup 0: normalized x bf16[M][K] */
+  /* CONV epilogue */
+  const uint16_t* conv_w;  /* bf16[10240][4] */
+  uint16_t* conv_state;    /* bf16[3][10240] of this layer */
+  uint16_t* conv_slots;    /* slot 0 of this layer, bf16[3][10240]; nullable */
+  uint64_t conv_slot_stride; /* elements between slot t and t+1 */
+  /* ARGMAX epilogue */
+  float* am_val; /* [M][gridDim.x] */
+  uint32_t* am_idx;
+  /* matrices */
+  LisaQ4Mat mats[LISA_QMV_MAX_MATS];
+  uint32_t tile_start[LISA_QMV_MAX_MATS + 1];
+  uint32_t n_mats;
+  uint32_t pro_mode;
+  uint32_t capture;
+  uint32_t ksplit; /* 1 or 4: waves of a workgroup split K of one tile */
+} LisaQmvParams;
+
+/* ---- GDN recurrence + gated RMSNorm --------------------------------------
+ * Kernels: lisa_gdn_recurrence_m{1,3}; grid 48 workgroups x 512 threads. */
+typedef struct LisaGdnParams {
+  const float* conv_out; /* [M][10240] */
+  const float* z;        /* [M][6144] raw */
+  const float* a;        /* [M][48] raw */
+  const float* b;        /* [M][48] raw */
+  const uint16_t* a_log;
+  const uint16_t* dt_bias;
+  const uint16_t* norm_w;
+  float* state;    /* this layer [48][128][128] */
+  float* slots;    /* slot 0 of this layer; nullable */
+  uint64_t slot_stride; /* floats between slot t and t+1 */
+  uint16_t* gated; /* [M][6144] bf16 */
+  float* y_out;    /* nullable: pre-norm readout [M][6144] */
+  float q_scale, k_scale;
+  uint32_t capture;
+  uint32_t pad0;
+} LisaGdnParams;
+
+/* ---- split-K decode attention --------------------------------------------
+ * Kernels: lisa_attn_partial_m{1,3} grid (s_max, 4) x 256,
+ *          lisa_attn_merge_m{1,3}   grid (24, M) x 256. */
+typedef struct LisaAttnParams {
+  const float* q_proj; /* [M][12288] raw */
+  const float* k_raw;  /* [M][1024] */
+  const float* v_raw;  /* [M][1024] */
+  const uint16_t* q_norm_w;
+  const uint16_t* k_norm_w;
+  uint16_t* key_cache;   /* this layer [4][capacity][256] */
+  uint16_t* value_cache;
+  float* part_o;  /* [M][24][s_max][256] */
+  float* part_ml; /* [M][24][s_max][2] = (max, denominator) */
+  const uint32_t* pos; /* device position of row 0 */
+  uint16_t* gated;     /* [M][6144] bf16 */
+  uint32_t capacity;
+  uint32_t s_max;
+} LisaAttnParams;
+
+/* ---- argmax finish + device-side step bookkeeping ------------------------
+ * Kernel: lisa_step_finalize, grid 1 x 256. */
+typedef struct LisaFinalizeParams {
+  const float* am_val;
+  const uint32_t* am_idx;
+  uint32_t* argmax_out;  /* [M] */
+  uint32_t* next_token;  /* nullable: receives argmax[M-1] */
+  uint32_t* history;     /* nullable: history[*step] = argmax[0] */
+  uint32_t* step;        /* nullable */
+  uint32_t* pos;         /* nullable: *pos += pos_advance */
+  uint32_t n_part;
+  uint32_t m_rows;
+  uint32_t pos_advance;
+  uint32_t history_cap;
+} LisaFinalizeParams;
+
+/* ---- synthetic fills -------------------------------------------------------
+ * Kernel: lisa_synth_fill, grid-stride. */
+enum {
+  LISA_FILL_WORDS = 0, /* u32 words */
+  LISA_FILL_BF16 = 1,  /* bf16 of lisa_synth_value(key, i, dist, a, b) */
+  LISA_FILL_F32 = 2,
+  LISA_FILL_SB = 3,    /* packed q4 scale/bias pairs from key (scales) and key2 (biases) */
+  LISA_FILL_KV = 4     /* bf16 [4][capacity][256] rows < filled, index (kvh<<20 + pos)*256 + d */
+};
+
+typedef struct LisaSynthParams {
+  void* out;
+  uint64_t n;
+  uint64_t key;
+  uint64_t key2;
+  uint32_t kind;
+  uint32_t dist;
+  float a, b;
+  uint32_t capacity;
+  uint32_t filled;
+} LisaSynthParams;
+
+#endif /* LISA_KERNELS_H */

@@ -1,0 +1,64 @@
+// bridge.h — internal definitions of the opaque handles of lisa_hip.h, shared
+// by device.cpp (the bridge) and runner.cpp (the runner built on it).
+#ifndef LISA_BRIDGE_H
+#define LISA_BRIDGE_H
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <string>
+#include <vector>
+
+struct LisaDevice {
+  int ordinal = 0;
+  hipStream_t stream = nullptr;
+  std::string name, arch;
+  uint64_t total_mem = 0;
+  int cu_count = 0;
+};
+
+struct LisaBuffer {
+  LisaDevice* dev = nullptr;
+  void* ptr = nullptr;
+  size_t len = 0;
+};
+
+struct LisaModule {
+  LisaDevice* dev;
+  hipModule_t mod;
+};
+
+struct LisaFunction {
+  hipFunction_t fn;
+  std::string name;
+};
+
+struct LisaEncoder {
+  LisaDevice* dev = nullptr;
+  LisaFunction* fn = nullptr;
+  std::vector<std::vector<uint8_t>> args;
+};
+
+struct LisaGraph {
+  hipGraph_t graph;
+  hipGraphExec_t exec;
+};
+
+struct LisaEvent {
+  hipEvent_t ev;
+};
+
+int lisa_fail(int code, const char* fmt, ...);
+int lisa_hip_check(hipError_t e, const char* what);
+std::string lisa_library_dir();
+// Launch a kernel taking one by-value argument block.
+int lisa_launch(LisaDevice* d, LisaFunction* f, const void* params, size_t len, uint32_t gx, uint32_t gy,
+                uint32_t gz, uint32_t tx, uint32_t ty, uint32_t tz);
+
+#define LISA_TRY(expr)          \
+  do {                          \
+    const int lisa_rc_ = (expr); \
+    if (lisa_rc_) return lisa_rc_; \
+  } while (0)
+
+#endif  // LISA_BRIDGE_H

@@ -1,0 +1,925 @@
+// runner.cpp — the decode-path runner behind include/lisa_hip.h: a C++
+// restatement of the reference's QwenRunner / MtpRunner (src/model/runner.rs)
+// and greedy block-3 speculative loop (src/speculative/mod.rs), driving the
+// gfx950 kernels through the bridge of device.cpp.
+//
+// Per-token dispatch recipe (one hipGraph for M=1):
+//   layer i, GDN      : qmv[in_proj: embed|residual + input RMSNorm -> qkv(conv)|z|a|b]
+//                       gdn_recurrence -> gated;  qmv[out_proj] -> branch
+//   layer i, attention: qmv[in_proj -> q|k|v];  attn_partial;  attn_merge -> gated;
+//                       qmv[o_proj] -> branch
+//   every layer       : qmv[residual + post RMSNorm -> gate/up -> SwiGLU];  qmv[down] -> branch
+//   final             : qmv[residual + final RMSNorm -> lm_head -> argmax partials];  step_finalize
+// 5 launches per GDN layer, 6 per attention layer, 2 final (338 for 64 layers)
+// against the reference's 852 dispatches (runner.rs:568-582, 1248-1592).
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdlib>
+#include <cstring>
+#include <memory>
+#include <string>
+#include <vector>
+
+#include "bridge.h"
+#include "lisa_hip.h"
+#include "lisa_kernels.h"
+#include "lisa_model.h"
+#include "lisa_numerics.h"
+#include "lisa_synth.h"
+
+namespace {
+
+constexpr uint32_t kHistoryCap = 1u << 16;
+
+struct Q4Dev {
+  uint32_t* w = nullptr;
+  uint32_t* sb = nullptr;
+  uint32_t n = 0, k = 0;
+};
+
+struct LayerDev {
+  bool attention = false;
+  uint16_t *input_norm = nullptr, *post_norm = nullptr;
+  Q4Dev gate, up, down;
+  Q4Dev qkv, z, a, b, out;
+  uint16_t *conv_w = nullptr, *a_log = nullptr, *dt_bias = nullptr, *gnorm = nullptr;
+  int state_index = -1;
+  Q4Dev q, k, v, o;
+  uint16_t *q_norm = nullptr, *k_norm = nullptr;
+  int cache_index = -1;
+};
+
+struct MtpDev {
+  uint16_t *pre_fc_emb, *pre_fc_hid, *input_norm, *post_norm, *final_norm, *q_norm, *k_norm;
+  Q4Dev fc, q, k, v, o, gate, up, down;
+};
+
+// Scratch of one forward context (target: rows <= 3; drafter: 1 row).
+struct Ctx {
+  int rows = 1;
+  uint16_t *H, *R, *gated, *act, *xnorm, *cond;
+  float *B, *conv_out, *z, *a, *b, *q_proj, *k_raw, *v_raw, *part_o, *part_ml, *logits, *am_val;
+  uint32_t *am_idx, *tokens, *argmax, *pos, *step, *history;
+};
+
+size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+// Bump allocator over one device buffer; a first pass with base==nullptr
+// only measures.
+struct Arena {
+  char* base = nullptr;
+  size_t used = 0;
+  template <typename T>
+  T* take(size_t count) {
+    used = align256(used);
+    T* p = base ? reinterpret_cast<T*>(base + used) : nullptr;
+    used += count * sizeof(T);
+    return p;
+  }
+};
+
+}  // namespace
+
+struct LisaCheckpoint {
+  LisaBuffer* gdn = nullptr;
+  LisaBuffer* conv = nullptr;
+  uint32_t position = 0;
+};
+
+struct LisaRunner {
+  LisaRunnerConfig cfg{};
+  LisaDevice* dev = nullptr;
+  LisaModule* mod = nullptr;
+  // kernels
+  LisaFunction *qmv[2][5] = {};  // [m3][K index]
+  LisaFunction *gdn[2] = {}, *attn_part[2] = {}, *attn_merge[2] = {}, *finalize = nullptr, *synth = nullptr;
+  // memory
+  LisaBuffer *weights = nullptr, *state = nullptr, *scratch = nullptr;
+  std::vector<LayerDev> layers;
+  Q4Dev embed, head;
+  uint16_t* final_norm = nullptr;
+  MtpDev mtp{};
+  int gdn_layers = 0, attn_layers = 0;
+  uint32_t s_max = 0;
+  float* gdn_state = nullptr;
+  uint16_t* conv_state = nullptr;
+  float* gdn_slots = nullptr;
+  uint16_t* conv_slots = nullptr;
+  uint16_t *key_cache = nullptr, *value_cache = nullptr;
+  uint16_t *mtp_key = nullptr, *mtp_value = nullptr;
+  Ctx tgt{}, drf{};
+  // host mirrors
+  uint32_t position = 0;
+  int64_t verify_base = -1;
+  uint32_t mtp_position = 0;
+  LisaGraph* step_graph = nullptr;
+  uint32_t qmv_grid_cap = 1024;
+};
+
+namespace {
+
+int k_index(uint32_t k) {
+  switch (k) {
+    case 5120: return 0;
+    case 6144: return 1;
+    case 10240: return 2;
+    case 17408: return 3;
+    case 1024: return 4;
+    default: return -1;
+  }
+}
+
+int upload_u32(LisaRunner* r, uint32_t* dst, const uint32_t* src, size_t n) {
+  return lisa_hip_check(hipMemcpyAsync(dst, src, n * 4, hipMemcpyHostToDevice, r->dev->stream), "H2D");
+}
+
+int sync(LisaRunner* r) { return lisa_hip_check(hipStreamSynchronize(r->dev->stream), "hipStreamSynchronize"); }
+
+// ---- synthetic checkpoint ----------------------------------------------------
+int fill(LisaRunner* r, void* out, uint64_t n, uint32_t kind, uint64_t key, uint64_t key2, uint32_t dist, float a,
+         float b, uint32_t capacity = 0, uint32_t filled = 0) {
+  LisaSynthParams p{};
+  p.out = out;
+  p.n = n;
+  p.key = key;
+  p.key2 = key2;
+  p.kind = kind;
+  p.dist = dist;
+  p.a = a;
+  p.b = b;
+  p.capacity = capacity;
+  p.filled = filled;
+  const uint64_t groups = std::min<uint64_t>((n + 255) / 256, 65536);
+  return lisa_launch(r->dev, r->synth, &p, sizeof p, (uint32_t)std::max<uint64_t>(groups, 1), 1, 1, 256, 1, 1);
+}
+
+uint64_t key_of(const LisaRunner* r, int scope, int kind, int part) {
+  return lisa_stream_key(r->cfg.seed, lisa_tensor_id(scope, kind, part));
+}
+
+int gen_q4(LisaRunner* r, const Q4Dev& q, int scope, int kind) {
+  LISA_TRY(fill(r, q.w, (uint64_t)q.n * q.k / 8, LISA_FILL_WORDS, key_of(r, scope, kind, 0), 0, 0, 0, 0));
+  return fill(r, q.sb, (uint64_t)q.n * q.k / 64, LISA_FILL_SB, key_of(r, scope, kind, 1), key_of(r, scope, kind, 2), 0,
+              0, 0);
+}
+
+int gen_vec(LisaRunner* r, uint16_t* v, uint64_t n, int scope, int kind, float lo, float hi) {
+  return fill(r, v, n, LISA_FILL_BF16, key_of(r, scope, kind, 0), 0, LISA_DIST_UNIFORM, lo, hi);
+}
+
+Q4Dev take_q4(Arena& A, uint32_t n, uint32_t k) {
+  Q4Dev q;
+  q.n = n;
+  q.k = k;
+  q.w = A.take<uint32_t>((size_t)n * k / 8);
+  q.sb = A.take<uint32_t>((size_t)n * k / 64);
+  return q;
+}
+
+void plan_weights(LisaRunner* r, Arena& A) {
+  const int L = r->cfg.layers;
+  r->layers.assign(L, LayerDev());
+  r->gdn_layers = r->attn_layers = 0;
+  for (int i = 0; i < L; ++i) {
+    LayerDev& l = r->layers[i];
+    l.attention = lisa_layer_is_attention(i);
+    l.input_norm = A.take<uint16_t>(LISA_HIDDEN);
+    l.post_norm = A.take<uint16_t>(LISA_HIDDEN);
+    l.gate = take_q4(A, LISA_INTER, LISA_HIDDEN);
+    l.up = take_q4(A, LISA_INTER, LISA_HIDDEN);
+    l.down = take_q4(A, LISA_HIDDEN, LISA_INTER);
+    if (l.attention) {
+      l.q = take_q4(A, LISA_ATT_Q_OUT, LISA_HIDDEN);
+      l.k = take_q4(A, LISA_ATT_KV_OUT, LISA_HIDDEN);
+      l.v = take_q4(A, LISA_ATT_KV_OUT, LISA_HIDDEN);
+      l.o = take_q4(A, LISA_HIDDEN, LISA_ATT_OUT);
+      l.q_norm = A.take<uint16_t>(LISA_ATT_HD);
+      l.k_norm = A.take<uint16_t>(LISA_ATT_HD);
+      l.cache_index = r->attn_layers++;
+    } else {
+      l.qkv = take_q4(A, LISA_GDN_CONV_DIM, LISA_HIDDEN);
+      l.z = take_q4(A, LISA_GDN_VALUE_DIM, LISA_HIDDEN);
+      l.a = take_q4(A, LISA_GDN_VH, LISA_HIDDEN);
+      l.b = take_q4(A, LISA_GDN_VH, LISA_HIDDEN);
+      l.out = take_q4(A, LISA_HIDDEN, LISA_GDN_VALUE_DIM);
+      l.conv_w = A.take<uint16_t>(LISA_GDN_CONV_DIM * 4);
+      l.a_log = A.take<uint16_t>(LISA_GDN_VH);
+      l.dt_bias = A.take<uint16_t>(LISA_GDN_VH);
+      l.gnorm = A.take<uint16_t>(LISA_GDN_HD);
+      l.state_index = r->gdn_layers++;
+    }
+  }
+  r->embed = take_q4(A, r->cfg.vocab, LISA_HIDDEN);
+  r->head = take_q4(A, r->cfg.vocab, LISA_HIDDEN);
+  r->final_norm = A.take<uint16_t>(LISA_HIDDEN);
+  if (r->cfg.with_mtp) {
+    MtpDev& t = r->mtp;
+    t.pre_fc_emb = A.take<uint16_t>(LISA_HIDDEN);
+    t.pre_fc_hid = A.take<uint16_t>(LISA_HIDDEN);
+    t.input_norm = A.take<uint16_t>(LISA_HIDDEN);
+    t.post_norm = A.take<uint16_t>(LISA_HIDDEN);
+    t.final_norm = A.take<uint16_t>(LISA_HIDDEN);
+    t.q_norm = A.take<uint16_t>(LISA_ATT_HD);
+    t.k_norm = A.take<uint16_t>(LISA_ATT_HD);
+    t.fc = take_q4(A, LISA_HIDDEN, 2 * LISA_HIDDEN);
+    t.q = take_q4(A, LISA_ATT_Q_OUT, LISA_HIDDEN);
+    t.k = take_q4(A, LISA_ATT_KV_OUT, LISA_HIDDEN);
+    t.v = take_q4(A, LISA_ATT_KV_OUT, LISA_HIDDEN);
+    t.o = take_q4(A, LISA_HIDDEN, LISA_ATT_OUT);
+    t.gate = take_q4(A, LISA_INTER, LISA_HIDDEN);
+    t.up = take_q4(A, LISA_INTER, LISA_HIDDEN);
+    t.down = take_q4(A, LISA_HIDDEN, LISA_INTER);
+  }
+}
+
+int generate_weights(LisaRunner* r) {
+  for (int i = 0; i < r->cfg.layers; ++i) {
+    const LayerDev& l = r->layers[i];
+    const int sc = i + 1;
+    LISA_TRY(gen_vec(r, l.input_norm, LISA_HIDDEN, sc, LISA_T_INPUT_NORM, 0.9f, 1.1f));
+    LISA_TRY(gen_vec(r, l.post_norm, LISA_HIDDEN, sc, LISA_T_POST_NORM, 0.9f, 1.1f));
+    LISA_TRY(gen_q4(r, l.gate, sc, LISA_T_MLP_GATE));
+    LISA_TRY(gen_q4(r, l.up, sc, LISA_T_MLP_UP));
+    LISA_TRY(gen_q4(r, l.down, sc, LISA_T_MLP_DOWN));
+    if (l.attention) {
+      LISA_TRY(gen_q4(r, l.q, sc, LISA_T_ATT_Q));
+      LISA_TRY(gen_q4(r, l.k, sc, LISA_T_ATT_K));
+      LISA_TRY(gen_q4(r, l.v, sc, LISA_T_ATT_V));
+      LISA_TRY(gen_q4(r, l.o, sc, LISA_T_ATT_O));
+      LISA_TRY(gen_vec(r, l.q_norm, LISA_ATT_HD, sc, LISA_T_ATT_Q_NORM, 0.9f, 1.1f));
+      LISA_TRY(gen_vec(r, l.k_norm, LISA_ATT_HD, sc, LISA_T_ATT_K_NORM, 0.9f, 1.1f));
+    } else {
+      LISA_TRY(gen_q4(r, l.qkv, sc, LISA_T_GDN_QKV));
+      LISA_TRY(gen_q4(r, l.z, sc, LISA_T_GDN_Z));
+      LISA_TRY(gen_q4(r, l.a, sc, LISA_T_GDN_A));
+      LISA_TRY(gen_q4(r, l.b, sc, LISA_T_GDN_B));
+      LISA_TRY(gen_q4(r, l.out, sc, LISA_T_GDN_OUT));
+      LISA_TRY(gen_vec(r, l.conv_w, LISA_GDN_CONV_DIM * 4, sc, LISA_T_GDN_CONV_W, -0.5f, 0.5f));
+      LISA_TRY(gen_vec(r, l.a_log, LISA_GDN_VH, sc, LISA_T_GDN_A_LOG, -2.0f, 0.0f));
+      LISA_TRY(gen_vec(r, l.dt_bias, LISA_GDN_VH, sc, LISA_T_GDN_DT_BIAS, -1.0f, 1.0f));
+      LISA_TRY(gen_vec(r, l.gnorm, LISA_GDN_HD, sc, LISA_T_GDN_NORM, 0.9f, 1.1f));
+    }
+  }
+  LISA_TRY(gen_q4(r, r->embed, 0, LISA_T_EMBED));
+  LISA_TRY(gen_q4(r, r->head, 0, LISA_T_LM_HEAD));
+  LISA_TRY(gen_vec(r, r->final_norm, LISA_HIDDEN, 0, LISA_T_FINAL_NORM, 0.9f, 1.1f));
+  if (r->cfg.with_mtp) {
+    const int sc = LISA_SCOPE_MTP;
+    const MtpDev& t = r->mtp;
+    LISA_TRY(gen_vec(r, t.pre_fc_emb, LISA_HIDDEN, sc, LISA_T_MTP_PRE_FC_EMB, 0.9f, 1.1f));
+    LISA_TRY(gen_vec(r, t.pre_fc_hid, LISA_HIDDEN, sc, LISA_T_MTP_PRE_FC_HID, 0.9f, 1.1f));
+    LISA_TRY(gen_vec(r, t.input_norm, LISA_HIDDEN, sc, LISA_T_INPUT_NORM, 0.9f, 1.1f));
+    LISA_TRY(gen_vec(r, t.post_norm, LISA_HIDDEN, sc, LISA_T_POST_NORM, 0.9f, 1.1f));
+    LISA_TRY(gen_vec(r, t.final_norm, LISA_HIDDEN, sc, LISA_T_FINAL_NORM, 0.9f, 1.1f));
+    LISA_TRY(gen_vec(r, t.q_norm, LISA_ATT_HD, sc, LISA_T_ATT_Q_NORM, 0.9f, 1.1f));
+    LISA_TRY(gen_vec(r, t.k_norm, LISA_ATT_HD, sc, LISA_T_ATT_K_NORM, 0.9f, 1.1f));
+    LISA_TRY(gen_q4(r, t.fc, sc, LISA_T_MTP_FC));
+    LISA_TRY(gen_q4(r, t.q, sc, LISA_T_ATT_Q));
+    LISA_TRY(gen_q4(r, t.k, sc, LISA_T_ATT_K));
+    LISA_TRY(gen_q4(r, t.v, sc, LISA_T_ATT_V));
+    LISA_TRY(gen_q4(r, t.o, sc, LISA_T_ATT_O));
+    LISA_TRY(gen_q4(r, t.gate, sc, LISA_T_MLP_GATE));
+    LISA_TRY(gen_q4(r, t.up, sc, LISA_T_MLP_UP));
+    LISA_TRY(gen_q4(r, t.down, sc, LISA_T_MLP_DOWN));
+  }
+  return sync(r);
+}
+
+void plan_state(LisaRunner* r, Arena& A) {
+  const size_t cap = (size_t)r->cfg.capacity;
+  r->gdn_state = A.take<float>((size_t)r->gdn_layers * LISA_GDN_STATE);
+  r->conv_state = A.take<uint16_t>((size_t)r->gdn_layers * 3 * LISA_GDN_CONV_DIM);
+  r->gdn_slots = A.take<float>((size_t)2 * r->gdn_layers * LISA_GDN_STATE);
+  r->conv_slots = A.take<uint16_t>((size_t)2 * r->gdn_layers * 3 * LISA_GDN_CONV_DIM);
+  r->key_cache = A.take<uint16_t>((size_t)r->attn_layers * LISA_ATT_KVH * cap * LISA_ATT_HD);
+  r->value_cache = A.take<uint16_t>((size_t)r->attn_layers * LISA_ATT_KVH * cap * LISA_ATT_HD);
+  if (r->cfg.with_mtp) {
+    r->mtp_key = A.take<uint16_t>((size_t)LISA_ATT_KVH * cap * LISA_ATT_HD);
+    r->mtp_value = A.take<uint16_t>((size_t)LISA_ATT_KVH * cap * LISA_ATT_HD);
+  }
+}
+
+void plan_ctx(LisaRunner* r, Arena& A, Ctx& c, int rows) {
+  c.rows = rows;
+  c.H = A.take<uint16_t>((size_t)3 * LISA_HIDDEN);
+  c.R = A.take<uint16_t>((size_t)rows * LISA_HIDDEN);
+  c.B = A.take<float>((size_t)rows * LISA_HIDDEN);
+  c.conv_out = A.take<float>((size_t)rows * LISA_GDN_CONV_DIM);
+  c.z = A.take<float>((size_t)rows * LISA_GDN_VALUE_DIM);
+  c.a = A.take<float>((size_t)rows * LISA_GDN_VH);
+  c.b = A.take<float>((size_t)rows * LISA_GDN_VH);
+  c.gated = A.take<uint16_t>((size_t)rows * LISA_ATT_OUT);
+  c.act = A.take<uint16_t>((size_t)rows * LISA_INTER);
+  c.q_proj = A.take<float>((size_t)rows * LISA_ATT_Q_OUT);
+  c.k_raw = A.take<float>((size_t)rows * LISA_ATT_KV_OUT);
+  c.v_raw = A.take<float>((size_t)rows * LISA_ATT_KV_OUT);
+  c.part_o = A.take<float>((size_t)rows * LISA_ATT_QH * r->s_max * LISA_ATT_HD);
+  c.part_ml = A.take<float>((size_t)rows * LISA_ATT_QH * r->s_max * 2);
+  c.logits = A.take<float>((size_t)rows * r->cfg.vocab);
+  c.am_val = A.take<float>((size_t)rows * 4096);
+  c.am_idx = A.take<uint32_t>((size_t)rows * 4096);
+  c.xnorm = A.take<uint16_t>((size_t)rows * LISA_HIDDEN);
+  c.cond = A.take<uint16_t>(LISA_HIDDEN);
+  c.tokens = A.take<uint32_t>(4);
+  c.argmax = A.take<uint32_t>(4);
+  c.pos = A.take<uint32_t>(4);
+  c.step = A.take<uint32_t>(4);
+  c.history = A.take<uint32_t>(kHistoryCap);
+}
+
+// ---- launch helpers --------------------------------------------------------------
+struct MatSpec {
+  const Q4Dev* w;
+  const Q4Dev* w2;  // GATEUP
+  void* out;
+  uint32_t kind;
+};
+
+int launch_qmv(LisaRunner* r, int m_rows, uint32_t K, LisaQmvParams& p, const std::vector<MatSpec>& mats) {
+  const int ki = k_index(K);
+  if (ki < 0) return lisa_fail(LISA_E_ARG, "no q4 kernel for K=%u", K);
+  LisaFunction* fn = r->qmv[m_rows == 3 ? 1 : 0][ki];
+  if (!fn) return lisa_fail(LISA_E_ARG, "no q4 kernel for K=%u M=%d", K, m_rows);
+  p.n_mats = (uint32_t)mats.size();
+  uint32_t tiles = 0, rows_total = 0;
+  for (size_t e = 0; e < mats.size(); ++e) {
+    const MatSpec& s = mats[e];
+    if (s.w->k != K) return lisa_fail(LISA_E_ARG, "q4 launch mixes K");
+    LisaQ4Mat& m = p.mats[e];
+    m.w = s.w->w;
+    m.sb = s.w->sb;
+    m.w2 = s.w2 ? s.w2->w : nullptr;
+    m.sb2 = s.w2 ? s.w2->sb : nullptr;
+    m.out = s.out;
+    m.rows = s.w->n;
+    m.kind = s.kind;
+    p.tile_start[e] = tiles;
+    const bool pair = s.kind == LISA_EPI_GATEUP;
+    tiles += pair ? (s.w->n + 3) / 4 : (s.w->n + 7) / 8;
+    rows_total += pair ? 2 * s.w->n : s.w->n;
+  }
+  p.tile_start[mats.size()] = tiles;
+  p.ksplit = rows_total <= 8192 ? 4 : 1;
+  uint32_t grid = p.ksplit == 4 ? tiles : (tiles + 3) / 4;
+  grid = std::max<uint32_t>(1, std::min(grid, r->qmv_grid_cap));
+  if (p.am_val && grid > 4096) grid = 4096;
+  return lisa_launch(r->dev, fn, &p, sizeof p, grid, 1, 1, 256, 1, 1);
+}
+
+LisaQmvParams pro_resnorm(const uint16_t* h, const float* o, const uint16_t* w, uint16_t* r_out) {
+  LisaQmvParams p{};
+  p.pro_mode = LISA_PRO_RESNORM;
+  p.h_in = h;
+  p.o_in = o;
+  p.norm_w = w;
+  p.r_out = r_out;
+  return p;
+}
+
+LisaQmvParams pro_loadx(const uint16_t* x) {
+  LisaQmvParams p{};
+  p.pro_mode = LISA_PRO_LOADX;
+  p.x_in = x;
+  return p;
+}
+
+int launch_attention(LisaRunner* r, Ctx& c, int m, const uint16_t* qn, const uint16_t* kn, uint16_t* kc,
+                     uint16_t* vc) {
+  LisaAttnParams a{};
+  a.q_proj = c.q_proj;
+  a.k_raw = c.k_raw;
+  a.v_raw = c.v_raw;
+  a.q_norm_w = qn;
+  a.k_norm_w = kn;
+  a.key_cache = kc;
+  a.value_cache = vc;
+  a.part_o = c.part_o;
+  a.part_ml = c.part_ml;
+  a.pos = c.pos;
+  a.gated = c.gated;
+  a.capacity = (uint32_t)r->cfg.capacity;
+  a.s_max = r->s_max;
+  const int mi = m == 3 ? 1 : 0;
+  LISA_TRY(lisa_launch(r->dev, r->attn_part[mi], &a, sizeof a, r->s_max, LISA_ATT_KVH, 1, 256, 1, 1));
+  return lisa_launch(r->dev, r->attn_merge[mi], &a, sizeof a, LISA_ATT_QH, m, 1, 256, 1, 1);
+}
+
+int launch_mlp(LisaRunner* r, Ctx& c, int m, const uint16_t* post_norm, const Q4Dev& gate, const Q4Dev& up,
+               const Q4Dev& down) {
+  LisaQmvParams p = pro_resnorm(c.H, c.B, post_norm, c.R);
+  LISA_TRY(launch_qmv(r, m, LISA_HIDDEN, p, {{&gate, &up, c.act, LISA_EPI_GATEUP}}));
+  LisaQmvParams d = pro_loadx(c.act);
+  return launch_qmv(r, m, LISA_INTER, d, {{&down, nullptr, c.B, LISA_EPI_STORE}});
+}
+
+int launch_lm_head(LisaRunner* r, Ctx& c, int m, const uint16_t* norm, uint16_t* x_out, uint16_t* h_out) {
+  LisaQmvParams p = pro_resnorm(c.R, c.B, norm, h_out);
+  p.x_out = x_out;
+  p.am_val = c.am_val;
+  p.am_idx = c.am_idx;
+  return launch_qmv(r, m, LISA_HIDDEN, p, {{&r->head, nullptr, c.logits, LISA_EPI_ARGMAX}});
+}
+
+int lm_head_grid(LisaRunner* r) {
+  const uint32_t tiles = ((uint32_t)r->cfg.vocab + 7) / 8;
+  const bool split = (uint32_t)r->cfg.vocab <= 8192;
+  uint32_t grid = split ? tiles : (tiles + 3) / 4;
+  return (int)std::max<uint32_t>(1, std::min(std::min(grid, r->qmv_grid_cap), 4096u));
+}
+
+int launch_finalize(LisaRunner* r, Ctx& c, int m, bool feedback, uint32_t advance) {
+  LisaFinalizeParams f{};
+  f.am_val = c.am_val;
+  f.am_idx = c.am_idx;
+  f.argmax_out = c.argmax;
+  f.next_token = feedback ? c.tokens : nullptr;
+  f.history = feedback ? c.history : nullptr;
+  f.step = feedback ? c.step : nullptr;
+  f.pos = c.pos;
+  f.n_part = (uint32_t)lm_head_grid(r);
+  f.m_rows = (uint32_t)m;
+  f.pos_advance = advance;
+  f.history_cap = kHistoryCap;
+  return lisa_launch(r->dev, r->finalize, &f, sizeof f, 1, 1, 1, 256, 1, 1);
+}
+
+// One target forward of m rows (runner.rs:555-591 for m=1, 866-909 for m=3).
+int encode_target(LisaRunner* r, int m, bool capture, bool feedback) {
+  Ctx& c = r->tgt;
+  const float inv = 1.0f / lisa_sqrt((float)LISA_GDN_HD);  // runner.rs:1316-1317
+  for (int i = 0; i < r->cfg.layers; ++i) {
+    const LayerDev& l = r->layers[i];
+    LisaQmvParams p{};
+    if (i == 0) {
+      p.pro_mode = LISA_PRO_EMBED;
+      p.tokens = c.tokens;
+      p.emb_w = r->embed.w;
+      p.emb_sb = r->embed.sb;
+      p.norm_w = l.input_norm;
+      p.r_out = c.H;
+    } else {
+      p = pro_resnorm(c.R, c.B, l.input_norm, c.H);
+    }
+    if (!l.attention) {
+      const int si = l.state_index;
+      p.conv_w = l.conv_w;
+      p.conv_state = r->conv_state + (size_t)si * 3 * LISA_GDN_CONV_DIM;
+      p.conv_slots = capture ? r->conv_slots + (size_t)si * 3 * LISA_GDN_CONV_DIM : nullptr;
+      p.conv_slot_stride = (uint64_t)r->gdn_layers * 3 * LISA_GDN_CONV_DIM;
+      p.capture = capture ? 1 : 0;
+      LISA_TRY(launch_qmv(r, m, LISA_HIDDEN, p,
+                          {{&l.qkv, nullptr, c.conv_out, LISA_EPI_CONV},
+                           {&l.z, nullptr, c.z, LISA_EPI_STORE},
+                           {&l.a, nullptr, c.a, LISA_EPI_STORE},
+                           {&l.b, nullptr, c.b, LISA_EPI_STORE}}));
+      LisaGdnParams g{};
+      g.conv_out = c.conv_out;
+      g.z = c.z;
+      g.a = c.a;
+      g.b = c.b;
+      g.a_log = l.a_log;
+      g.dt_bias = l.dt_bias;
+      g.norm_w = l.gnorm;
+      g.state = r->gdn_state + (size_t)si * LISA_GDN_STATE;
+      g.slots = capture ? r->gdn_slots + (size_t)si * LISA_GDN_STATE : nullptr;
+      g.slot_stride = (uint64_t)r->gdn_layers * LISA_GDN_STATE;
+      g.gated = c.gated;
+      g.q_scale = inv * inv;
+      g.k_scale = inv;
+      g.capture = capture ? 1 : 0;
+      LISA_TRY(lisa_launch(r->dev, r->gdn[m == 3 ? 1 : 0], &g, sizeof g, LISA_GDN_VH, 1, 1, 512, 1, 1));
+      LisaQmvParams o = pro_loadx(c.gated);
+      LISA_TRY(launch_qmv(r, m, LISA_GDN_VALUE_DIM, o, {{&l.out, nullptr, c.B, LISA_EPI_STORE}}));
+    } else {
+      LISA_TRY(launch_qmv(r, m, LISA_HIDDEN, p,
+                          {{&l.q, nullptr, c.q_proj, LISA_EPI_STORE},
+                           {&l.k, nullptr, c.k_raw, LISA_EPI_STORE},
+                           {&l.v, nullptr, c.v_raw, LISA_EPI_STORE}}));
+      const size_t off = (size_t)l.cache_index * LISA_ATT_KVH * r->cfg.capacity * LISA_ATT_HD;
+      LISA_TRY(launch_attention(r, c, m, l.q_norm, l.k_norm, r->key_cache + off, r->value_cache + off));
+      LisaQmvParams o = pro_loadx(c.gated);
+      LISA_TRY(launch_qmv(r, m, LISA_ATT_OUT, o, {{&l.o, nullptr, c.B, LISA_EPI_STORE}}));
+    }
+    LISA_TRY(launch_mlp(r, c, m, l.post_norm, l.gate, l.up, l.down));
+  }
+  LISA_TRY(launch_lm_head(r, c, m, r->final_norm, nullptr, c.H));
+  return launch_finalize(r, c, m, feedback, (uint32_t)m);
+}
+
+// MTP drafter step (runner.rs:2711-2765, attention/MLP encoders :3097-3271).
+int encode_mtp(LisaRunner* r, const uint16_t* cond) {
+  Ctx& c = r->drf;
+  const MtpDev& t = r->mtp;
+  LisaQmvParams p{};
+  p.pro_mode = LISA_PRO_MTPFC;
+  p.tokens = c.tokens;
+  p.emb_w = r->embed.w;
+  p.emb_sb = r->embed.sb;
+  p.norm_w = t.pre_fc_emb;
+  p.norm_w2 = t.pre_fc_hid;
+  p.x_in = cond;
+  LISA_TRY(launch_qmv(r, 1, 2 * LISA_HIDDEN, p, {{&t.fc, nullptr, c.B, LISA_EPI_STORE}}));
+  LisaQmvParams q{};
+  q.pro_mode = LISA_PRO_CAST;  // f32_to_bf16 of the fc output (norm.metal:132-137)
+  q.o_in = c.B;
+  q.norm_w = t.input_norm;
+  q.r_out = c.H;
+  LISA_TRY(launch_qmv(r, 1, LISA_HIDDEN, q,
+                      {{&t.q, nullptr, c.q_proj, LISA_EPI_STORE},
+                       {&t.k, nullptr, c.k_raw, LISA_EPI_STORE},
+                       {&t.v, nullptr, c.v_raw, LISA_EPI_STORE}}));
+  LISA_TRY(launch_attention(r, c, 1, t.q_norm, t.k_norm, r->mtp_key, r->mtp_value));
+  LisaQmvParams o = pro_loadx(c.gated);
+  LISA_TRY(launch_qmv(r, 1, LISA_ATT_OUT, o, {{&t.o, nullptr, c.B, LISA_EPI_STORE}}));
+  LISA_TRY(launch_mlp(r, c, 1, t.post_norm, t.gate, t.up, t.down));
+  LISA_TRY(launch_lm_head(r, c, 1, t.final_norm, c.xnorm, nullptr));
+  return launch_finalize(r, c, 1, false, 1);
+}
+
+int write_pos(LisaRunner* r, Ctx& c, uint32_t pos) {
+  return lisa_hip_check(hipMemcpyAsync(c.pos, &pos, 4, hipMemcpyHostToDevice, r->dev->stream), "H2D pos");
+}
+
+int read_hidden(LisaRunner* r, const uint16_t* src, int rows, float* out) {
+  std::vector<uint16_t> h((size_t)rows * LISA_HIDDEN);
+  LISA_TRY(lisa_hip_check(
+      hipMemcpyAsync(h.data(), src, h.size() * 2, hipMemcpyDeviceToHost, r->dev->stream), "D2H hidden"));
+  LISA_TRY(sync(r));
+  for (size_t i = 0; i < h.size(); ++i) out[i] = lisa_bf16_to_f32(h[i]);
+  return LISA_OK;
+}
+
+int check_token(const LisaRunner* r, uint32_t token) {
+  if (token >= (uint32_t)r->cfg.vocab) return lisa_fail(LISA_E_VOCAB, "token %u is outside vocabulary", token);
+  return LISA_OK;
+}
+
+int do_decode(LisaRunner* r, uint32_t token, uint32_t* argmax, float* hidden, float* logits) {
+  LISA_TRY(check_token(r, token));
+  if (r->position >= (uint32_t)r->cfg.capacity)
+    return lisa_fail(LISA_E_CAPACITY, "KV capacity %d exhausted", r->cfg.capacity);
+  Ctx& c = r->tgt;
+  LISA_TRY(upload_u32(r, c.tokens, &token, 1));
+  if (r->cfg.use_graph) {
+    if (!r->step_graph) {
+      LISA_TRY(lisa_capture_begin(r->dev));
+      const int rc = encode_target(r, 1, false, true);
+      LisaGraph* g = nullptr;
+      const int re = lisa_capture_end(r->dev, &g);
+      if (rc) {
+        if (g) lisa_graph_free(g);
+        return rc;
+      }
+      LISA_TRY(re);
+      r->step_graph = g;
+    }
+    LISA_TRY(lisa_graph_launch(r->step_graph, r->dev));
+  } else {
+    LISA_TRY(encode_target(r, 1, false, true));
+  }
+  uint32_t am = 0;
+  LISA_TRY(lisa_hip_check(hipMemcpyAsync(&am, c.argmax, 4, hipMemcpyDeviceToHost, r->dev->stream), "D2H argmax"));
+  LISA_TRY(sync(r));
+  if (argmax) *argmax = am;
+  if (hidden) LISA_TRY(read_hidden(r, c.H, 1, hidden));
+  if (logits)
+    LISA_TRY(lisa_hip_check(hipMemcpy(logits, c.logits, (size_t)r->cfg.vocab * 4, hipMemcpyDeviceToHost), "D2H logits"));
+  r->position += 1;
+  r->verify_base = -1;
+  return LISA_OK;
+}
+
+}  // namespace
+
+// =============================================================================
+// C ABI
+// =============================================================================
+extern "C" int lisa_runner_create(const LisaRunnerConfig* cfg, LisaRunner** out) {
+  if (!cfg || !out) return lisa_fail(LISA_E_ARG, "lisa_runner_create: null argument");
+  if (cfg->layers <= 0 || cfg->layers % 4 != 0)
+    return lisa_fail(LISA_E_ARG, "layers must be a positive multiple of 4 (got %d)", cfg->layers);
+  if (cfg->vocab <= 0 || cfg->vocab % 8 != 0) return lisa_fail(LISA_E_ARG, "vocab must be a positive multiple of 8");
+  if (cfg->capacity <= 0) return lisa_fail(LISA_E_ARG, "KV capacity must be greater than zero");
+  if (cfg->capacity > 64 * 1024) return lisa_fail(LISA_E_ARG, "KV capacity above 65536 is not supported");
+  std::unique_ptr<LisaRunner> r(new LisaRunner());
+  r->cfg = *cfg;
+  if (const char* g = std::getenv("LISA_QMV_GRID")) r->qmv_grid_cap = (uint32_t)std::max(1, std::atoi(g));
+  LISA_TRY(lisa_device_create(cfg->device, &r->dev));
+  LISA_TRY(lisa_module_load_default(r->dev, &r->mod));
+  static const char* knames[5] = {"5120", "6144", "10240", "17408", "1024"};
+  for (int mi = 0; mi < 2; ++mi)
+    for (int ki = 0; ki < 5; ++ki) {
+      const std::string name = std::string("lisa_qmv_k") + knames[ki] + (mi ? "_m3" : "_m1");
+      LisaFunction* f = nullptr;
+      if (lisa_function_get(r->mod, name.c_str(), &f) == LISA_OK) r->qmv[mi][ki] = f;
+    }
+  for (int mi = 0; mi < 2; ++mi) {
+    const char* sfx = mi ? "_m3" : "_m1";
+    LISA_TRY(lisa_function_get(r->mod, (std::string("lisa_gdn_recurrence") + sfx).c_str(), &r->gdn[mi]));
+    LISA_TRY(lisa_function_get(r->mod, (std::string("lisa_attn_partial") + sfx).c_str(), &r->attn_part[mi]));
+    LISA_TRY(lisa_function_get(r->mod, (std::string("lisa_attn_merge") + sfx).c_str(), &r->attn_merge[mi]));
+  }
+  LISA_TRY(lisa_function_get(r->mod, "lisa_step_finalize", &r->finalize));
+  LISA_TRY(lisa_function_get(r->mod, "lisa_synth_fill", &r->synth));
+  r->s_max = ((uint32_t)cfg->capacity + LISA_ATT_SLICE - 1) / LISA_ATT_SLICE;
+
+  Arena wa;
+  plan_weights(r.get(), wa);
+  LISA_TRY(lisa_buffer_alloc(r->dev, wa.used, &r->weights));
+  wa.base = (char*)r->weights->ptr;
+  wa.used = 0;
+  plan_weights(r.get(), wa);
+
+  Arena sa;
+  plan_state(r.get(), sa);
+  LISA_TRY(lisa_buffer_alloc(r->dev, sa.used, &r->state));
+  sa.base = (char*)r->state->ptr;
+  sa.used = 0;
+  plan_state(r.get(), sa);
+
+  Arena xa;
+  plan_ctx(r.get(), xa, r->tgt, 3);
+  plan_ctx(r.get(), xa, r->drf, 1);
+  LISA_TRY(lisa_buffer_alloc(r->dev, xa.used, &r->scratch));
+  xa.base = (char*)r->scratch->ptr;
+  xa.used = 0;
+  plan_ctx(r.get(), xa, r->tgt, 3);
+  plan_ctx(r.get(), xa, r->drf, 1);
+
+  LISA_TRY(generate_weights(r.get()));
+  LISA_TRY(lisa_runner_reset_state(r.get()));
+  *out = r.release();
+  return LISA_OK;
+}
+
+extern "C" void lisa_runner_free(LisaRunner* r) {
+  if (!r) return;
+  if (r->dev) (void)hipStreamSynchronize(r->dev->stream);
+  lisa_graph_free(r->step_graph);
+  lisa_buffer_free(r->scratch);
+  lisa_buffer_free(r->state);
+  lisa_buffer_free(r->weights);
+  lisa_module_free(r->mod);
+  lisa_device_free(r->dev);
+  delete r;
+}
+
+extern "C" LisaDevice* lisa_runner_device(LisaRunner* r) { return r ? r->dev : nullptr; }
+extern "C" uint32_t lisa_runner_position(LisaRunner* r) { return r ? r->position : 0; }
+extern "C" uint64_t lisa_runner_weight_bytes(LisaRunner* r) { return r && r->weights ? r->weights->len : 0; }
+
+extern "C" int lisa_runner_reset_state(LisaRunner* r) {
+  if (!r) return lisa_fail(LISA_E_ARG, "null runner");
+  LISA_TRY(lisa_hip_check(hipMemsetAsync(r->state->ptr, 0, r->state->len, r->dev->stream), "memset state"));
+  LISA_TRY(write_pos(r, r->tgt, 0));
+  LISA_TRY(write_pos(r, r->drf, 0));
+  LISA_TRY(sync(r));
+  r->position = 0;
+  r->mtp_position = 0;
+  r->verify_base = -1;
+  return LISA_OK;
+}
+
+extern "C" int lisa_runner_fill_state(LisaRunner* r, uint32_t filled, uint64_t seed) {
+  if (!r) return lisa_fail(LISA_E_ARG, "null runner");
+  if (filled > (uint32_t)r->cfg.capacity) return lisa_fail(LISA_E_CAPACITY, "fill beyond KV capacity");
+  LISA_TRY(lisa_runner_reset_state(r));
+  const uint32_t cap = (uint32_t)r->cfg.capacity;
+  for (int i = 0; i < r->cfg.layers; ++i) {
+    const LayerDev& l = r->layers[i];
+    const int sc = i + 1;
+    if (!l.attention) {
+      LISA_TRY(fill(r, r->gdn_state + (size_t)l.state_index * LISA_GDN_STATE, LISA_GDN_STATE, LISA_FILL_F32,
+                    lisa_stream_key(seed, lisa_tensor_id(sc, LISA_T_GDN_STATE, 0)), 0, LISA_DIST_NORMAL, 0.0f, 0.01f));
+      LISA_TRY(fill(r, r->conv_state + (size_t)l.state_index * 3 * LISA_GDN_CONV_DIM, 3 * LISA_GDN_CONV_DIM,
+                    LISA_FILL_BF16, lisa_stream_key(seed, lisa_tensor_id(sc, LISA_T_CONV_STATE, 0)), 0,
+                    LISA_DIST_NORMAL, 0.0f, 1.0f));
+    } else if (filled) {
+      const size_t off = (size_t)l.cache_index * LISA_ATT_KVH * cap * LISA_ATT_HD;
+      const uint64_t n = (uint64_t)LISA_ATT_KVH * filled * LISA_ATT_HD;
+      LISA_TRY(fill(r, r->key_cache + off, n, LISA_FILL_KV, lisa_stream_key(seed, lisa_tensor_id(sc, LISA_T_KEY_CACHE, 0)),
+                    0, 0, 0, 0, cap, filled));
+      LISA_TRY(fill(r, r->value_cache + off, n, LISA_FILL_KV,
+                    lisa_stream_key(seed, lisa_tensor_id(sc, LISA_T_VALUE_CACHE, 0)), 0, 0, 0, 0, cap, filled));
+    }
+  }
+  if (r->cfg.with_mtp && filled) {
+    const uint64_t n = (uint64_t)LISA_ATT_KVH * filled * LISA_ATT_HD;
+    LISA_TRY(fill(r, r->mtp_key, n, LISA_FILL_KV, lisa_stream_key(seed, lisa_tensor_id(LISA_SCOPE_MTP, LISA_T_KEY_CACHE, 0)),
+                  0, 0, 0, 0, cap, filled));
+    LISA_TRY(fill(r, r->mtp_value, n, LISA_FILL_KV,
+                  lisa_stream_key(seed, lisa_tensor_id(LISA_SCOPE_MTP, LISA_T_VALUE_CACHE, 0)), 0, 0, 0, 0, cap, filled));
+  }
+  LISA_TRY(write_pos(r, r->tgt, filled));
+  LISA_TRY(write_pos(r, r->drf, r->cfg.with_mtp ? filled : 0));
+  LISA_TRY(sync(r));
+  r->position = filled;
+  r->mtp_position = r->cfg.with_mtp ? filled : 0;
+  return LISA_OK;
+}
+
+extern "C" int lisa_runner_forward_token_decode(LisaRunner* r, uint32_t token, uint32_t* argmax, float* hidden) {
+  if (!r) return lisa_fail(LISA_E_ARG, "null runner");
+  return do_decode(r, token, argmax, hidden, nullptr);
+}
+
+extern "C" int lisa_runner_forward_token_with_hidden(LisaRunner* r, uint32_t token, uint32_t* argmax, float* hidden,
+                                                     float* logits) {
+  if (!r) return lisa_fail(LISA_E_ARG, "null runner");
+  return do_decode(r, token, argmax, hidden, logits);
+}
+
+extern "C" int lisa_runner_decode_greedy(LisaRunner* r, uint32_t token, int32_t steps, uint32_t* tokens_out) {
+  if (!r || steps < 0 || (steps && !tokens_out)) return lisa_fail(LISA_E_ARG, "lisa_runner_decode_greedy: bad argument");
+  if (!steps) return LISA_OK;
+  LISA_TRY(check_token(r, token));
+  if (r->position + (uint32_t)steps > (uint32_t)r->cfg.capacity)
+    return lisa_fail(LISA_E_CAPACITY, "KV capacity %d exhausted by %d steps", r->cfg.capacity, steps);
+  if ((uint32_t)steps > kHistoryCap) return lisa_fail(LISA_E_ARG, "at most %u steps per call", kHistoryCap);
+  // first step through the host path (captures the graph), the rest replay it
+  uint32_t first = 0;
+  const uint32_t zero = 0;
+  Ctx& c = r->tgt;
+  LISA_TRY(upload_u32(r, c.step, &zero, 1));
+  LISA_TRY(do_decode(r, token, &first, nullptr, nullptr));
+  for (int s = 1; s < steps; ++s) {
+    if (r->step_graph) {
+      LISA_TRY(lisa_graph_launch(r->step_graph, r->dev));
+    } else {
+      LISA_TRY(encode_target(r, 1, false, true));
+    }
+  }
+  LISA_TRY(lisa_hip_check(hipMemcpyAsync(tokens_out, c.history, (size_t)steps * 4, hipMemcpyDeviceToHost, r->dev->stream),
+                          "D2H history"));
+  LISA_TRY(sync(r));
+  r->position += (uint32_t)steps - 1;
+  return LISA_OK;
+}
+
+extern "C" int lisa_runner_verify_block3(LisaRunner* r, const uint32_t tokens[3], uint32_t argmax[3], float* hidden,
+                                         float* logits) {
+  if (!r || !tokens) return lisa_fail(LISA_E_ARG, "lisa_runner_verify_block3: bad argument");
+  for (int i = 0; i < 3; ++i) LISA_TRY(check_token(r, tokens[i]));
+  if (r->position + 3 > (uint32_t)r->cfg.capacity)
+    return lisa_fail(LISA_E_CAPACITY, "KV capacity %d exhausted", r->cfg.capacity);
+  Ctx& c = r->tgt;
+  LISA_TRY(upload_u32(r, c.tokens, tokens, 3));
+  LISA_TRY(encode_target(r, 3, true, false));
+  uint32_t am[3];
+  LISA_TRY(lisa_hip_check(hipMemcpyAsync(am, c.argmax, 12, hipMemcpyDeviceToHost, r->dev->stream), "D2H argmax"));
+  LISA_TRY(sync(r));
+  if (argmax) std::memcpy(argmax, am, 12);
+  if (hidden) LISA_TRY(read_hidden(r, c.H, 3, hidden));
+  if (logits)
+    LISA_TRY(lisa_hip_check(hipMemcpy(logits, c.logits, (size_t)3 * r->cfg.vocab * 4, hipMemcpyDeviceToHost),
+                            "D2H logits"));
+  r->verify_base = r->position;
+  r->position += 3;
+  return LISA_OK;
+}
+
+extern "C" int lisa_runner_commit_verified_prefix(LisaRunner* r, int32_t rows) {
+  if (!r) return lisa_fail(LISA_E_ARG, "null runner");
+  if (r->verify_base < 0) return lisa_fail(LISA_E_STATE, "no pending block-3 verification");
+  if (rows < 1 || rows > 3) {
+    r->verify_base = -1;
+    return lisa_fail(LISA_E_ARG, "verified prefix must contain 1 to 3 rows");
+  }
+  const uint32_t base = (uint32_t)r->verify_base;
+  r->verify_base = -1;
+  if (rows < 3) {
+    const size_t gs = (size_t)r->gdn_layers * LISA_GDN_STATE;
+    const size_t cs = (size_t)r->gdn_layers * 3 * LISA_GDN_CONV_DIM;
+    LISA_TRY(lisa_hip_check(hipMemcpyAsync(r->gdn_state, r->gdn_slots + (size_t)(rows - 1) * gs, gs * 4,
+                                           hipMemcpyDeviceToDevice, r->dev->stream),
+                            "D2D gdn slot"));
+    LISA_TRY(lisa_hip_check(hipMemcpyAsync(r->conv_state, r->conv_slots + (size_t)(rows - 1) * cs, cs * 2,
+                                           hipMemcpyDeviceToDevice, r->dev->stream),
+                            "D2D conv slot"));
+  }
+  r->position = base + (uint32_t)rows;
+  LISA_TRY(write_pos(r, r->tgt, r->position));
+  return sync(r);
+}
+
+extern "C" int lisa_runner_checkpoint_state(LisaRunner* r, LisaCheckpoint** out) {
+  if (!r || !out) return lisa_fail(LISA_E_ARG, "lisa_runner_checkpoint_state: bad argument");
+  std::unique_ptr<LisaCheckpoint> ck(new LisaCheckpoint());
+  const size_t gs = (size_t)r->gdn_layers * LISA_GDN_STATE * 4, cs = (size_t)r->gdn_layers * 3 * LISA_GDN_CONV_DIM * 2;
+  LISA_TRY(lisa_buffer_alloc(r->dev, gs, &ck->gdn));
+  LISA_TRY(lisa_buffer_alloc(r->dev, cs, &ck->conv));
+  LISA_TRY(lisa_hip_check(hipMemcpyAsync(ck->gdn->ptr, r->gdn_state, gs, hipMemcpyDeviceToDevice, r->dev->stream), "D2D"));
+  LISA_TRY(lisa_hip_check(hipMemcpyAsync(ck->conv->ptr, r->conv_state, cs, hipMemcpyDeviceToDevice, r->dev->stream), "D2D"));
+  LISA_TRY(sync(r));
+  ck->position = r->position;
+  *out = ck.release();
+  return LISA_OK;
+}
+
+extern "C" int lisa_runner_restore_state(LisaRunner* r, const LisaCheckpoint* ck) {
+  if (!r || !ck) return lisa_fail(LISA_E_ARG, "lisa_runner_restore_state: bad argument");
+  if (ck->position > (uint32_t)r->cfg.capacity)
+    return lisa_fail(LISA_E_CAPACITY, "checkpoint position %u exceeds KV capacity %d", ck->position, r->cfg.capacity);
+  LISA_TRY(lisa_hip_check(hipMemcpyAsync(r->gdn_state, ck->gdn->ptr, ck->gdn->len, hipMemcpyDeviceToDevice, r->dev->stream), "D2D"));
+  LISA_TRY(lisa_hip_check(hipMemcpyAsync(r->conv_state, ck->conv->ptr, ck->conv->len, hipMemcpyDeviceToDevice, r->dev->stream), "D2D"));
+  r->position = ck->position;
+  r->verify_base = -1;
+  LISA_TRY(write_pos(r, r->tgt, r->position));
+  return sync(r);
+}
+
+extern "C" void lisa_checkpoint_free(LisaCheckpoint* ck) {
+  if (!ck) return;
+  lisa_buffer_free(ck->gdn);
+  lisa_buffer_free(ck->conv);
+  delete ck;
+}
+
+extern "C" int lisa_runner_read_gdn_state(LisaRunner* r, int32_t idx, float* out) {
+  if (!r || !out || idx < 0 || idx >= r->gdn_layers) return lisa_fail(LISA_E_ARG, "bad GDN layer index");
+  LISA_TRY(lisa_hip_check(hipMemcpy(out, r->gdn_state + (size_t)idx * LISA_GDN_STATE, LISA_GDN_STATE * 4,
+                                    hipMemcpyDeviceToHost), "D2H state"));
+  return LISA_OK;
+}
+
+extern "C" int lisa_runner_read_conv_state(LisaRunner* r, int32_t idx, uint16_t* out) {
+  if (!r || !out || idx < 0 || idx >= r->gdn_layers) return lisa_fail(LISA_E_ARG, "bad GDN layer index");
+  LISA_TRY(lisa_hip_check(hipMemcpy(out, r->conv_state + (size_t)idx * 3 * LISA_GDN_CONV_DIM, 3 * LISA_GDN_CONV_DIM * 2,
+                                    hipMemcpyDeviceToHost), "D2H conv"));
+  return LISA_OK;
+}
+
+// ---- MTP drafter --------------------------------------------------------------
+extern "C" int lisa_mtp_forward(LisaRunner* r, uint32_t token, int32_t cond_source, int32_t cond_row,
+                                uint32_t* argmax) {
+  if (!r) return lisa_fail(LISA_E_ARG, "null runner");
+  if (!r->cfg.with_mtp) return lisa_fail(LISA_E_STATE, "runner was created without the MTP drafter");
+  LISA_TRY(check_token(r, token));
+  if (r->mtp_position >= (uint32_t)r->cfg.capacity)
+    return lisa_fail(LISA_E_CAPACITY, "MTP KV capacity %d exhausted", r->cfg.capacity);
+  const uint16_t* cond;
+  switch (cond_source) {
+    case 0:
+      if (cond_row < 0 || cond_row > 2) return lisa_fail(LISA_E_ARG, "cond_row must be 0..2");
+      cond = r->tgt.H + (size_t)cond_row * LISA_HIDDEN;
+      break;
+    case 1: cond = r->drf.xnorm; break;
+    case 2: cond = r->drf.cond; break;
+    default: return lisa_fail(LISA_E_ARG, "bad cond_source %d", cond_source);
+  }
+  Ctx& c = r->drf;
+  LISA_TRY(upload_u32(r, c.tokens, &token, 1));
+  LISA_TRY(encode_mtp(r, cond));
+  uint32_t am = 0;
+  LISA_TRY(lisa_hip_check(hipMemcpyAsync(&am, c.argmax, 4, hipMemcpyDeviceToHost, r->dev->stream), "D2H argmax"));
+  LISA_TRY(sync(r));
+  if (argmax) *argmax = am;
+  r->mtp_position += 1;
+  return LISA_OK;
+}
+
+namespace {
+int upload_bf16_trunc(LisaRunner* r, uint16_t* dst, const float* hidden) {
+  std::vector<uint16_t> h(LISA_HIDDEN);
+  for (int i = 0; i < LISA_HIDDEN; ++i) h[i] = lisa_f32_to_bf16_trunc(hidden[i]);
+  LISA_TRY(lisa_hip_check(hipMemcpyAsync(dst, h.data(), LISA_HIDDEN * 2, hipMemcpyHostToDevice, r->dev->stream), "H2D"));
+  return sync(r);
+}
+}  // namespace
+
+extern "C" int lisa_runner_upload_hidden(LisaRunner* r, int32_t row, const float* hidden) {
+  if (!r || !hidden || row < 0 || row > 2) return lisa_fail(LISA_E_ARG, "lisa_runner_upload_hidden: bad argument");
+  return upload_bf16_trunc(r, r->tgt.H + (size_t)row * LISA_HIDDEN, hidden);
+}
+
+extern "C" int32_t lisa_runner_vocab(LisaRunner* r) { return r ? r->cfg.vocab : 0; }
+
+extern "C" int lisa_mtp_upload_normalized(LisaRunner* r, const float* hidden) {
+  if (!r || !hidden) return lisa_fail(LISA_E_ARG, "lisa_mtp_upload_normalized: bad argument");
+  return upload_bf16_trunc(r, r->drf.xnorm, hidden);
+}
+
+extern "C" int lisa_mtp_upload_cond(LisaRunner* r, const uint16_t* hidden) {
+  if (!r || !hidden) return lisa_fail(LISA_E_ARG, "lisa_mtp_upload_cond: bad argument");
+  LISA_TRY(lisa_hip_check(hipMemcpyAsync(r->drf.cond, hidden, LISA_HIDDEN * 2, hipMemcpyHostToDevice, r->dev->stream), "H2D"));
+  return sync(r);
+}
+
+extern "C" int lisa_mtp_read_normalized(LisaRunner* r, uint16_t* out) {
+  if (!r || !out) return lisa_fail(LISA_E_ARG, "lisa_mtp_read_normalized: bad argument");
+  LISA_TRY(lisa_hip_check(hipMemcpyAsync(out, r->drf.xnorm, LISA_HIDDEN * 2, hipMemcpyDeviceToHost, r->dev->stream), "D2H"));
+  return sync(r);
+}
+
+extern "C" uint32_t lisa_mtp_position(LisaRunner* r) { return r ? r->mtp_position : 0; }
+
+extern "C" int lisa_mtp_trim_state(LisaRunner* r, int32_t count) {
+  if (!r) return lisa_fail(LISA_E_ARG, "null runner");
+  if (count < 0 || (uint32_t)count > r->mtp_position)
+    return lisa_fail(LISA_E_ARG, "cannot trim %d MTP positions from %u", count, r->mtp_position);
+  r->mtp_position -= (uint32_t)count;
+  LISA_TRY(write_pos(r, r->drf, r->mtp_position));
+  return sync(r);
+}

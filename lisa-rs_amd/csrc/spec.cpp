@@ -1,0 +1,129 @@
+// spec.cpp — greedy block-3 speculative decoding over the runner
+// (src/speculative/mod.rs): accept_greedy, mtp_reconcile_plan and the
+// device-resident-hidden loop run_block3_loop.
+#include <cstring>
+#include <vector>
+
+#include "bridge.h"
+#include "lisa_hip.h"
+#include "lisa_synth.h"
+
+// speculative/mod.rs:16-32
+extern "C" int lisa_accept_greedy(const uint32_t* drafts, int32_t n, const uint32_t* target, LisaAcceptance* out) {
+  if (!drafts || !target || !out || n < 0 || n > 2) return lisa_fail(LISA_E_ARG, "lisa_accept_greedy: bad argument");
+  int accepted = 0;
+  while (accepted < n && drafts[accepted] == target[accepted]) ++accepted;
+  out->accepted_drafts = accepted;
+  out->emitted_count = accepted + 1;
+  for (int i = 0; i < accepted; ++i) out->emitted[i] = drafts[i];
+  out->emitted[accepted] = target[accepted];
+  out->target_trim = (n + 1) - out->emitted_count;
+  return LISA_OK;
+}
+
+// speculative/mod.rs:49-65
+extern "C" int lisa_mtp_reconcile_plan(int32_t draft_count, int32_t round_appended, int32_t accepted,
+                                       LisaReconcilePlan* out) {
+  if (!out || accepted < 0 || accepted > draft_count || round_appended < 0 || round_appended > draft_count ||
+      draft_count > 2)
+    return lisa_fail(LISA_E_ARG, "lisa_mtp_reconcile_plan: bad argument");
+  const int keep = accepted < round_appended ? accepted : round_appended;
+  out->replay_count = 0;
+  for (int i = keep; i < accepted; ++i) out->replay[out->replay_count++] = i;
+  out->replay[out->replay_count++] = -1;
+  out->trim = round_appended - keep;
+  return LISA_OK;
+}
+
+// run_block3_loop (speculative/mod.rs:102-198) after
+// generate_greedy_block3_prefilled (:384-413).
+extern "C" int lisa_generate_greedy_block3(LisaRunner* r, uint32_t bonus, const float* target_hidden,
+                                           uint32_t mtp_seed_token, const float* mtp_seed_hidden,
+                                           int32_t max_tokens, const uint32_t* force_truth, int32_t force_len,
+                                           uint64_t force_seed, float p_accept, uint32_t* tokens_out,
+                                           LisaSpecStats* stats) {
+  if (!r || !target_hidden || !mtp_seed_hidden || max_tokens < 0 || (max_tokens && !tokens_out))
+    return lisa_fail(LISA_E_ARG, "lisa_generate_greedy_block3: bad argument");
+  LisaSpecStats st{};
+  std::vector<uint32_t> out;
+  if (max_tokens == 0) {
+    if (stats) *stats = st;
+    return LISA_OK;
+  }
+  out.push_back(bonus);
+  // target.upload_hidden_device(0, ...) and mtp.upload_normalized_device(seed)
+  // (speculative/mod.rs:117-122)
+  LISA_TRY(lisa_runner_upload_hidden(r, 0, target_hidden));
+  LISA_TRY(lisa_mtp_upload_normalized(r, mtp_seed_hidden));
+  bool have_seed = true;
+  uint32_t seed_token = mtp_seed_token;
+  const uint64_t force_key = lisa_stream_key(force_seed, 0x5eedull);
+  uint64_t force_ctr = 0;
+  const uint32_t vocab = (uint32_t)lisa_runner_vocab(r);
+  while ((int32_t)out.size() < max_tokens) {
+    const int remaining = max_tokens - (int32_t)out.size();
+    if (remaining < 3) {
+      for (int i = 0; i < remaining; ++i) {
+        uint32_t next = 0;
+        LISA_TRY(lisa_runner_forward_token_decode(r, bonus, &next, nullptr));
+        st.target_forwards += 1;
+        bonus = next;
+        out.push_back(next);
+      }
+      break;
+    }
+    uint32_t drafts[2];
+    int round_appended;
+    if (have_seed) {
+      uint32_t d1 = 0;
+      LISA_TRY(lisa_mtp_forward(r, seed_token, 1, 0, &d1));
+      drafts[0] = seed_token;
+      drafts[1] = d1;
+      round_appended = 1;
+      have_seed = false;
+    } else {
+      uint32_t d0 = 0, d1 = 0;
+      LISA_TRY(lisa_mtp_forward(r, bonus, 0, 0, &d0));
+      LISA_TRY(lisa_mtp_forward(r, d0, 1, 0, &d1));
+      drafts[0] = d0;
+      drafts[1] = d1;
+      round_appended = 2;
+    }
+    if (force_truth) {
+      for (int j = 0; j < 2; ++j) {
+        const size_t idx = out.size() + (size_t)j;
+        if ((int64_t)idx < force_len) {
+          const float u = lisa_rand_unit(lisa_rand64(force_key, force_ctr++));
+          const uint32_t truth = force_truth[idx];
+          drafts[j] = (u < p_accept) ? truth : (truth + 1u) % vocab;
+        }
+      }
+    }
+    const uint32_t verify_tokens[3] = {bonus, drafts[0], drafts[1]};
+    uint32_t target[3];
+    LISA_TRY(lisa_runner_verify_block3(r, verify_tokens, target, nullptr, nullptr));
+    st.target_forwards += 1;
+    LisaAcceptance acc;
+    LISA_TRY(lisa_accept_greedy(drafts, 2, target, &acc));
+    LISA_TRY(lisa_runner_commit_verified_prefix(r, acc.accepted_drafts + 1));
+    LisaReconcilePlan plan;
+    LISA_TRY(lisa_mtp_reconcile_plan(2, round_appended, acc.accepted_drafts, &plan));
+    LISA_TRY(lisa_mtp_trim_state(r, plan.trim));
+    // only the last replay entry is forwarded (speculative/mod.rs:169-183)
+    const int last = plan.replay[plan.replay_count - 1];
+    const uint32_t token = last >= 0 ? drafts[last] : acc.emitted[acc.emitted_count - 1];
+    const int cond_row = last >= 0 ? last : acc.accepted_drafts;
+    uint32_t next_seed = 0;
+    LISA_TRY(lisa_mtp_forward(r, token, 0, cond_row, &next_seed));
+    seed_token = next_seed;
+    have_seed = true;
+    bonus = acc.emitted[acc.emitted_count - 1];
+    for (int i = 0; i < acc.emitted_count; ++i) out.push_back(acc.emitted[i]);
+    st.rounds += 1;
+    st.accepted_drafts += acc.accepted_drafts;
+    st.drafted_tokens += 2;
+  }
+  std::memcpy(tokens_out, out.data(), sizeof(uint32_t) * (size_t)max_tokens);
+  if (stats) *stats = st;
+  return LISA_OK;
+}

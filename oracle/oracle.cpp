@@ -1,0 +1,923 @@
+// oracle.cpp — CPU oracle of the lisa-rs decode path. TEST INFRASTRUCTURE:
+// loaded only by tests/, __graft_entry__.smoke() and bench.py's cpu_baseline.
+//
+// Every function restates the reference's Metal arithmetic (file:line cited)
+// with the evaluation order fixed: which products are fused (fma), the order
+// of every sum, and the reduction trees. The HIP kernels evaluate the same
+// expressions in the same order, so agreement is bit-exact; agreement with
+// the reference itself is pinned by the reference's own known-answer tests
+// restated in tests/test_oracle.py (tolerance-based, as Metal uses fast-math).
+//
+// Reduction trees used throughout (names used in comments below):
+//   tree64(v[64])  : xor butterfly over 64 lanes, masks 32,16,8,4,2,1,
+//                    v'[i] = v[i] + v[i^m]; result v[0].
+//   tree16(v[16])  : the same over 16 lanes, masks 8,4,2,1.
+//   rows-of-256    : thread t (0..255) sums its elements t, t+256, ...
+//                    sequentially (s = s + x*x), tree64 per 64-thread wave,
+//                    then (W0 + W1) + (W2 + W3).
+//   tree128        : lane l (0..63) holds v[l]^2 + v[l+64]^2, then tree64.
+#include "oracle.h"
+
+#include <immintrin.h>
+#include <omp.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdlib>
+#include <cstring>
+#include <vector>
+
+#include "../include/lisa_model.h"
+#include "../include/lisa_numerics.h"
+#include "../include/lisa_synth.h"
+
+namespace {
+
+inline float bf(uint16_t h) { return lisa_bf16_to_f32(h); }
+inline uint16_t tobf(float x) { return lisa_f32_to_bf16(x); }
+inline float bfr(float x) { return lisa_bf16r(x); }
+
+float tree_xor(float* v, int n) {
+  for (int m = n / 2; m >= 1; m >>= 1) {
+    float t[64];
+    for (int i = 0; i < n; ++i) t[i] = v[i] + v[i ^ m];
+    std::memcpy(v, t, sizeof(float) * n);
+  }
+  return v[0];
+}
+
+// Sum of squares of `cols` values (multiple of 256) with the rows-of-256 tree.
+float sumsq_rows256(const float* x, int cols) {
+  float lanes[256];
+  for (int t = 0; t < 256; ++t) {
+    float s = 0.0f;
+    for (int j = t; j < cols; j += 256) s = s + x[j] * x[j];
+    lanes[t] = s;
+  }
+  float w[4];
+  for (int q = 0; q < 4; ++q) w[q] = tree_xor(lanes + 64 * q, 64);
+  return (w[0] + w[1]) + (w[2] + w[3]);
+}
+
+// tree128 sum of squares of 128 values.
+float sumsq_tree128(const float* v) {
+  float lanes[64];
+  for (int l = 0; l < 64; ++l) lanes[l] = v[l] * v[l] + v[l + 64] * v[l + 64];
+  return tree_xor(lanes, 64);
+}
+
+// RMSNorm of a row of f32 (bf16-valued) inputs; norm.metal:10-47:
+// inv = rsqrt(sum/cols + eps), y = bf16(x * inv * w).
+void rms_norm_f(const float* x, const uint16_t* w, int cols, uint16_t* out) {
+  const float ss = sumsq_rows256(x, cols);
+  const float inv = lisa_rsqrt(ss / (float)cols + LISA_EPS);
+  for (int j = 0; j < cols; ++j) out[j] = tobf((x[j] * inv) * bf(w[j]));
+}
+
+// ---- q4 linear -------------------------------------------------------------
+// qmv.metal:9-76. Per 64-wide group g of row n:
+//   acc_lo = fma chain over the low nibbles  (x[k_even] * q)
+//   acc_hi = fma chain over the high nibbles (x[k_odd]/16 * (byte & 0xf0)),
+//            which is the reference's own odd-nibble trick (qmv.metal:30-36,49)
+//   G = acc_lo + acc_hi;  P_g = fma(scale, G, bias * X_g), X_g = sum of the
+//   group's 64 x values in ascending order.
+// The 16 lanes of a row-group accumulate P over g = 16i + lane (ascending i),
+// then tree16 (the simd_sum of qmv.metal:71-75 with 16 lanes).
+struct XPrep {
+  std::vector<float> xs;  // x with odd positions divided by 16 (exact)
+  std::vector<float> gsum;
+};
+
+void prep_x(const uint16_t* x, int k, XPrep& p) {
+  p.xs.resize(k);
+  p.gsum.resize(k / 64);
+  for (int i = 0; i < k; ++i) {
+    const float v = bf(x[i]);
+    p.xs[i] = (i & 1) ? v / 16.0f : v;
+  }
+  for (int g = 0; g < k / 64; ++g) {
+    float s = 0.0f;
+    for (int i = 0; i < 64; ++i) s = s + bf(x[64 * g + i]);
+    p.gsum[g] = s;
+  }
+}
+
+inline float group_partial(const float* xs, const uint32_t* w8, float scale, float bias, float xsum) {
+  float acc_lo = 0.0f, acc_hi = 0.0f;
+  for (int j = 0; j < 8; ++j) {
+    const uint32_t word = w8[j];
+    for (int b = 0; b < 4; ++b) {
+      const uint32_t byte = (word >> (8 * b)) & 0xffu;
+      acc_lo = lisa_fma(xs[8 * j + 2 * b], (float)(byte & 0x0fu), acc_lo);
+      acc_hi = lisa_fma(xs[8 * j + 2 * b + 1], (float)(byte & 0xf0u), acc_hi);
+    }
+  }
+  const float g = acc_lo + acc_hi;
+  return lisa_fma(scale, g, bias * xsum);
+}
+
+// ksplit = 1: lane l sums its groups over all iterations, tree16.
+// ksplit = 4: iterations split into four contiguous ranges
+// [ITER*w/4, ITER*(w+1)/4); tree16 per range; (W0 + W1) + (W2 + W3).
+float q4_row(const XPrep& xp, const uint32_t* wrow, const uint16_t* srow, const uint16_t* brow, int k,
+             int ksplit) {
+  const int groups = k / 64, iters = (groups + 15) / 16;
+  float wsum[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  const int nsplit = (ksplit == 4) ? 4 : 1;
+  for (int w = 0; w < nsplit; ++w) {
+    const int i0 = (nsplit == 4) ? (iters * w) / 4 : 0, i1 = (nsplit == 4) ? (iters * (w + 1)) / 4 : iters;
+    float lanes[16];
+    for (int l = 0; l < 16; ++l) {
+      float t = 0.0f;
+      for (int i = i0; i < i1; ++i) {
+        const int g = 16 * i + l;
+        if (g >= groups) continue;
+        t = t + group_partial(&xp.xs[64 * g], wrow + 8 * g, bf(srow[g]), bf(brow[g]), xp.gsum[g]);
+      }
+      lanes[l] = t;
+    }
+    wsum[w] = tree_xor(lanes, 16);
+  }
+  return (nsplit == 4) ? (wsum[0] + wsum[1]) + (wsum[2] + wsum[3]) : wsum[0];
+}
+
+// AVX2 version of q4_row over 8 rows at once; identical operations per lane.
+void q4_rows8(const XPrep& xp, const uint32_t* w, const uint16_t* s, const uint16_t* b, int k,
+              int row0, int ksplit, float* out /*8*/) {
+  const int groups = k / 64, wpr = k / 8, iters = groups / 16;
+  const int nsplit = (ksplit == 4) ? 4 : 1;
+  __m256 wsum[4];
+  for (int sp = 0; sp < nsplit; ++sp) {
+    const int i0 = (nsplit == 4) ? (iters * sp) / 4 : 0, i1 = (nsplit == 4) ? (iters * (sp + 1)) / 4 : iters;
+    __m256 lanes[16];
+    for (int l = 0; l < 16; ++l) {
+      __m256 t = _mm256_setzero_ps();
+      for (int it = i0; it < i1; ++it) {
+        const int g = 16 * it + l;
+        __m256 lo = _mm256_setzero_ps(), hi = _mm256_setzero_ps();
+        alignas(32) float sc[8], bi[8];
+        for (int r = 0; r < 8; ++r) {
+          sc[r] = bf(s[(size_t)(row0 + r) * groups + g]);
+          bi[r] = bf(b[(size_t)(row0 + r) * groups + g]);
+        }
+        const float* xs = &xp.xs[64 * g];
+        for (int j = 0; j < 8; ++j) {
+          alignas(32) uint32_t wd[8];
+          for (int r = 0; r < 8; ++r) wd[r] = w[(size_t)(row0 + r) * wpr + 8 * g + j];
+          const __m256i wv = _mm256_load_si256((const __m256i*)wd);
+          for (int bb = 0; bb < 4; ++bb) {
+            const __m256i byte = _mm256_and_si256(_mm256_srli_epi32(wv, 8 * bb), _mm256_set1_epi32(0xff));
+            const __m256 qlo = _mm256_cvtepi32_ps(_mm256_and_si256(byte, _mm256_set1_epi32(0x0f)));
+            const __m256 qhi = _mm256_cvtepi32_ps(_mm256_and_si256(byte, _mm256_set1_epi32(0xf0)));
+            lo = _mm256_fmadd_ps(_mm256_set1_ps(xs[8 * j + 2 * bb]), qlo, lo);
+            hi = _mm256_fmadd_ps(_mm256_set1_ps(xs[8 * j + 2 * bb + 1]), qhi, hi);
+          }
+        }
+        const __m256 gv = _mm256_add_ps(lo, hi);
+        const __m256 pp = _mm256_fmadd_ps(_mm256_load_ps(sc), gv,
+                                          _mm256_mul_ps(_mm256_load_ps(bi), _mm256_set1_ps(xp.gsum[g])));
+        t = _mm256_add_ps(t, pp);
+      }
+      lanes[l] = t;
+    }
+    for (int m = 8; m >= 1; m >>= 1) {
+      __m256 tmp[16];
+      for (int i = 0; i < 16; ++i) tmp[i] = _mm256_add_ps(lanes[i], lanes[i ^ m]);
+      for (int i = 0; i < 16; ++i) lanes[i] = tmp[i];
+    }
+    wsum[sp] = lanes[0];
+  }
+  const __m256 res = (nsplit == 4) ? _mm256_add_ps(_mm256_add_ps(wsum[0], wsum[1]), _mm256_add_ps(wsum[2], wsum[3]))
+                                   : wsum[0];
+  _mm256_storeu_ps(out, res);
+}
+
+void q4_linear_prepped(const XPrep* xp, int m_rows, const uint32_t* w, const uint16_t* s,
+                       const uint16_t* b, int n, int k, int ksplit, float* out) {
+  const int groups = k / 64, wpr = k / 8;
+  const int n8 = (k % 1024 == 0) ? (n & ~7) : 0;
+#pragma omp parallel for schedule(static)
+  for (int r0 = 0; r0 < n8; r0 += 8) {
+    for (int m = 0; m < m_rows; ++m) {
+      float o[8];
+      q4_rows8(xp[m], w, s, b, k, r0, ksplit, o);
+      for (int r = 0; r < 8; ++r) out[(size_t)m * n + r0 + r] = o[r];
+    }
+  }
+  for (int r = n8; r < n; ++r)
+    for (int m = 0; m < m_rows; ++m)
+      out[(size_t)m * n + r] =
+          q4_row(xp[m], w + (size_t)r * wpr, s + (size_t)r * groups, b + (size_t)r * groups, k, ksplit);
+}
+
+// ---- synthetic tensors -------------------------------------------------------
+struct Q4 {
+  std::vector<uint32_t> w;
+  std::vector<uint16_t> s, b;
+  int n = 0, k = 0;
+};
+
+void synth_words(uint64_t seed, uint64_t id, size_t n, uint32_t* out) {
+  const uint64_t key = lisa_stream_key(seed, id);
+#pragma omp parallel for schedule(static)
+  for (size_t i = 0; i < n; ++i) out[i] = lisa_synth_word(key, i);
+}
+void synth_bf16(uint64_t seed, uint64_t id, int dist, float a, float b, size_t n, uint16_t* out) {
+  const uint64_t key = lisa_stream_key(seed, id);
+#pragma omp parallel for schedule(static)
+  for (size_t i = 0; i < n; ++i) out[i] = tobf(lisa_synth_value(key, i, dist, a, b));
+}
+void synth_f32(uint64_t seed, uint64_t id, int dist, float a, float b, size_t n, float* out) {
+  const uint64_t key = lisa_stream_key(seed, id);
+#pragma omp parallel for schedule(static)
+  for (size_t i = 0; i < n; ++i) out[i] = lisa_synth_value(key, i, dist, a, b);
+}
+
+Q4 make_q4(uint64_t seed, int scope, int kind, int n, int k) {
+  Q4 q;
+  q.n = n;
+  q.k = k;
+  q.w.resize((size_t)n * k / 8);
+  q.s.resize((size_t)n * k / 64);
+  q.b.resize((size_t)n * k / 64);
+  synth_words(seed, lisa_tensor_id(scope, kind, 0), q.w.size(), q.w.data());
+  synth_bf16(seed, lisa_tensor_id(scope, kind, 1), LISA_DIST_UNIFORM, LISA_SCALE_LO, LISA_SCALE_HI,
+             q.s.size(), q.s.data());
+  synth_bf16(seed, lisa_tensor_id(scope, kind, 2), LISA_DIST_UNIFORM, LISA_BIAS_LO, LISA_BIAS_HI,
+             q.b.size(), q.b.data());
+  return q;
+}
+
+std::vector<uint16_t> make_vec(uint64_t seed, int scope, int kind, int n, float lo, float hi) {
+  std::vector<uint16_t> v(n);
+  synth_bf16(seed, lisa_tensor_id(scope, kind, 0), LISA_DIST_UNIFORM, lo, hi, n, v.data());
+  return v;
+}
+
+std::vector<uint16_t> make_norm(uint64_t seed, int scope, int kind, int n) {
+  return make_vec(seed, scope, kind, n, 0.9f, 1.1f);
+}
+
+// The HIP launch splits K across the four waves of a workgroup when the launch
+// has at most 8192 virtual rows; `launch_rows` is the row total of the launch
+// this matrix is part of.
+int ksplit_for(int launch_rows) { return launch_rows <= 8192 ? 4 : 1; }
+
+void q4_apply(const Q4& q, const std::vector<XPrep>& xp, int m_rows, int launch_rows, float* out) {
+  q4_linear_prepped(xp.data(), m_rows, q.w.data(), q.s.data(), q.b.data(), q.n, q.k, ksplit_for(launch_rows),
+                    out);
+}
+
+}  // namespace
+
+// =============================================================================
+// kernel-level C API
+// =============================================================================
+extern "C" {
+
+void orc_q4_linear(const uint16_t* x, const uint32_t* w, const uint16_t* scales,
+                   const uint16_t* biases, int n_rows, int k, int m_rows, int ksplit, float* out) {
+  std::vector<XPrep> xp(m_rows);
+  for (int m = 0; m < m_rows; ++m) prep_x(x + (size_t)m * k, k, xp[m]);
+  q4_linear_prepped(xp.data(), m_rows, w, scales, biases, n_rows, k, ksplit, out);
+}
+
+void orc_rms_norm(const uint16_t* x, const uint16_t* w, int cols, uint16_t* out) {
+  std::vector<float> xf(cols);
+  for (int j = 0; j < cols; ++j) xf[j] = bf(x[j]);
+  rms_norm_f(xf.data(), w, cols, out);
+}
+
+void orc_residual(const uint16_t* x, const float* o, int n, uint16_t* y) {
+  for (int i = 0; i < n; ++i) y[i] = tobf(bf(x[i]) + bfr(o[i]));
+}
+
+// embed.metal:6-28: value = float(q)*scale + bias, stored bf16.
+void orc_embed(const uint32_t* w, const uint16_t* scales, const uint16_t* biases, uint32_t token,
+               int hidden, uint16_t* out) {
+  const size_t wpr = hidden / 8, gpr = hidden / 64;
+  for (int c = 0; c < hidden; ++c) {
+    const uint32_t word = w[(size_t)token * wpr + c / 8];
+    const uint32_t q = (word >> ((c & 7) * 4)) & 0xfu;
+    const float v = (float)q * bf(scales[(size_t)token * gpr + c / 64]) + bf(biases[(size_t)token * gpr + c / 64]);
+    out[c] = tobf(v);
+  }
+}
+
+// mlp.metal:6-17
+void orc_silu_mul(const float* g, const float* u, int n, uint16_t* act) {
+  for (int i = 0; i < n; ++i) act[i] = tobf(lisa_silu_exp2(bfr(g[i])) * bfr(u[i]));
+}
+
+// gdn.metal:125-207 (conv part) and 212-240 (history update).
+void orc_gdn_conv(const float* qkv, const uint16_t* conv_w, uint16_t* conv_state, int m_rows,
+                  float* conv_out, uint16_t* slots) {
+  const int C = LISA_GDN_CONV_DIM;
+  if (m_rows < 1 || m_rows > 16) return;
+  for (int c = 0; c < C; ++c) {
+    float hist[3 + 16];
+    for (int i = 0; i < 3; ++i) hist[i] = bf(conv_state[(size_t)i * C + c]);
+    for (int t = 0; t < m_rows; ++t) hist[3 + t] = bfr(qkv[(size_t)t * C + c]);
+    for (int t = 0; t < m_rows; ++t) {
+      float acc = 0.0f;
+      for (int tap = 0; tap < 4; ++tap) acc = acc + hist[t + tap] * bf(conv_w[(size_t)c * 4 + tap]);
+      const float conv = bfr(acc);
+      conv_out[(size_t)t * C + c] = bfr(lisa_silu_exp(conv));
+      if (slots)
+        for (int i = 0; i < 3; ++i) slots[((size_t)t * 3 + i) * C + c] = tobf(hist[t + 1 + i]);
+    }
+    for (int i = 0; i < 3; ++i) conv_state[(size_t)i * C + c] = tobf(hist[m_rows + i]);
+  }
+}
+
+// gdn.metal:125-207 (norms and gates), 245-328 (recurrence), 367-391 (gate).
+void orc_gdn_recurrence(const float* conv_out, const float* z, const float* a, const float* b,
+                        const uint16_t* a_log, const uint16_t* dt_bias, const uint16_t* norm_w,
+                        float* state, int m_rows, uint16_t* gated, float* slots, float* y_out) {
+  const int C = LISA_GDN_CONV_DIM, HD = LISA_GDN_HD, VH = LISA_GDN_VH;
+  const float inv = 1.0f / lisa_sqrt((float)HD);  // runner.rs:1317 scales
+  const float q_scale = inv * inv, k_scale = inv;
+#pragma omp parallel for schedule(static)
+  for (int h = 0; h < VH; ++h) {
+    const int kh = h / (VH / LISA_GDN_KH);
+    float* S = state + (size_t)h * HD * HD;
+    for (int t = 0; t < m_rows; ++t) {
+      const float* co = conv_out + (size_t)t * C;
+      float cq[128], ck[128], qn[128], kn[128];
+      for (int i = 0; i < HD; ++i) {
+        cq[i] = co[kh * HD + i];
+        ck[i] = co[LISA_GDN_KEY_DIM + kh * HD + i];
+      }
+      const float q_inv = lisa_rsqrt(sumsq_tree128(cq) / (float)HD + 1.0e-6f) * q_scale;
+      const float k_inv = lisa_rsqrt(sumsq_tree128(ck) / (float)HD + 1.0e-6f) * k_scale;
+      for (int i = 0; i < HD; ++i) {
+        qn[i] = bfr(cq[i] * q_inv);
+        kn[i] = bfr(ck[i] * k_inv);
+      }
+      const float beta = bfr(lisa_sigmoid_exp(bfr(b[(size_t)t * VH + h])));
+      const float dt_arg = bfr(bfr(a[(size_t)t * VH + h]) + bf(dt_bias[h]));
+      const float dt = bfr(lisa_softplus(dt_arg));
+      const float decay = lisa_expf(-lisa_expf(bf(a_log[h])) * dt);
+      float y[128];
+      for (int v = 0; v < HD; ++v) {
+        float* row = S + (size_t)v * HD;
+        for (int k = 0; k < HD; ++k) row[k] = row[k] * decay;
+        float pk[4], pq[4];
+        for (int q = 0; q < 4; ++q) {
+          float p = row[32 * q] * kn[32 * q];
+          for (int k = 32 * q + 1; k < 32 * q + 32; ++k) p = lisa_fma(row[k], kn[k], p);
+          pk[q] = p;
+        }
+        const float kv = (pk[0] + pk[1]) + (pk[2] + pk[3]);
+        const float vval = co[2 * LISA_GDN_KEY_DIM + h * HD + v];
+        const float delta = (vval - kv) * beta;
+        for (int k = 0; k < HD; ++k) row[k] = lisa_fma(delta, kn[k], row[k]);
+        for (int q = 0; q < 4; ++q) {
+          float p = row[32 * q] * qn[32 * q];
+          for (int k = 32 * q + 1; k < 32 * q + 32; ++k) p = lisa_fma(row[k], qn[k], p);
+          pq[q] = p;
+        }
+        y[v] = bfr((pq[0] + pq[1]) + (pq[2] + pq[3]));
+      }
+      if (y_out)
+        for (int v = 0; v < HD; ++v) y_out[(size_t)t * LISA_GDN_VALUE_DIM + h * HD + v] = y[v];
+      const float ginv = lisa_rsqrt(sumsq_tree128(y) / 128.0f + LISA_EPS);
+      for (int v = 0; v < HD; ++v) {
+        const float n = bfr((y[v] * ginv) * bf(norm_w[v]));
+        const float zz = bfr(z[(size_t)t * LISA_GDN_VALUE_DIM + h * HD + v]);
+        gated[(size_t)t * LISA_GDN_VALUE_DIM + h * HD + v] = tobf(n * lisa_silu_exp(zz));
+      }
+      if (slots)
+        std::memcpy(slots + (size_t)t * LISA_GDN_STATE + (size_t)h * HD * HD, S,
+                    sizeof(float) * HD * HD);
+    }
+  }
+}
+
+// attention.metal:118-155 / 158-197: RMSNorm with learned gain then partial
+// NeoX RoPE on dims [0,64) with pairs (j, j+32); sum of squares by
+// rows-of-256 (one element per thread).
+void orc_head_norm_rope(const float* raw, const uint16_t* w, uint32_t position, uint16_t* out) {
+  static const float inv_freq[LISA_ROPE_PAIRS] = LISA_ROPE_INV_FREQ_TABLE;
+  float v[256], n[256];
+  for (int j = 0; j < 256; ++j) v[j] = bfr(raw[j]);
+  const float inv = lisa_rsqrt(sumsq_rows256(v, 256) / 256.0f + LISA_EPS);
+  for (int j = 0; j < 256; ++j) n[j] = (v[j] * inv) * bf(w[j]);
+  for (int j = 0; j < 32; ++j) {
+    const float angle = (float)position * inv_freq[j];
+    float s, c;
+    lisa_sincosf(angle, &s, &c);
+    out[j] = tobf(n[j] * c - n[j + 32] * s);
+    out[j + 32] = tobf(n[j + 32] * c + n[j] * s);
+  }
+  for (int j = 64; j < 256; ++j) out[j] = tobf(n[j]);
+}
+
+// attention.metal:158-197 (store), 550-604 (slice partials), 611-641 (merge),
+// 520-531 (output gate). Slice s covers tokens [64s, 64s+64) of the row's own
+// context, so a row's result does not depend on the other rows of the batch.
+void orc_attention(const float* q_proj, const float* k_raw, const float* v_raw,
+                   const uint16_t* q_norm_w, const uint16_t* k_norm_w, uint16_t* key_cache,
+                   uint16_t* value_cache, uint32_t capacity, uint32_t base, int m_rows,
+                   uint16_t* gated) {
+  const int HD = LISA_ATT_HD;
+  for (int t = 0; t < m_rows; ++t) {
+    const uint32_t pos = base + t;
+    for (int kvh = 0; kvh < LISA_ATT_KVH; ++kvh) {
+      uint16_t kr[256];
+      orc_head_norm_rope(k_raw + (size_t)t * LISA_ATT_KV_OUT + kvh * HD, k_norm_w, pos, kr);
+      const size_t off = ((size_t)kvh * capacity + pos) * HD;
+      std::memcpy(key_cache + off, kr, sizeof(kr));
+      for (int j = 0; j < HD; ++j) value_cache[off + j] = tobf(v_raw[(size_t)t * LISA_ATT_KV_OUT + kvh * HD + j]);
+    }
+  }
+  std::vector<uint16_t> query((size_t)m_rows * LISA_ATT_OUT);
+  for (int t = 0; t < m_rows; ++t)
+    for (int h = 0; h < LISA_ATT_QH; ++h)
+      orc_head_norm_rope(q_proj + (size_t)t * LISA_ATT_Q_OUT + h * 512, q_norm_w, base + t,
+                         &query[(size_t)t * LISA_ATT_OUT + h * HD]);
+  std::vector<float> o((size_t)m_rows * LISA_ATT_OUT);
+  orc_sdpa(query.data(), key_cache, value_cache, capacity, base, m_rows, o.data());
+  for (int t = 0; t < m_rows; ++t)
+    for (int h = 0; h < LISA_ATT_QH; ++h)
+      for (int d = 0; d < HD; ++d) {
+        const float g = bfr(q_proj[(size_t)t * LISA_ATT_Q_OUT + h * 512 + 256 + d]);
+        gated[(size_t)t * LISA_ATT_OUT + h * HD + d] =
+            tobf(o[(size_t)t * LISA_ATT_OUT + h * HD + d] * lisa_sigmoid_exp2(g));
+      }
+}
+
+// attention.metal:550-604 and 611-641: per slice s of 64 tokens of the row's
+// own context, scores (4 accumulators over d mod 4, then (a0+a1)+(a2+a3)),
+// slice max, p = exp2(log2e*(score-max)), denominator by tree64 over the 64
+// token lanes, P.V accumulated over tokens in order; then the flash merge in
+// ascending slice order with fma. query bf16[m][24][256]; out f32[m][24][256].
+void orc_sdpa(const uint16_t* query, const uint16_t* key_cache, const uint16_t* value_cache, uint32_t capacity,
+              uint32_t base, int m_rows, float* out) {
+  const int HD = LISA_ATT_HD;
+#pragma omp parallel for collapse(2) schedule(static)
+  for (int t = 0; t < m_rows; ++t) {
+    for (int h = 0; h < LISA_ATT_QH; ++h) {
+      const uint32_t pos = base + t, ctx = pos + 1;
+      const int kvh = h / (LISA_ATT_QH / LISA_ATT_KVH);
+      float q[256];
+      for (int d = 0; d < HD; ++d) q[d] = bf(query[(size_t)t * LISA_ATT_OUT + h * HD + d]);
+      const int used = (int)((ctx + LISA_ATT_SLICE - 1) / LISA_ATT_SLICE);
+      std::vector<float> ms(used), dens(used), acc((size_t)used * HD);
+      for (int s = 0; s < used; ++s) {
+        const uint32_t t0 = s * LISA_ATT_SLICE, t1 = std::min<uint32_t>(t0 + LISA_ATT_SLICE, ctx);
+        float score[64], p[64];
+        float mx = -INFINITY;
+        for (uint32_t tok = t0; tok < t1; ++tok) {
+          const uint16_t* kr = key_cache + ((size_t)kvh * capacity + tok) * HD;
+          float a4[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+          for (int d = 0; d < HD; ++d) a4[d & 3] = lisa_fma(q[d], bf(kr[d]), a4[d & 3]);
+          score[tok - t0] = ((a4[0] + a4[1]) + (a4[2] + a4[3])) * 0.0625f;
+          mx = std::max(mx, score[tok - t0]);
+        }
+        for (int i = 0; i < 64; ++i)
+          p[i] = (i < (int)(t1 - t0)) ? lisa_exp2f(1.4426950408889634f * (score[i] - mx)) : 0.0f;
+        float den_l[64];
+        std::memcpy(den_l, p, sizeof(p));
+        dens[s] = tree_xor(den_l, 64);
+        ms[s] = mx;
+        for (int d = 0; d < HD; ++d) {
+          float a = 0.0f;
+          for (uint32_t tok = t0; tok < t1; ++tok)
+            a = lisa_fma(p[tok - t0], bf(value_cache[((size_t)kvh * capacity + tok) * HD + d]), a);
+          acc[(size_t)s * HD + d] = a;
+        }
+      }
+      float gmax = -INFINITY;
+      for (int s = 0; s < used; ++s) gmax = std::max(gmax, ms[s]);
+      std::vector<float> wts(used);
+      float tot = 0.0f;
+      for (int s = 0; s < used; ++s) {
+        wts[s] = lisa_exp2f(1.4426950408889634f * (ms[s] - gmax));
+        tot = lisa_fma(wts[s], dens[s], tot);
+      }
+      for (int d = 0; d < HD; ++d) {
+        float res = 0.0f;
+        for (int s = 0; s < used; ++s) res = lisa_fma(wts[s], acc[(size_t)s * HD + d], res);
+        out[(size_t)t * LISA_ATT_OUT + h * HD + d] = res / tot;
+      }
+    }
+  }
+}
+
+uint32_t orc_argmax(const float* v, int n) {
+  uint32_t best = 0;
+  float bv = -INFINITY;
+  bool any = false;
+  for (int i = 0; i < n; ++i) {
+    if (!any) {
+      if (v[i] == v[i]) { bv = v[i]; best = i; any = true; }
+    } else if (v[i] > bv) {
+      bv = v[i];
+      best = i;
+    }
+  }
+  return best;
+}
+
+void orc_synth_bf16(uint64_t seed, uint64_t tensor_id, int dist, float a, float b, size_t n,
+                    uint16_t* out) {
+  synth_bf16(seed, tensor_id, dist, a, b, n, out);
+}
+
+// Element-wise evaluation of the shared numerics (lisa_numerics.h) for tests:
+// fn 0 exp, 1 exp2, 2 log, 3 sin, 4 cos, 5 rsqrt, 6 bf16 round, 7 silu(exp),
+// 8 softplus, 9 sigmoid(exp), 10 silu(exp2), 11 sigmoid(exp2).
+void orc_math(int fn, const float* x, size_t n, float* out) {
+  for (size_t i = 0; i < n; ++i) {
+    const float v = x[i];
+    float s, c;
+    switch (fn) {
+      case 0: out[i] = lisa_expf(v); break;
+      case 1: out[i] = lisa_exp2f(v); break;
+      case 2: out[i] = lisa_logf(v); break;
+      case 3: lisa_sincosf(v, &s, &c); out[i] = s; break;
+      case 4: lisa_sincosf(v, &s, &c); out[i] = c; break;
+      case 5: out[i] = lisa_rsqrt(v); break;
+      case 6: out[i] = lisa_bf16r(v); break;
+      case 7: out[i] = lisa_silu_exp(v); break;
+      case 8: out[i] = lisa_softplus(v); break;
+      case 9: out[i] = lisa_sigmoid_exp(v); break;
+      case 10: out[i] = lisa_silu_exp2(v); break;
+      default: out[i] = lisa_sigmoid_exp2(v); break;
+    }
+  }
+}
+void orc_synth_f32(uint64_t seed, uint64_t tensor_id, int dist, float a, float b, size_t n,
+                   float* out) {
+  synth_f32(seed, tensor_id, dist, a, b, n, out);
+}
+void orc_synth_words(uint64_t seed, uint64_t tensor_id, size_t n, uint32_t* out) {
+  synth_words(seed, tensor_id, n, out);
+}
+
+}  // extern "C"
+
+// =============================================================================
+// model-level restatement
+// =============================================================================
+struct OrcLayer {
+  bool attention = false;
+  std::vector<uint16_t> input_norm, post_norm;
+  Q4 gate, up, down;
+  // GDN
+  Q4 qkv, z, a, b, out;
+  std::vector<uint16_t> conv_w, a_log, dt_bias, gnorm;
+  int state_index = -1;
+  // attention
+  Q4 q, k, v, o;
+  std::vector<uint16_t> q_norm, k_norm;
+  int cache_index = -1;
+};
+
+struct OrcMtp {
+  std::vector<uint16_t> pre_fc_emb, pre_fc_hid, input_norm, post_norm, final_norm, q_norm, k_norm;
+  Q4 fc, q, k, v, o, gate, up, down;
+  std::vector<uint16_t> key_cache, value_cache;
+  uint32_t position = 0;
+};
+
+struct OrcModel {
+  int layers = 0, vocab = 0, gdn_layers = 0, attn_layers = 0;
+  uint32_t capacity = 0;
+  uint64_t seed = 0;
+  std::vector<OrcLayer> L;
+  Q4 embed, head;
+  std::vector<uint16_t> final_norm;
+  std::vector<float> gdn_state;       // [gdn][48*128*128]
+  std::vector<uint16_t> conv_state;   // [gdn][3][10240]
+  std::vector<float> gdn_slots;       // [3][gdn][state]
+  std::vector<uint16_t> conv_slots;   // [3][gdn][3][10240]
+  std::vector<uint16_t> key_cache, value_cache;  // [attn][4][cap][256]
+  uint32_t position = 0;
+  int64_t verify_base = -1;
+  bool has_mtp = false;
+  OrcMtp mtp;
+};
+
+static void embed_rows(const OrcModel* M, const uint32_t* tokens, int m, std::vector<float>& h) {
+  h.assign((size_t)m * LISA_HIDDEN, 0.0f);
+  std::vector<uint16_t> row(LISA_HIDDEN);
+  for (int t = 0; t < m; ++t) {
+    orc_embed(M->embed.w.data(), M->embed.s.data(), M->embed.b.data(), tokens[t], LISA_HIDDEN, row.data());
+    for (int c = 0; c < LISA_HIDDEN; ++c) h[(size_t)t * LISA_HIDDEN + c] = bf(row[c]);
+  }
+}
+
+static void norm_rows(const std::vector<float>& h, int m, const std::vector<uint16_t>& w,
+                      std::vector<XPrep>& xp, std::vector<uint16_t>* keep = nullptr) {
+  xp.resize(m);
+  std::vector<uint16_t> x(LISA_HIDDEN);
+  if (keep) keep->resize((size_t)m * LISA_HIDDEN);
+  for (int t = 0; t < m; ++t) {
+    rms_norm_f(&h[(size_t)t * LISA_HIDDEN], w.data(), LISA_HIDDEN, x.data());
+    prep_x(x.data(), LISA_HIDDEN, xp[t]);
+    if (keep) std::memcpy(keep->data() + (size_t)t * LISA_HIDDEN, x.data(), LISA_HIDDEN * 2);
+  }
+}
+
+static void prep_rows(const std::vector<uint16_t>& x, int m, int k, std::vector<XPrep>& xp) {
+  xp.resize(m);
+  for (int t = 0; t < m; ++t) prep_x(&x[(size_t)t * k], k, xp[t]);
+}
+
+static void residual_rows(const std::vector<float>& h, const std::vector<float>& o, int m,
+                          std::vector<float>& r) {
+  r.resize((size_t)m * LISA_HIDDEN);
+  for (size_t i = 0; i < (size_t)m * LISA_HIDDEN; ++i) r[i] = bfr(h[i] + bfr(o[i]));
+}
+
+static void mlp_block(const Q4& gate, const Q4& up, const Q4& down, const std::vector<XPrep>& xp,
+                      int m, std::vector<float>& branch) {
+  std::vector<float> g((size_t)m * LISA_INTER), u((size_t)m * LISA_INTER);
+  q4_apply(gate, xp, m, 2 * LISA_INTER, g.data());
+  q4_apply(up, xp, m, 2 * LISA_INTER, u.data());
+  std::vector<uint16_t> act((size_t)m * LISA_INTER);
+  orc_silu_mul(g.data(), u.data(), m * LISA_INTER, act.data());
+  std::vector<XPrep> ap;
+  prep_rows(act, m, LISA_INTER, ap);
+  branch.resize((size_t)m * LISA_HIDDEN);
+  q4_apply(down, ap, m, LISA_HIDDEN, branch.data());
+}
+
+static void attention_block(const Q4& q, const Q4& k, const Q4& v, const Q4& o,
+                            const std::vector<uint16_t>& qn, const std::vector<uint16_t>& kn,
+                            uint16_t* kc, uint16_t* vc, uint32_t capacity, uint32_t base,
+                            const std::vector<XPrep>& xp, int m, std::vector<float>& branch) {
+  std::vector<float> qp((size_t)m * LISA_ATT_Q_OUT), kr((size_t)m * LISA_ATT_KV_OUT),
+      vr((size_t)m * LISA_ATT_KV_OUT);
+  const int att_rows = LISA_ATT_Q_OUT + 2 * LISA_ATT_KV_OUT;
+  q4_apply(q, xp, m, att_rows, qp.data());
+  q4_apply(k, xp, m, att_rows, kr.data());
+  q4_apply(v, xp, m, att_rows, vr.data());
+  std::vector<uint16_t> gated((size_t)m * LISA_ATT_OUT);
+  orc_attention(qp.data(), kr.data(), vr.data(), qn.data(), kn.data(), kc, vc, capacity, base, m,
+                gated.data());
+  std::vector<XPrep> gp;
+  prep_rows(gated, m, LISA_ATT_OUT, gp);
+  branch.resize((size_t)m * LISA_HIDDEN);
+  q4_apply(o, gp, m, LISA_HIDDEN, branch.data());
+}
+
+extern "C" {
+
+OrcModel* orc_model_create(int layers, int vocab, int capacity, uint64_t seed, int with_mtp) {
+  if (layers <= 0 || layers % 4 != 0 || vocab <= 0 || capacity <= 0) return nullptr;
+  OrcModel* M = new OrcModel();
+  M->layers = layers;
+  M->vocab = vocab;
+  M->capacity = capacity;
+  M->seed = seed;
+  M->L.resize(layers);
+  for (int i = 0; i < layers; ++i) {
+    OrcLayer& l = M->L[i];
+    const int sc = i + 1;
+    l.attention = lisa_layer_is_attention(i);
+    l.input_norm = make_norm(seed, sc, LISA_T_INPUT_NORM, LISA_HIDDEN);
+    l.post_norm = make_norm(seed, sc, LISA_T_POST_NORM, LISA_HIDDEN);
+    l.gate = make_q4(seed, sc, LISA_T_MLP_GATE, LISA_INTER, LISA_HIDDEN);
+    l.up = make_q4(seed, sc, LISA_T_MLP_UP, LISA_INTER, LISA_HIDDEN);
+    l.down = make_q4(seed, sc, LISA_T_MLP_DOWN, LISA_HIDDEN, LISA_INTER);
+    if (l.attention) {
+      l.q = make_q4(seed, sc, LISA_T_ATT_Q, LISA_ATT_Q_OUT, LISA_HIDDEN);
+      l.k = make_q4(seed, sc, LISA_T_ATT_K, LISA_ATT_KV_OUT, LISA_HIDDEN);
+      l.v = make_q4(seed, sc, LISA_T_ATT_V, LISA_ATT_KV_OUT, LISA_HIDDEN);
+      l.o = make_q4(seed, sc, LISA_T_ATT_O, LISA_HIDDEN, LISA_ATT_OUT);
+      l.q_norm = make_norm(seed, sc, LISA_T_ATT_Q_NORM, LISA_ATT_HD);
+      l.k_norm = make_norm(seed, sc, LISA_T_ATT_K_NORM, LISA_ATT_HD);
+      l.cache_index = M->attn_layers++;
+    } else {
+      l.qkv = make_q4(seed, sc, LISA_T_GDN_QKV, LISA_GDN_CONV_DIM, LISA_HIDDEN);
+      l.z = make_q4(seed, sc, LISA_T_GDN_Z, LISA_GDN_VALUE_DIM, LISA_HIDDEN);
+      l.a = make_q4(seed, sc, LISA_T_GDN_A, LISA_GDN_VH, LISA_HIDDEN);
+      l.b = make_q4(seed, sc, LISA_T_GDN_B, LISA_GDN_VH, LISA_HIDDEN);
+      l.out = make_q4(seed, sc, LISA_T_GDN_OUT, LISA_HIDDEN, LISA_GDN_VALUE_DIM);
+      l.conv_w = make_vec(seed, sc, LISA_T_GDN_CONV_W, LISA_GDN_CONV_DIM * 4, -0.5f, 0.5f);
+      l.a_log = make_vec(seed, sc, LISA_T_GDN_A_LOG, LISA_GDN_VH, -2.0f, 0.0f);
+      l.dt_bias = make_vec(seed, sc, LISA_T_GDN_DT_BIAS, LISA_GDN_VH, -1.0f, 1.0f);
+      l.gnorm = make_norm(seed, sc, LISA_T_GDN_NORM, LISA_GDN_HD);
+      l.state_index = M->gdn_layers++;
+    }
+  }
+  M->embed = make_q4(seed, 0, LISA_T_EMBED, vocab, LISA_HIDDEN);
+  M->head = make_q4(seed, 0, LISA_T_LM_HEAD, vocab, LISA_HIDDEN);
+  M->final_norm = make_norm(seed, 0, LISA_T_FINAL_NORM, LISA_HIDDEN);
+  M->gdn_state.assign((size_t)M->gdn_layers * LISA_GDN_STATE, 0.0f);
+  M->conv_state.assign((size_t)M->gdn_layers * 3 * LISA_GDN_CONV_DIM, 0);
+  M->gdn_slots.assign((size_t)3 * M->gdn_layers * LISA_GDN_STATE, 0.0f);
+  M->conv_slots.assign((size_t)3 * M->gdn_layers * 3 * LISA_GDN_CONV_DIM, 0);
+  const size_t cache = (size_t)M->attn_layers * LISA_ATT_KVH * capacity * LISA_ATT_HD;
+  M->key_cache.assign(cache, 0);
+  M->value_cache.assign(cache, 0);
+  if (with_mtp) {
+    const int sc = LISA_SCOPE_MTP;
+    OrcMtp& t = M->mtp;
+    M->has_mtp = true;
+    t.pre_fc_emb = make_norm(seed, sc, LISA_T_MTP_PRE_FC_EMB, LISA_HIDDEN);
+    t.pre_fc_hid = make_norm(seed, sc, LISA_T_MTP_PRE_FC_HID, LISA_HIDDEN);
+    t.fc = make_q4(seed, sc, LISA_T_MTP_FC, LISA_HIDDEN, 2 * LISA_HIDDEN);
+    t.input_norm = make_norm(seed, sc, LISA_T_INPUT_NORM, LISA_HIDDEN);
+    t.post_norm = make_norm(seed, sc, LISA_T_POST_NORM, LISA_HIDDEN);
+    t.final_norm = make_norm(seed, sc, LISA_T_FINAL_NORM, LISA_HIDDEN);
+    t.q = make_q4(seed, sc, LISA_T_ATT_Q, LISA_ATT_Q_OUT, LISA_HIDDEN);
+    t.k = make_q4(seed, sc, LISA_T_ATT_K, LISA_ATT_KV_OUT, LISA_HIDDEN);
+    t.v = make_q4(seed, sc, LISA_T_ATT_V, LISA_ATT_KV_OUT, LISA_HIDDEN);
+    t.o = make_q4(seed, sc, LISA_T_ATT_O, LISA_HIDDEN, LISA_ATT_OUT);
+    t.q_norm = make_norm(seed, sc, LISA_T_ATT_Q_NORM, LISA_ATT_HD);
+    t.k_norm = make_norm(seed, sc, LISA_T_ATT_K_NORM, LISA_ATT_HD);
+    t.gate = make_q4(seed, sc, LISA_T_MLP_GATE, LISA_INTER, LISA_HIDDEN);
+    t.up = make_q4(seed, sc, LISA_T_MLP_UP, LISA_INTER, LISA_HIDDEN);
+    t.down = make_q4(seed, sc, LISA_T_MLP_DOWN, LISA_HIDDEN, LISA_INTER);
+    t.key_cache.assign((size_t)LISA_ATT_KVH * capacity * LISA_ATT_HD, 0);
+    t.value_cache.assign((size_t)LISA_ATT_KVH * capacity * LISA_ATT_HD, 0);
+  }
+  return M;
+}
+
+void orc_model_free(OrcModel* m) { delete m; }
+uint32_t orc_model_position(const OrcModel* m) { return m->position; }
+uint32_t orc_mtp_position(const OrcModel* m) { return m->mtp.position; }
+
+void orc_model_reset(OrcModel* M) {
+  std::fill(M->gdn_state.begin(), M->gdn_state.end(), 0.0f);
+  std::fill(M->conv_state.begin(), M->conv_state.end(), 0);
+  std::fill(M->key_cache.begin(), M->key_cache.end(), 0);
+  std::fill(M->value_cache.begin(), M->value_cache.end(), 0);
+  if (M->has_mtp) {
+    std::fill(M->mtp.key_cache.begin(), M->mtp.key_cache.end(), 0);
+    std::fill(M->mtp.value_cache.begin(), M->mtp.value_cache.end(), 0);
+    M->mtp.position = 0;
+  }
+  M->position = 0;
+  M->verify_base = -1;
+}
+
+// Synthetic start state: GDN state N(0,0.01), conv history and KV rows N(0,1).
+// Element indices are independent of capacity: KV element (kvh, pos, d) is
+// number (kvh * 2^20 + pos) * 256 + d of its stream.
+static void fill_kv(uint64_t seed, int scope, uint16_t* kc, uint16_t* vc, uint32_t capacity,
+                    uint32_t filled) {
+  const uint64_t kk = lisa_stream_key(seed, lisa_tensor_id(scope, LISA_T_KEY_CACHE, 0));
+  const uint64_t vk = lisa_stream_key(seed, lisa_tensor_id(scope, LISA_T_VALUE_CACHE, 0));
+#pragma omp parallel for collapse(2) schedule(static)
+  for (int kvh = 0; kvh < LISA_ATT_KVH; ++kvh)
+    for (uint32_t p = 0; p < filled; ++p)
+      for (int d = 0; d < LISA_ATT_HD; ++d) {
+        const uint64_t e = (((uint64_t)kvh << 20) + p) * LISA_ATT_HD + d;
+        const size_t off = ((size_t)kvh * capacity + p) * LISA_ATT_HD + d;
+        kc[off] = tobf(lisa_synth_value(kk, e, LISA_DIST_NORMAL, 0.0f, 1.0f));
+        vc[off] = tobf(lisa_synth_value(vk, e, LISA_DIST_NORMAL, 0.0f, 1.0f));
+      }
+}
+
+void orc_model_fill_state(OrcModel* M, uint32_t filled, uint64_t seed) {
+  orc_model_reset(M);
+  for (int i = 0; i < M->layers; ++i) {
+    const OrcLayer& l = M->L[i];
+    const int sc = i + 1;
+    if (!l.attention) {
+      synth_f32(seed, lisa_tensor_id(sc, LISA_T_GDN_STATE, 0), LISA_DIST_NORMAL, 0.0f, 0.01f,
+                LISA_GDN_STATE, &M->gdn_state[(size_t)l.state_index * LISA_GDN_STATE]);
+      synth_bf16(seed, lisa_tensor_id(sc, LISA_T_CONV_STATE, 0), LISA_DIST_NORMAL, 0.0f, 1.0f,
+                 3 * LISA_GDN_CONV_DIM, &M->conv_state[(size_t)l.state_index * 3 * LISA_GDN_CONV_DIM]);
+    } else {
+      const size_t off = (size_t)l.cache_index * LISA_ATT_KVH * M->capacity * LISA_ATT_HD;
+      fill_kv(seed, sc, &M->key_cache[off], &M->value_cache[off], M->capacity, filled);
+    }
+  }
+  if (M->has_mtp) {
+    fill_kv(seed, LISA_SCOPE_MTP, M->mtp.key_cache.data(), M->mtp.value_cache.data(), M->capacity, filled);
+    M->mtp.position = filled;
+  }
+  M->position = filled;
+}
+
+int orc_model_forward(OrcModel* M, const uint32_t* tokens, int m, int capture, uint32_t* argmax_out,
+                      float* hidden_out, float* logits_out) {
+  if (m < 1 || m > 3) return -1;
+  for (int t = 0; t < m; ++t)
+    if ((int)tokens[t] >= M->vocab) return -2;
+  if (M->position + m > M->capacity) return -3;
+  const uint32_t base = M->position;
+  std::vector<float> H, R, B;
+  embed_rows(M, tokens, m, H);
+  std::vector<XPrep> xp;
+  for (int i = 0; i < M->layers; ++i) {
+    OrcLayer& l = M->L[i];
+    norm_rows(H, m, l.input_norm, xp);
+    if (!l.attention) {
+      const int si = l.state_index;
+      std::vector<float> qkv((size_t)m * LISA_GDN_CONV_DIM), z((size_t)m * LISA_GDN_VALUE_DIM),
+          a((size_t)m * LISA_GDN_VH), b((size_t)m * LISA_GDN_VH);
+      const int gdn_rows = LISA_GDN_CONV_DIM + LISA_GDN_VALUE_DIM + 2 * LISA_GDN_VH;
+      q4_apply(l.qkv, xp, m, gdn_rows, qkv.data());
+      q4_apply(l.z, xp, m, gdn_rows, z.data());
+      q4_apply(l.a, xp, m, gdn_rows, a.data());
+      q4_apply(l.b, xp, m, gdn_rows, b.data());
+      std::vector<float> conv_out((size_t)m * LISA_GDN_CONV_DIM);
+      std::vector<uint16_t> cslots;
+      if (capture) cslots.resize((size_t)m * 3 * LISA_GDN_CONV_DIM);
+      uint16_t* cs = &M->conv_state[(size_t)si * 3 * LISA_GDN_CONV_DIM];
+      orc_gdn_conv(qkv.data(), l.conv_w.data(), cs, m, conv_out.data(), capture ? cslots.data() : nullptr);
+      std::vector<float> gslots;
+      if (capture) gslots.resize((size_t)m * LISA_GDN_STATE);
+      std::vector<uint16_t> gated((size_t)m * LISA_GDN_VALUE_DIM);
+      float* st = &M->gdn_state[(size_t)si * LISA_GDN_STATE];
+      orc_gdn_recurrence(conv_out.data(), z.data(), a.data(), b.data(), l.a_log.data(),
+                         l.dt_bias.data(), l.gnorm.data(), st, m, gated.data(),
+                         capture ? gslots.data() : nullptr, nullptr);
+      if (capture) {
+        for (int t = 0; t < m; ++t) {
+          std::memcpy(&M->gdn_slots[((size_t)t * M->gdn_layers + si) * LISA_GDN_STATE],
+                      &gslots[(size_t)t * LISA_GDN_STATE], sizeof(float) * LISA_GDN_STATE);
+          std::memcpy(&M->conv_slots[((size_t)t * M->gdn_layers + si) * 3 * LISA_GDN_CONV_DIM],
+                      &cslots[(size_t)t * 3 * LISA_GDN_CONV_DIM], 2 * 3 * LISA_GDN_CONV_DIM);
+        }
+      }
+      std::vector<XPrep> gp;
+      prep_rows(gated, m, LISA_GDN_VALUE_DIM, gp);
+      B.resize((size_t)m * LISA_HIDDEN);
+      q4_apply(l.out, gp, m, LISA_HIDDEN, B.data());
+    } else {
+      const size_t off = (size_t)l.cache_index * LISA_ATT_KVH * M->capacity * LISA_ATT_HD;
+      attention_block(l.q, l.k, l.v, l.o, l.q_norm, l.k_norm, &M->key_cache[off],
+                      &M->value_cache[off], M->capacity, base, xp, m, B);
+    }
+    residual_rows(H, B, m, R);
+    norm_rows(R, m, l.post_norm, xp);
+    mlp_block(l.gate, l.up, l.down, xp, m, B);
+    residual_rows(R, B, m, H);
+  }
+  norm_rows(H, m, M->final_norm, xp);
+  std::vector<float> logits((size_t)m * M->vocab);
+  q4_apply(M->head, xp, m, M->vocab, logits.data());
+  for (int t = 0; t < m; ++t) {
+    if (argmax_out) argmax_out[t] = orc_argmax(&logits[(size_t)t * M->vocab], M->vocab);
+  }
+  if (hidden_out) std::memcpy(hidden_out, H.data(), sizeof(float) * H.size());
+  if (logits_out) std::memcpy(logits_out, logits.data(), sizeof(float) * logits.size());
+  M->position += m;
+  M->verify_base = capture ? (int64_t)base : -1;
+  return 0;
+}
+
+int orc_model_commit(OrcModel* M, int rows) {
+  if (M->verify_base < 0) return -1;
+  if (rows < 1 || rows > 3) return -2;
+  const uint32_t base = (uint32_t)M->verify_base;
+  M->verify_base = -1;
+  if (rows < 3) {
+    const size_t gs = (size_t)M->gdn_layers * LISA_GDN_STATE;
+    const size_t cs = (size_t)M->gdn_layers * 3 * LISA_GDN_CONV_DIM;
+    std::memcpy(M->gdn_state.data(), &M->gdn_slots[(size_t)(rows - 1) * gs], sizeof(float) * gs);
+    std::memcpy(M->conv_state.data(), &M->conv_slots[(size_t)(rows - 1) * cs], 2 * cs);
+  }
+  M->position = base + rows;
+  return 0;
+}
+
+int orc_mtp_forward(OrcModel* M, uint32_t token, const uint16_t* cond, uint32_t* argmax_out,
+                    uint16_t* normalized_out) {
+  if (!M->has_mtp) return -1;
+  if ((int)token >= M->vocab) return -2;
+  OrcMtp& t = M->mtp;
+  if (t.position >= M->capacity) return -3;
+  std::vector<uint16_t> e(LISA_HIDDEN), x((size_t)2 * LISA_HIDDEN);
+  orc_embed(M->embed.w.data(), M->embed.s.data(), M->embed.b.data(), token, LISA_HIDDEN, e.data());
+  orc_rms_norm(e.data(), t.pre_fc_emb.data(), LISA_HIDDEN, x.data());
+  orc_rms_norm(cond, t.pre_fc_hid.data(), LISA_HIDDEN, x.data() + LISA_HIDDEN);
+  std::vector<XPrep> xp(1);
+  prep_x(x.data(), 2 * LISA_HIDDEN, xp[0]);
+  std::vector<float> fc(LISA_HIDDEN);
+  q4_apply(t.fc, xp, 1, LISA_HIDDEN, fc.data());
+  std::vector<float> H(LISA_HIDDEN), R, B;
+  for (int c = 0; c < LISA_HIDDEN; ++c) H[c] = bfr(fc[c]);  // f32_to_bf16 (norm.metal:132-137)
+  norm_rows(H, 1, t.input_norm, xp);
+  attention_block(t.q, t.k, t.v, t.o, t.q_norm, t.k_norm, t.key_cache.data(), t.value_cache.data(),
+                  M->capacity, t.position, xp, 1, B);
+  residual_rows(H, B, 1, R);
+  norm_rows(R, 1, t.post_norm, xp);
+  mlp_block(t.gate, t.up, t.down, xp, 1, B);
+  residual_rows(R, B, 1, H);
+  std::vector<uint16_t> xn;
+  norm_rows(H, 1, t.final_norm, xp, &xn);
+  std::vector<float> logits(M->vocab);
+  q4_apply(M->head, xp, 1, M->vocab, logits.data());
+  if (argmax_out) *argmax_out = orc_argmax(logits.data(), M->vocab);
+  if (normalized_out) std::memcpy(normalized_out, xn.data(), 2 * LISA_HIDDEN);
+  t.position += 1;
+  return 0;
+}
+
+int orc_mtp_trim(OrcModel* M, int count) {
+  if (count < 0 || (uint32_t)count > M->mtp.position) return -1;
+  M->mtp.position -= count;
+  return 0;
+}
+
+}  // extern "C"

@@ -1,0 +1,88 @@
+"""Shared helpers for the tests: package/oracle loading, random q4 tensors,
+and a Python restatement of the runner's q4 launch rule (tile ranges, ksplit,
+grid) for kernel-level dispatches."""
+import ctypes as C
+import importlib.util
+import sys
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parents[1]
+
+
+def load_pkg():
+    if "lisa_rs_amd" in sys.modules:
+        return sys.modules["lisa_rs_amd"]
+    pkg_dir = ROOT / "lisa-rs_amd"
+    spec = importlib.util.spec_from_file_location("lisa_rs_amd", pkg_dir / "__init__.py",
+                                                  submodule_search_locations=[str(pkg_dir)])
+    mod = importlib.util.module_from_spec(spec)
+    sys.modules["lisa_rs_amd"] = mod
+    spec.loader.exec_module(mod)
+    return mod
+
+
+def load_oracle():
+    if "lisa_oracle" in sys.modules:
+        return sys.modules["lisa_oracle"]
+    spec = importlib.util.spec_from_file_location("lisa_oracle", ROOT / "oracle" / "oracle.py")
+    mod = importlib.util.module_from_spec(spec)
+    sys.modules["lisa_oracle"] = mod
+    spec.loader.exec_module(mod)
+    return mod
+
+
+def bf16(x):
+    return load_oracle().f32_to_bf16_bits(x)
+
+
+def f32(h):
+    return load_oracle().bf16_bits_to_f32(h)
+
+
+def rand_q4(rng, n, k):
+    """MLX-affine q4 of BASELINE config 0: nibbles U{0..15}, scales U(0.005,0.02),
+    biases U(-0.1,0.1), both bf16."""
+    w = rng.integers(0, 2**32, size=(n, k // 8), dtype=np.uint64).astype(np.uint32)
+    s = bf16(rng.uniform(0.005, 0.02, size=(n, k // 64)).astype(np.float32))
+    b = bf16(rng.uniform(-0.1, 0.1, size=(n, k // 64)).astype(np.float32))
+    return w, s, b
+
+
+def pack_sb(s, b):
+    return (s.astype(np.uint32) | (b.astype(np.uint32) << 16)).astype(np.uint32)
+
+
+class DevQ4:
+    def __init__(self, dev, w, s, b):
+        self.n, self.k = w.shape[0], w.shape[1] * 8
+        self.wbuf = dev.upload(w)
+        self.sbbuf = dev.upload(pack_sb(s, b))
+        self.w, self.s, self.b = w, s, b
+
+
+def launch_qmv(pkg, dev, K, M, params, mats, grid_cap=1024):
+    """Restates launch_qmv of lisa-rs_amd/csrc/runner.cpp. mats: list of
+    (DevQ4, DevQ4-or-None, out_ptr, kind)."""
+    tiles = 0
+    rows_total = 0
+    for e, (q, q2, out, kind) in enumerate(mats):
+        m = params.mats[e]
+        m.w, m.sb = q.wbuf.ptr, q.sbbuf.ptr
+        m.w2 = q2.wbuf.ptr if q2 else 0
+        m.sb2 = q2.sbbuf.ptr if q2 else 0
+        m.out = out
+        m.rows = q.n
+        m.kind = kind
+        params.tile_start[e] = tiles
+        pair = kind == pkg.EPI_GATEUP
+        tiles += (q.n + 3) // 4 if pair else (q.n + 7) // 8
+        rows_total += 2 * q.n if pair else q.n
+    params.tile_start[len(mats)] = tiles
+    params.n_mats = len(mats)
+    params.ksplit = 4 if rows_total <= 8192 else 1
+    grid = tiles if params.ksplit == 4 else (tiles + 3) // 4
+    grid = max(1, min(grid, grid_cap))
+    dev.dispatch(f"lisa_qmv_k{K}_m{M}", params, (grid,), (256,))
+    return params.ksplit, grid

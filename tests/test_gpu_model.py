@@ -1,0 +1,139 @@
+"""GPU runner vs the CPU oracle on a reduced-depth model with the real layer
+shapes: M=1 greedy decode (graph replay), M=3 verify + rollback, the MTP
+drafter, and the speculative loop against sequential greedy decoding."""
+import numpy as np
+import pytest
+
+from _lisa import load_oracle, load_pkg
+
+pytestmark = pytest.mark.gpu
+
+LAYERS, VOCAB, CAP, SEED, CTX_SEED = 4, 4096, 320, 0x5EED1, 0xC0FFEE
+
+
+@pytest.fixture(scope="module")
+def pair():
+    pkg, orc = load_pkg(), load_oracle()
+    r = pkg.Runner(layers=LAYERS, vocab=VOCAB, capacity=CAP, seed=SEED, with_mtp=True, use_graph=True)
+    m = orc.Model(LAYERS, VOCAB, CAP, SEED, with_mtp=True)
+    yield pkg, orc, r, m
+    r.close()
+    m.close()
+
+
+def fresh(r, m, filled=64):
+    r.fill_state(filled, CTX_SEED)
+    m.fill_state(filled, CTX_SEED)
+    assert r.position == m.position == filled
+
+
+def test_decode_matches_oracle(pair):
+    pkg, orc, r, m = pair
+    fresh(r, m)
+    tok = 17
+    for _ in range(4):
+        am, hid = r.forward_token_decode(tok, want_hidden=True)
+        wam, whid = m.forward([tok])
+        assert am == int(wam[0])
+        assert np.array_equal(hid.view(np.uint32), whid[0].view(np.uint32))
+        tok = am
+    # device-side greedy loop (hipGraph replays, token fed back on device)
+    got = r.decode_greedy(tok, 6)
+    want = []
+    for _ in range(6):
+        wam, _ = m.forward([tok])
+        tok = int(wam[0])
+        want.append(tok)
+    assert list(got) == want
+    assert r.position == m.position
+
+
+def test_logits_match_oracle(pair):
+    pkg, orc, r, m = pair
+    fresh(r, m, filled=10)
+    am, hid, logits = r.forward_token_with_hidden(5)
+    wam, whid, wlog = m.forward([5], want_logits=True)
+    assert np.array_equal(logits.view(np.uint32), wlog[0].view(np.uint32))
+    assert am == orc.argmax(wlog[0]) == int(wam[0])
+
+
+@pytest.mark.parametrize("rows", [1, 2, 3])
+def test_verify_commit_matches_oracle(pair, rows):
+    """verify_block3 + commit_verified_prefix (runner.rs:866-944) against the
+    oracle, then two more M=1 steps from the rolled-back state."""
+    pkg, orc, r, m = pair
+    fresh(r, m, filled=62)  # rows cross the 64-token slice boundary
+    toks = [101, 2002, 303]
+    am, hid = r.verify_block3(toks, want_hidden=True)
+    wam, whid = m.forward(toks, capture=True)
+    assert list(am) == list(wam)
+    assert np.array_equal(hid.view(np.uint32), whid.view(np.uint32))
+    r.commit_verified_prefix(rows)
+    m.commit(rows)
+    assert r.position == m.position == 62 + rows
+    tok = int(am[rows - 1])
+    for _ in range(2):
+        a1, h1 = r.forward_token_decode(tok, want_hidden=True)
+        w1, wh1 = m.forward([tok])
+        assert a1 == int(w1[0])
+        assert np.array_equal(h1.view(np.uint32), wh1[0].view(np.uint32))
+        tok = a1
+
+
+def test_verify_row_equals_decode(pair):
+    """runner_checkpoint.rs invariant: row t of an M=3 verify equals M=1
+    decoding of the same tokens (bit-exact here: identical per-row order)."""
+    pkg, orc, r, m = pair
+    fresh(r, m, filled=40)
+    ck = r.checkpoint_state()
+    toks = [9, 99, 999]
+    am3, h3 = r.verify_block3(toks, want_hidden=True)
+    r.commit_verified_prefix(3)
+    r.restore_state(ck)
+    r.free_checkpoint(ck)
+    assert r.position == 40
+    for t in range(3):
+        a1, h1 = r.forward_token_decode(toks[t], want_hidden=True)
+        assert a1 == int(am3[t])
+        assert np.array_equal(h1.view(np.uint32), h3[t].view(np.uint32))
+
+
+def test_mtp_matches_oracle(pair):
+    pkg, orc, r, m = pair
+    fresh(r, m, filled=30)
+    am, hid = r.forward_token_decode(11, want_hidden=True)
+    wam, whid = m.forward([11])
+    cond = orc.f32_to_bf16_trunc(whid[0])  # the bf16 hidden row the drafter reads
+    d0 = r.mtp_forward(am, 0, 0)
+    w0, wn0 = m.mtp_forward(int(wam[0]), cond)
+    assert d0 == w0
+    assert np.array_equal(r.mtp_normalized(), wn0)
+    d1 = r.mtp_forward(d0, 1)
+    w1, wn1 = m.mtp_forward(w0, wn0)
+    assert d1 == w1
+    assert np.array_equal(r.mtp_normalized(), wn1)
+    assert r.mtp_position == m.mtp_position == 32
+    r.mtp_trim_state(1)
+    m.mtp_trim(1)
+    assert r.mtp_position == m.mtp_position == 31
+
+
+def test_speculative_equals_sequential(pair):
+    """tests/speculative_loop.rs:32-82: the block-3 speculative stream equals
+    sequential greedy decoding; drafts forced to a seeded Bernoulli(0.6)
+    acceptance pattern so that 1, 2 and 3 accepted rows all occur."""
+    pkg, orc, r, m = pair
+    steps = 40
+    fresh(r, m, filled=50)
+    am, hid = r.forward_token_decode(7, want_hidden=True)
+    truth = [am] + list(r.decode_greedy(am, steps - 1))
+    fresh(r, m, filled=50)
+    am2, hid2 = r.forward_token_decode(7, want_hidden=True)
+    assert am2 == am
+    seed_tok = r.mtp_forward(am2, 0, 0)
+    seed_hidden = orc.bf16_bits_to_f32(r.mtp_normalized())
+    toks, stats = r.generate_greedy_block3(am2, hid2, seed_tok, seed_hidden, steps, force_truth=truth,
+                                           force_seed=1234, p_accept=0.6)
+    assert list(toks) == truth
+    assert stats["rounds"] > 3
+    assert 0 < stats["accepted_drafts"] < stats["drafted_tokens"]
