@@ -144,6 +144,26 @@ int lisa_runner_forward_token_with_hidden(LisaRunner* r, uint32_t token, uint32_
  * receives the `steps` generated tokens. The loop of src/cli/run.rs:69-73. */
 int lisa_runner_decode_greedy(LisaRunner* r, uint32_t token, int32_t steps, uint32_t* tokens_out);
 
+/* Per-kernel profile of `steps` eager M=1 steps from `token`: every launch is
+ * bracketed by hipEvents on the device stream; kind_ms[k] / kind_count[k]
+ * receive the summed duration (ms) and number of launches of kind k. The
+ * diagnostic counterpart of profile_token_m1_diagnostic (runner.rs:660-730). */
+enum {
+  LISA_KIND_GDN_IN = 0,        /* GDN qkv/z/a/b projections (+ residual, norm, conv) */
+  LISA_KIND_GDN_RECURRENCE,    /* gated-delta recurrence + gated norm */
+  LISA_KIND_GDN_OUT,           /* GDN out_proj */
+  LISA_KIND_ATTN_IN,           /* attention q/k/v projections (+ residual, norm) */
+  LISA_KIND_ATTN_PARTIAL,      /* norm + RoPE + KV append + split-K slices */
+  LISA_KIND_ATTN_MERGE,        /* flash merge + output gate */
+  LISA_KIND_ATTN_OUT,          /* o_proj */
+  LISA_KIND_MLP_GATE_UP,       /* residual + norm + gate/up + SwiGLU */
+  LISA_KIND_MLP_DOWN,          /* down_proj */
+  LISA_KIND_LM_HEAD,           /* final residual + norm + lm_head + argmax partials */
+  LISA_KIND_FINALIZE,          /* argmax finish + token/position feedback */
+  LISA_KIND_COUNT
+};
+int lisa_runner_profile_step(LisaRunner* r, uint32_t token, int32_t steps, float* kind_ms, int32_t* kind_count);
+
 /* verify_block3_decode (runner.rs:734-909): M=3 pass with GDN/conv capture;
  * argmax[3]; hidden (nullable) f32[3][5120]; logits (nullable) f32[3][vocab].
  * position += 3 until commit. */

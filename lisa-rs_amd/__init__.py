@@ -39,6 +39,10 @@ GDN_CONV_DIM = 10240
 GDN_STATE = GDN_VH * GDN_HD * GDN_HD
 ATT_QH, ATT_KVH, ATT_HD = 24, 4, 256
 
+# launch kinds of lisa_runner_profile_step (lisa_hip.h LISA_KIND_*)
+KINDS = ["gdn_in_proj", "gdn_recurrence", "gdn_out_proj", "attn_in_proj", "attn_partial", "attn_merge",
+         "attn_o_proj", "mlp_gate_up", "mlp_down", "lm_head", "finalize"]
+
 # lisa_kernels.h enums
 PRO_LOADX, PRO_RESNORM, PRO_EMBED, PRO_CAST, PRO_NORM, PRO_MTPFC = range(6)
 EPI_STORE, EPI_GATEUP, EPI_CONV, EPI_ARGMAX = range(4)
@@ -159,6 +163,7 @@ _SIGS = {
     "lisa_runner_forward_token_decode": (C.c_int, [_P, C.c_uint32, C.POINTER(C.c_uint32), _P]),
     "lisa_runner_forward_token_with_hidden": (C.c_int, [_P, C.c_uint32, C.POINTER(C.c_uint32), _P, _P]),
     "lisa_runner_decode_greedy": (C.c_int, [_P, C.c_uint32, C.c_int32, _P]),
+    "lisa_runner_profile_step": (C.c_int, [_P, C.c_uint32, C.c_int32, _P, _P]),
     "lisa_runner_verify_block3": (C.c_int, [_P, _P, _P, _P, _P]),
     "lisa_runner_commit_verified_prefix": (C.c_int, [_P, C.c_int32]),
     "lisa_runner_checkpoint_state": (C.c_int, [_P, C.POINTER(_P)]),
@@ -377,6 +382,13 @@ class Runner:
         out = np.zeros(steps, np.uint32)
         _check(lib().lisa_runner_decode_greedy(self.h, token, steps, _ptr(out)))
         return out
+
+    def profile_step(self, token: int, steps: int = 1) -> dict:
+        """Eager M=1 steps with hipEvents around every launch: {kind: (total_ms, launches)}."""
+        ms = np.zeros(len(KINDS), np.float32)
+        cnt = np.zeros(len(KINDS), np.int32)
+        _check(lib().lisa_runner_profile_step(self.h, token, steps, _ptr(ms), _ptr(cnt)))
+        return {k: (float(ms[i]), int(cnt[i])) for i, k in enumerate(KINDS)}
 
     def verify_block3(self, tokens, want_hidden: bool = False, want_logits: bool = False):
         t = np.asarray(tokens, dtype=np.uint32)

@@ -116,6 +116,10 @@ struct LisaRunner {
   uint32_t mtp_position = 0;
   LisaGraph* step_graph = nullptr;
   uint32_t qmv_grid_cap = 1024;
+  // per-launch event profiling of eager steps (lisa_runner_profile_step)
+  bool profiling = false;
+  std::vector<hipEvent_t> prof_events;
+  std::vector<int> prof_kinds;
 };
 
 namespace {
@@ -330,6 +334,7 @@ void plan_ctx(LisaRunner* r, Arena& A, Ctx& c, int rows) {
 }
 
 // ---- launch helpers --------------------------------------------------------------
+int prof_mark(LisaRunner* r, int kind);
 struct MatSpec {
   const Q4Dev* w;
   const Q4Dev* w2;  // GATEUP
@@ -402,15 +407,19 @@ int launch_attention(LisaRunner* r, Ctx& c, int m, const uint16_t* qn, const uin
   a.capacity = (uint32_t)r->cfg.capacity;
   a.s_max = r->s_max;
   const int mi = m == 3 ? 1 : 0;
+  LISA_TRY(prof_mark(r, LISA_KIND_ATTN_PARTIAL));
   LISA_TRY(lisa_launch(r->dev, r->attn_part[mi], &a, sizeof a, r->s_max, LISA_ATT_KVH, 1, 256, 1, 1));
+  LISA_TRY(prof_mark(r, LISA_KIND_ATTN_MERGE));
   return lisa_launch(r->dev, r->attn_merge[mi], &a, sizeof a, LISA_ATT_QH, m, 1, 256, 1, 1);
 }
 
 int launch_mlp(LisaRunner* r, Ctx& c, int m, const uint16_t* post_norm, const Q4Dev& gate, const Q4Dev& up,
                const Q4Dev& down) {
   LisaQmvParams p = pro_resnorm(c.H, c.B, post_norm, c.R);
+  LISA_TRY(prof_mark(r, LISA_KIND_MLP_GATE_UP));
   LISA_TRY(launch_qmv(r, m, LISA_HIDDEN, p, {{&gate, &up, c.act, LISA_EPI_GATEUP}}));
   LisaQmvParams d = pro_loadx(c.act);
+  LISA_TRY(prof_mark(r, LISA_KIND_MLP_DOWN));
   return launch_qmv(r, m, LISA_INTER, d, {{&down, nullptr, c.B, LISA_EPI_STORE}});
 }
 
@@ -446,6 +455,8 @@ int launch_finalize(LisaRunner* r, Ctx& c, int m, bool feedback, uint32_t advanc
 }
 
 // One target forward of m rows (runner.rs:555-591 for m=1, 866-909 for m=3).
+// prof_mark(kind) is recorded before each launch (and a final -1 mark after
+// the last) when an eager profile step is running.
 int encode_target(LisaRunner* r, int m, bool capture, bool feedback) {
   Ctx& c = r->tgt;
   const float inv = 1.0f / lisa_sqrt((float)LISA_GDN_HD);  // runner.rs:1316-1317
@@ -469,6 +480,7 @@ int encode_target(LisaRunner* r, int m, bool capture, bool feedback) {
       p.conv_slots = capture ? r->conv_slots + (size_t)si * 3 * LISA_GDN_CONV_DIM : nullptr;
       p.conv_slot_stride = (uint64_t)r->gdn_layers * 3 * LISA_GDN_CONV_DIM;
       p.capture = capture ? 1 : 0;
+      LISA_TRY(prof_mark(r, LISA_KIND_GDN_IN));
       LISA_TRY(launch_qmv(r, m, LISA_HIDDEN, p,
                           {{&l.qkv, nullptr, c.conv_out, LISA_EPI_CONV},
                            {&l.z, nullptr, c.z, LISA_EPI_STORE},
@@ -489,10 +501,13 @@ int encode_target(LisaRunner* r, int m, bool capture, bool feedback) {
       g.q_scale = inv * inv;
       g.k_scale = inv;
       g.capture = capture ? 1 : 0;
+      LISA_TRY(prof_mark(r, LISA_KIND_GDN_RECURRENCE));
       LISA_TRY(lisa_launch(r->dev, r->gdn[m == 3 ? 1 : 0], &g, sizeof g, LISA_GDN_VH, 1, 1, 512, 1, 1));
       LisaQmvParams o = pro_loadx(c.gated);
+      LISA_TRY(prof_mark(r, LISA_KIND_GDN_OUT));
       LISA_TRY(launch_qmv(r, m, LISA_GDN_VALUE_DIM, o, {{&l.out, nullptr, c.B, LISA_EPI_STORE}}));
     } else {
+      LISA_TRY(prof_mark(r, LISA_KIND_ATTN_IN));
       LISA_TRY(launch_qmv(r, m, LISA_HIDDEN, p,
                           {{&l.q, nullptr, c.q_proj, LISA_EPI_STORE},
                            {&l.k, nullptr, c.k_raw, LISA_EPI_STORE},
@@ -500,12 +515,16 @@ int encode_target(LisaRunner* r, int m, bool capture, bool feedback) {
       const size_t off = (size_t)l.cache_index * LISA_ATT_KVH * r->cfg.capacity * LISA_ATT_HD;
       LISA_TRY(launch_attention(r, c, m, l.q_norm, l.k_norm, r->key_cache + off, r->value_cache + off));
       LisaQmvParams o = pro_loadx(c.gated);
+      LISA_TRY(prof_mark(r, LISA_KIND_ATTN_OUT));
       LISA_TRY(launch_qmv(r, m, LISA_ATT_OUT, o, {{&l.o, nullptr, c.B, LISA_EPI_STORE}}));
     }
     LISA_TRY(launch_mlp(r, c, m, l.post_norm, l.gate, l.up, l.down));
   }
+  LISA_TRY(prof_mark(r, LISA_KIND_LM_HEAD));
   LISA_TRY(launch_lm_head(r, c, m, r->final_norm, nullptr, c.H));
-  return launch_finalize(r, c, m, feedback, (uint32_t)m);
+  LISA_TRY(prof_mark(r, LISA_KIND_FINALIZE));
+  LISA_TRY(launch_finalize(r, c, m, feedback, (uint32_t)m));
+  return prof_mark(r, -1);
 }
 
 // MTP drafter step (runner.rs:2711-2765, attention/MLP encoders :3097-3271).
@@ -538,6 +557,17 @@ int encode_mtp(LisaRunner* r, const uint16_t* cond) {
   return launch_finalize(r, c, 1, false, 1);
 }
 
+// Launch-kind tags of the per-kernel profile (LISA_KIND_* in lisa_hip.h).
+int prof_mark(LisaRunner* r, int kind) {
+  if (!r->profiling) return LISA_OK;
+  hipEvent_t e;
+  LISA_TRY(lisa_hip_check(hipEventCreate(&e), "hipEventCreate"));
+  LISA_TRY(lisa_hip_check(hipEventRecord(e, r->dev->stream), "hipEventRecord"));
+  r->prof_events.push_back(e);
+  r->prof_kinds.push_back(kind);
+  return LISA_OK;
+}
+
 int write_pos(LisaRunner* r, Ctx& c, uint32_t pos) {
   return lisa_hip_check(hipMemcpyAsync(c.pos, &pos, 4, hipMemcpyHostToDevice, r->dev->stream), "H2D pos");
 }
@@ -556,6 +586,21 @@ int check_token(const LisaRunner* r, uint32_t token) {
   return LISA_OK;
 }
 
+// Record the M=1 step (with device-side token/position feedback) as a graph.
+int capture_step(LisaRunner* r) {
+  LISA_TRY(lisa_capture_begin(r->dev));
+  const int rc = encode_target(r, 1, false, true);
+  LisaGraph* g = nullptr;
+  const int re = lisa_capture_end(r->dev, &g);
+  if (rc) {
+    if (g) lisa_graph_free(g);
+    return rc;
+  }
+  LISA_TRY(re);
+  r->step_graph = g;
+  return LISA_OK;
+}
+
 int do_decode(LisaRunner* r, uint32_t token, uint32_t* argmax, float* hidden, float* logits) {
   LISA_TRY(check_token(r, token));
   if (r->position >= (uint32_t)r->cfg.capacity)
@@ -563,18 +608,7 @@ int do_decode(LisaRunner* r, uint32_t token, uint32_t* argmax, float* hidden, fl
   Ctx& c = r->tgt;
   LISA_TRY(upload_u32(r, c.tokens, &token, 1));
   if (r->cfg.use_graph) {
-    if (!r->step_graph) {
-      LISA_TRY(lisa_capture_begin(r->dev));
-      const int rc = encode_target(r, 1, false, true);
-      LisaGraph* g = nullptr;
-      const int re = lisa_capture_end(r->dev, &g);
-      if (rc) {
-        if (g) lisa_graph_free(g);
-        return rc;
-      }
-      LISA_TRY(re);
-      r->step_graph = g;
-    }
+    if (!r->step_graph) LISA_TRY(capture_step(r));
     LISA_TRY(lisa_graph_launch(r->step_graph, r->dev));
   } else {
     LISA_TRY(encode_target(r, 1, false, true));
@@ -738,13 +772,12 @@ extern "C" int lisa_runner_decode_greedy(LisaRunner* r, uint32_t token, int32_t 
   if (r->position + (uint32_t)steps > (uint32_t)r->cfg.capacity)
     return lisa_fail(LISA_E_CAPACITY, "KV capacity %d exhausted by %d steps", r->cfg.capacity, steps);
   if ((uint32_t)steps > kHistoryCap) return lisa_fail(LISA_E_ARG, "at most %u steps per call", kHistoryCap);
-  // first step through the host path (captures the graph), the rest replay it
-  uint32_t first = 0;
-  const uint32_t zero = 0;
   Ctx& c = r->tgt;
+  if (r->cfg.use_graph && !r->step_graph) LISA_TRY(capture_step(r));
+  const uint32_t zero = 0;
+  LISA_TRY(upload_u32(r, c.tokens, &token, 1));
   LISA_TRY(upload_u32(r, c.step, &zero, 1));
-  LISA_TRY(do_decode(r, token, &first, nullptr, nullptr));
-  for (int s = 1; s < steps; ++s) {
+  for (int s = 0; s < steps; ++s) {
     if (r->step_graph) {
       LISA_TRY(lisa_graph_launch(r->step_graph, r->dev));
     } else {
@@ -754,7 +787,41 @@ extern "C" int lisa_runner_decode_greedy(LisaRunner* r, uint32_t token, int32_t 
   LISA_TRY(lisa_hip_check(hipMemcpyAsync(tokens_out, c.history, (size_t)steps * 4, hipMemcpyDeviceToHost, r->dev->stream),
                           "D2H history"));
   LISA_TRY(sync(r));
-  r->position += (uint32_t)steps - 1;
+  r->position += (uint32_t)steps;
+  r->verify_base = -1;
+  return LISA_OK;
+}
+
+extern "C" int lisa_runner_profile_step(LisaRunner* r, uint32_t token, int32_t steps, float* kind_ms,
+                                        int32_t* kind_count) {
+  if (!r || steps <= 0 || !kind_ms || !kind_count) return lisa_fail(LISA_E_ARG, "lisa_runner_profile_step: bad argument");
+  LISA_TRY(check_token(r, token));
+  if (r->position + (uint32_t)steps > (uint32_t)r->cfg.capacity)
+    return lisa_fail(LISA_E_CAPACITY, "KV capacity %d exhausted by %d steps", r->cfg.capacity, steps);
+  for (int k = 0; k < LISA_KIND_COUNT; ++k) {
+    kind_ms[k] = 0.0f;
+    kind_count[k] = 0;
+  }
+  Ctx& c = r->tgt;
+  LISA_TRY(upload_u32(r, c.tokens, &token, 1));
+  r->profiling = true;
+  int rc = LISA_OK;
+  for (int s = 0; s < steps && !rc; ++s) rc = encode_target(r, 1, false, true);
+  r->profiling = false;
+  if (!rc) rc = sync(r);
+  for (size_t i = 0; !rc && i + 1 < r->prof_events.size(); ++i) {
+    const int kind = r->prof_kinds[i];
+    if (kind < 0 || kind >= LISA_KIND_COUNT) continue;
+    float ms = 0.0f;
+    rc = lisa_hip_check(hipEventElapsedTime(&ms, r->prof_events[i], r->prof_events[i + 1]), "hipEventElapsedTime");
+    kind_ms[kind] += ms;
+    kind_count[kind] += 1;
+  }
+  for (hipEvent_t e : r->prof_events) (void)hipEventDestroy(e);
+  r->prof_events.clear();
+  r->prof_kinds.clear();
+  if (rc) return rc;
+  r->position += (uint32_t)steps;
   return LISA_OK;
 }
 

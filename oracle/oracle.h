@@ -94,6 +94,8 @@ typedef struct OrcModel OrcModel;
 OrcModel* orc_model_create(int layers, int vocab, int capacity, uint64_t seed, int with_mtp);
 void orc_model_free(OrcModel* m);
 uint32_t orc_model_position(const OrcModel* m);
+/* OpenMP threads the oracle runs on. */
+int orc_threads(void);
 /* Fill recurrent state, conv history and the first `filled` KV positions with
  * synthetic values and set position = filled (the bench's 4k-context start). */
 void orc_model_fill_state(OrcModel* m, uint32_t filled, uint64_t seed);

@@ -30,6 +30,7 @@ _SIGS = {
     "orc_model_create": (_P, [C.c_int, C.c_int, C.c_int, C.c_uint64, C.c_int]),
     "orc_model_free": (None, [_P]),
     "orc_model_position": (C.c_uint32, [_P]),
+    "orc_threads": (C.c_int, []),
     "orc_model_fill_state": (None, [_P, C.c_uint32, C.c_uint64]),
     "orc_model_reset": (None, [_P]),
     "orc_model_forward": (C.c_int, [_P, _P, C.c_int, C.c_int, _P, _P, _P]),
@@ -90,6 +91,10 @@ def math(fn: str, x):
     out = np.empty_like(x)
     lib().orc_math(MATH[fn], p(x), x.size, p(out))
     return out
+
+
+def threads():
+    return int(lib().orc_threads())
 
 
 def argmax(v):
