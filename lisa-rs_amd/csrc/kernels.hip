@@ -75,65 +75,109 @@ DEV float hi_bf(uint32_t u) { return __uint_as_float(u & 0xffff0000u); }
 // ===========================================================================
 // q4 linear
 // ===========================================================================
-// Work split: 256 threads = 4 waves; a wave owns an 8-row tile; the 16 lanes
-// of row-group rp (lane/16) own rows (2rp, 2rp+1) of the tile (for GATEUP the
-// gate and up rows of one output), and lane li = lane%16 walks the 64-wide
-// groups g = li, li+16, ... of K. Per group and row the partial is
-//   acc_lo = fma chain x[k_even] * lo_nibble,  acc_hi = fma chain (x[k_odd]/16) * (byte & 0xf0)
-//   P = fma(scale, acc_lo + acc_hi, bias * X_g)
-// (qmv.metal:26-55 with 64-wide groups), accumulated per lane in ascending g,
-// then tree16 across the row-group (qmv.metal:71-75).
+// Arithmetic (the reference's qmv.metal:9-76 with 64-wide groups). Per
+// 64-group g of a row with nibbles q_k, scale s and bias b:
+//   acc_lo = fma chain over even k ascending of x_k * q_k
+//   acc_hi = fma chain over odd k ascending of x_k * (16 q_k)     [the odd-nibble trick, qmv.metal:30-36]
+//   P_g    = fma(s, acc_lo + acc_hi / 16, b * X_g),  X_g = sum of the group's 64 x
+// The hardware evaluates the same chains in a power-of-two scaled form: a
+// nibble field of a packed word, masked in place, read as an f16 bit pattern
+// is the subnormal q * 2^-24 (low nibble of a half) or 16q * 2^-24 (high
+// nibble), which v_fma_mix_f32 consumes directly. Scaling by 2^-24 commutes
+// with rounding in the normal range, so the chains are the oracle's chains
+// times 2^-24 exactly, and fma(s * 2^24, lo' + hi' / 16, b * X_g) equals P_g.
+// The oracle computes the same scaled form.
 //
-// x lives in LDS, one copy per input row, odd positions pre-divided by 16
-// (exact), 16-byte chunks rotated by the group index so that the 16 lanes of
-// a row-group hit distinct banks. X_g (sum of the group's 64 x values in
-// ascending order) sits after it.
+// Work split: a wave owns an 8-row tile; the 16 lanes of row-group rp = lane/16
+// own two rows (rows 2rp, 2rp+1 of the tile, or the gate and up rows of one
+// output), lane li = lane%16 walks groups g = 16i + li and sums P_g in
+// ascending i, then tree16 across the row-group (qmv.metal:71-75).
+// K = 5120: each wave owns one tile over the whole of K (4 tiles per
+// workgroup). Other K: the four waves share one tile, wave w takes group
+// iterations [ITER*w/4, ITER*(w+1)/4), and the results are combined as
+// (W0 + W1) + (W2 + W3).
+//
+// One tile per wave, no persistent loop: every wave issues the whole of its
+// weight stream at once (after the few prologue loads, so the prologue never
+// waits for weights), and the dispatcher balances the tail.
+//
+// x lives in LDS (f32, or bf16 for K = 17408), one copy per input row, in
+// 64-element groups whose 16-byte chunks are rotated by the group index so
+// the 16 lanes of a row-group read distinct banks. X_g follows it.
 
-template <int K, int M, bool XF32>
-struct QmvLds {
+template <int K, int M>
+struct QmvCfg {
   static constexpr int G = K / 64;
-  /* prologues that normalize a 5120-wide row need a staging row in LDS */
-  static constexpr bool NORM = (K == LISA_HIDDEN || K == 2 * LISA_HIDDEN);
+  static constexpr int ITER = G / 16;
+  static constexpr bool SPLIT = (K != LISA_HIDDEN);
+  static constexpr int IMAX = SPLIT ? (ITER + 3) / 4 : ITER;
+  static constexpr bool XF32 = (K != LISA_INTER);
+  static constexpr int NCH = K / 8;                 // 8-element chunks of x
+  static constexpr int RX = (NCH + 255) / 256;      // chunk rounds per thread (plain x)
+  static constexpr bool NORMK = (K == LISA_HIDDEN || K == 2 * LISA_HIDDEN);
+  static constexpr int RR = (NORMK && RX < 3) ? 3 : RX;
   static constexpr int XBYTES = M * K * (XF32 ? 4 : 2);
-  static constexpr int GBYTES = M * G * 4 + (64 + 32 * M) * 4;
-  static constexpr int TBYTES = NORM ? LISA_HIDDEN * 4 : 0;
-  static constexpr int BYTES = XBYTES + GBYTES + TBYTES;
+  static constexpr int GBYTES = M * G * 4;
+  static constexpr int RBYTES = 64 * 4;
+  static constexpr int KBYTES = 4 * 8 * M * 4;
+  static constexpr int BYTES = XBYTES + GBYTES + RBYTES + KBYTES;
+  static_assert(G % 16 == 0, "K must be a multiple of 1024");
 };
 
-template <bool XF32>
-DEV void lds_put_x(unsigned char* lds, int K, int m, int k, float v) {
-  const int g = k >> 6;
-  const float vs = (k & 1) ? v / 16.0f : v;
-  if (XF32) {
-    const int c = (k >> 2) & 15;
-    float* xs = reinterpret_cast<float*>(lds) + (size_t)m * K;
-    xs[g * 64 + 4 * ((c + g) & 15) + (k & 3)] = vs;
+// The 5120-wide segments a normalizing prologue reads: 640 chunks of 8, thread
+// t owns chunks t, t + 256, t + 512 (< 640).
+constexpr int kSegChunks = LISA_HIDDEN / 8;
+
+template <int R>
+struct ProRaw {
+  uint4 a[R], b[R], c[R], w[R];
+};
+
+DEV float h16(uint32_t bits16) {
+  return (float)__builtin_bit_cast(_Float16, (uint16_t)bits16);
+}
+// acc + x * (f16 bit pattern), one v_fma_mix_f32
+DEV float fmix_lo(float x, uint32_t p, float acc) { return __builtin_fmaf(x, h16(p & 0xffffu), acc); }
+DEV float fmix_hi(float x, uint32_t p, float acc) { return __builtin_fmaf(x, h16(p >> 16), acc); }
+
+template <int K, int M>
+DEV void put_chunk(unsigned char* lds, int m, int k0, const float (&x)[8]) {
+  const int g = k0 >> 6, j = (k0 >> 3) & 7;
+  if constexpr (QmvCfg<K, M>::XF32) {
+    float* xs = reinterpret_cast<float*>(lds) + (size_t)m * K + g * 64;
+    *reinterpret_cast<float4*>(xs + 4 * ((2 * j + g) & 15)) = make_float4(x[0], x[1], x[2], x[3]);
+    *reinterpret_cast<float4*>(xs + 4 * ((2 * j + 1 + g) & 15)) = make_float4(x[4], x[5], x[6], x[7]);
   } else {
-    const int c = (k >> 3) & 7;
-    uint16_t* xb = reinterpret_cast<uint16_t*>(lds) + (size_t)m * K;
-    xb[g * 64 + 8 * ((c + g) & 7) + (k & 7)] = lisa_f32_to_bf16(vs);
+    uint16_t* xb = reinterpret_cast<uint16_t*>(lds) + (size_t)m * K + g * 64;
+    uint4 v;
+    v.x = (__float_as_uint(x[0]) >> 16) | (__float_as_uint(x[1]) & 0xffff0000u);
+    v.y = (__float_as_uint(x[2]) >> 16) | (__float_as_uint(x[3]) & 0xffff0000u);
+    v.z = (__float_as_uint(x[4]) >> 16) | (__float_as_uint(x[5]) & 0xffff0000u);
+    v.w = (__float_as_uint(x[6]) >> 16) | (__float_as_uint(x[7]) & 0xffff0000u);
+    *reinterpret_cast<uint4*>(xb + 8 * ((j + g) & 7)) = v;
   }
 }
 
-template <bool XF32>
-DEV float lds_get_x(const unsigned char* lds, int K, int m, int k) {
-  const int g = k >> 6;
-  float vs;
-  if (XF32) {
-    const int c = (k >> 2) & 15;
-    const float* xs = reinterpret_cast<const float*>(lds) + (size_t)m * K;
-    vs = xs[g * 64 + 4 * ((c + g) & 15) + (k & 3)];
-  } else {
-    const int c = (k >> 3) & 7;
-    const uint16_t* xb = reinterpret_cast<const uint16_t*>(lds) + (size_t)m * K;
-    vs = bf2f(xb[g * 64 + 8 * ((c + g) & 7) + (k & 7)]);
-  }
-  return (k & 1) ? vs * 16.0f : vs;
+// X_g of the chunk's group: ascending-distance tree over the 64 values
+// (distances 1, 2, 4 inside the chunk, 8, 16, 32 across the 8 lanes that hold
+// the group's chunks). Every lane calls it; lane c%8 == 0 stores.
+template <int K, int M>
+DEV void put_gsum(float* gsum, int m, int k0, bool valid, const float (&x)[8]) {
+  float s = ((x[0] + x[1]) + (x[2] + x[3])) + ((x[4] + x[5]) + (x[6] + x[7]));
+  s = s + xor_lane<1>(s);
+  s = s + xor_lane<2>(s);
+  s = s + xor_lane<4>(s);
+  if (valid && ((k0 >> 3) & 7) == 0) gsum[m * QmvCfg<K, M>::G + (k0 >> 6)] = s;
 }
 
-// RMSNorm statistic of one 5120-wide row given each thread's partial sum of
-// squares over its elements j = tid + 256 i: rows-of-256 tree (norm.metal:10-47).
-DEV float rms_inv_5120(float s, float* red, int tid) {
+DEV void unpack_bf8(const uint4& u, float (&v)[8]) {
+  v[0] = lo_bf(u.x); v[1] = hi_bf(u.x); v[2] = lo_bf(u.y); v[3] = hi_bf(u.y);
+  v[4] = lo_bf(u.z); v[5] = hi_bf(u.z); v[6] = lo_bf(u.w); v[7] = hi_bf(u.w);
+}
+
+// RMSNorm statistic of one 5120-wide segment from each thread's partial sum of
+// squares: tree64 per wave, then (W0 + W1) + (W2 + W3).
+DEV float seg_rms_inv(float s, float* red, int tid) {
   s = tree64(s);
   __syncthreads();
   if ((tid & 63) == 0) red[tid >> 6] = s;
@@ -142,145 +186,164 @@ DEV float rms_inv_5120(float s, float* red, int tid) {
   return lisa_rsqrt(tot / (float)LISA_HIDDEN + LISA_EPS);
 }
 
-DEV float embed_value(const uint32_t* ew, const uint32_t* esb, uint32_t tok, int j) {
-  const uint32_t word = ew[(size_t)tok * (LISA_HIDDEN / 8) + (j >> 3)];
-  const uint32_t q = (word >> ((j & 7) * 4)) & 0xfu;
-  const uint32_t sb = esb[(size_t)tok * (LISA_HIDDEN / 64) + (j >> 6)];
-  // embed.metal:24-26: float(q) * scale + bias, stored bf16
-  return lisa_bf16r((float)q * lo_bf(sb) + hi_bf(sb));
+// Sources of a normalized segment (pro_mode, or the two halves of MTPFC).
+enum SegSrc { SEG_RESNORM, SEG_EMBED, SEG_CAST, SEG_NORM };
+
+template <int MODE>
+DEV constexpr int seg_source(int seg) {
+  return MODE == LISA_PRO_RESNORM ? SEG_RESNORM
+         : MODE == LISA_PRO_EMBED ? SEG_EMBED
+         : MODE == LISA_PRO_CAST  ? SEG_CAST
+         : MODE == LISA_PRO_NORM  ? SEG_NORM
+         : (seg == 0 ? SEG_EMBED : SEG_NORM); /* MTPFC */
 }
 
-// Fill LDS with x (and X_g) for all M rows according to the prologue mode.
-template <int K, int M, bool XF32>
-DEV void qmv_prologue(const LisaQmvParams& p, unsigned char* lds) {
-  constexpr int G = K / 64;
+// Raw loads of segment `seg` of input row m.
+template <int MODE, int SEG, int R>
+DEV void seg_load(const LisaQmvParams& p, int m, ProRaw<R>& raw) {
   const int tid = threadIdx.x;
-  float* gsum = reinterpret_cast<float*>(lds + QmvLds<K, M, XF32>::XBYTES);
-  float* red = gsum + M * G;
-  const bool writer = blockIdx.x == 0;
-  if (p.pro_mode == LISA_PRO_LOADX) {
-    for (int m = 0; m < M; ++m)
-      for (int k8 = tid; k8 < K / 8; k8 += 256) {
-        const uint4 v = *reinterpret_cast<const uint4*>(p.x_in + (size_t)m * K + 8 * k8);
-        const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+  constexpr int src = seg_source<MODE>(SEG);
+  const uint16_t* nw = SEG == 0 ? p.norm_w : p.norm_w2;
+  const uint16_t* hsrc = (MODE == LISA_PRO_MTPFC) ? p.x_in : p.h_in + (size_t)m * LISA_HIDDEN;
+  const float* osrc = p.o_in + (size_t)m * LISA_HIDDEN;
+  uint32_t tok = 0;
+  if constexpr (src == SEG_EMBED) tok = p.tokens[MODE == LISA_PRO_MTPFC ? 0 : m];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          lds_put_x<XF32>(lds, K, m, 8 * k8 + 2 * e, lo_bf(w[e]));
-          lds_put_x<XF32>(lds, K, m, 8 * k8 + 2 * e + 1, hi_bf(w[e]));
-        }
+  for (int i = 0; i < 3; ++i) {
+    const int c = min(tid + 256 * i, kSegChunks - 1);
+    raw.w[i] = reinterpret_cast<const uint4*>(nw)[c];
+    if constexpr (src == SEG_RESNORM || src == SEG_NORM) raw.a[i] = reinterpret_cast<const uint4*>(hsrc)[c];
+    if constexpr (src == SEG_RESNORM || src == SEG_CAST) {
+      raw.b[i] = reinterpret_cast<const uint4*>(osrc)[2 * c];
+      raw.c[i] = reinterpret_cast<const uint4*>(osrc)[2 * c + 1];
+    }
+    if constexpr (src == SEG_EMBED) {
+      raw.a[i].x = p.emb_w[(size_t)tok * (LISA_HIDDEN / 8) + c];
+      raw.a[i].y = p.emb_sb[(size_t)tok * (LISA_HIDDEN / 64) + (c >> 3)];
+    }
+  }
+}
+
+// Decode, normalize and stage one 5120-wide segment (norm.metal:10-47; the
+// residual add of the residual encoders; embed.metal:24-26).
+template <int K, int M, int MODE, int SEG, int R>
+DEV void seg_process(const LisaQmvParams& p, unsigned char* lds, int m, const ProRaw<R>& raw) {
+  using C = QmvCfg<K, M>;
+  const int tid = threadIdx.x;
+  float* gsum = reinterpret_cast<float*>(lds + C::XBYTES);
+  float* red = gsum + M * C::G;
+  constexpr int src = seg_source<MODE>(SEG);
+  float v[3][8];
+  float ss = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 3; ++i) {
+    const bool valid = tid + 256 * i < kSegChunks;
+    float hv[8] = {}, ov[8] = {};
+    if constexpr (src == SEG_RESNORM || src == SEG_NORM) unpack_bf8(raw.a[i], hv);
+    if constexpr (src == SEG_RESNORM || src == SEG_CAST) {
+      ov[0] = __uint_as_float(raw.b[i].x); ov[1] = __uint_as_float(raw.b[i].y);
+      ov[2] = __uint_as_float(raw.b[i].z); ov[3] = __uint_as_float(raw.b[i].w);
+      ov[4] = __uint_as_float(raw.c[i].x); ov[5] = __uint_as_float(raw.c[i].y);
+      ov[6] = __uint_as_float(raw.c[i].z); ov[7] = __uint_as_float(raw.c[i].w);
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      float r;
+      if constexpr (src == SEG_RESNORM) r = lisa_bf16r(hv[e] + lisa_bf16r(ov[e]));
+      else if constexpr (src == SEG_CAST) r = lisa_bf16r(ov[e]);
+      else if constexpr (src == SEG_NORM) r = hv[e];
+      else r = lisa_bf16r((float)((raw.a[i].x >> (4 * e)) & 0xfu) * lo_bf(raw.a[i].y) + hi_bf(raw.a[i].y));
+      v[i][e] = r;
+      if (valid) ss = ss + r * r;
+    }
+  }
+  const float inv = seg_rms_inv(ss, red, tid);
+  const bool writer = blockIdx.x == 0;
+#pragma unroll
+  for (int i = 0; i < 3; ++i) {
+    const int c = tid + 256 * i;
+    const bool valid = c < kSegChunks;
+    float wv[8], x[8];
+    unpack_bf8(raw.w[i], wv);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) x[e] = lisa_bf16r((v[i][e] * inv) * wv[e]);
+    const int k0 = SEG * LISA_HIDDEN + 8 * c;
+    if (valid) put_chunk<K, M>(lds, m, k0, x);
+    put_gsum<K, M>(gsum, m, k0, valid, x);
+    if (valid && writer) {
+      if (MODE != LISA_PRO_MTPFC && p.r_out) {
+        uint4 o;
+        o.x = (__float_as_uint(v[i][0]) >> 16) | (__float_as_uint(v[i][1]) & 0xffff0000u);
+        o.y = (__float_as_uint(v[i][2]) >> 16) | (__float_as_uint(v[i][3]) & 0xffff0000u);
+        o.z = (__float_as_uint(v[i][4]) >> 16) | (__float_as_uint(v[i][5]) & 0xffff0000u);
+        o.w = (__float_as_uint(v[i][6]) >> 16) | (__float_as_uint(v[i][7]) & 0xffff0000u);
+        reinterpret_cast<uint4*>(p.r_out + (size_t)m * LISA_HIDDEN)[c] = o;
       }
-  } else if constexpr (QmvLds<K, M, XF32>::NORM) {
-    float* tmp = reinterpret_cast<float*>(lds + QmvLds<K, M, XF32>::XBYTES + QmvLds<K, M, XF32>::GBYTES);
-    const int halves = (p.pro_mode == LISA_PRO_MTPFC) ? 2 : 1;
-    for (int m = 0; m < M; ++m) {
-      for (int hf = 0; hf < halves; ++hf) {
-        float ss = 0.0f;
-#pragma unroll 4
-        for (int i = 0; i < LISA_HIDDEN / 256; ++i) {
-          const int j = tid + 256 * i;
-          const size_t off = (size_t)m * LISA_HIDDEN + j;
-          float v;
-          switch (p.pro_mode) {
-            case LISA_PRO_RESNORM: v = lisa_bf16r(bf2f(p.h_in[off]) + lisa_bf16r(p.o_in[off])); break;
-            case LISA_PRO_EMBED: v = embed_value(p.emb_w, p.emb_sb, p.tokens[m], j); break;
-            case LISA_PRO_CAST: v = lisa_bf16r(p.o_in[off]); break;
-            case LISA_PRO_NORM: v = bf2f(p.h_in[off]); break;
-            default: /* MTPFC */
-              v = (hf == 0) ? embed_value(p.emb_w, p.emb_sb, p.tokens[0], j) : bf2f(p.x_in[j]);
-              break;
-          }
-          tmp[j] = v;
-          ss = ss + v * v;
-        }
-        const float inv = rms_inv_5120(ss, red, tid);
-        const uint16_t* nw = (hf == 0) ? p.norm_w : p.norm_w2;
-#pragma unroll 4
-        for (int i = 0; i < LISA_HIDDEN / 256; ++i) {
-          const int j = tid + 256 * i;
-          const float r = tmp[j];
-          const float x = lisa_bf16r((r * inv) * bf2f(nw[j]));
-          lds_put_x<XF32>(lds, K, m, hf * LISA_HIDDEN + j, x);
-          if (writer) {
-            if (p.r_out && p.pro_mode != LISA_PRO_MTPFC)
-              p.r_out[(size_t)m * LISA_HIDDEN + j] = lisa_f32_to_bf16(r);
-            if (p.x_out) p.x_out[(size_t)m * K + hf * LISA_HIDDEN + j] = lisa_f32_to_bf16(x);
-          }
-        }
-        __syncthreads();
+      if (p.x_out) {
+        uint4 o;
+        o.x = (__float_as_uint(x[0]) >> 16) | (__float_as_uint(x[1]) & 0xffff0000u);
+        o.y = (__float_as_uint(x[2]) >> 16) | (__float_as_uint(x[3]) & 0xffff0000u);
+        o.z = (__float_as_uint(x[4]) >> 16) | (__float_as_uint(x[5]) & 0xffff0000u);
+        o.w = (__float_as_uint(x[6]) >> 16) | (__float_as_uint(x[7]) & 0xffff0000u);
+        reinterpret_cast<uint4*>(p.x_out + (size_t)m * K + SEG * LISA_HIDDEN)[c] = o;
       }
     }
   }
-  __syncthreads();
-  for (int m = 0; m < M; ++m)
-    for (int g = tid; g < G; g += 256) {
-      float s = 0.0f;
-      for (int k = 0; k < 64; ++k) s = s + lds_get_x<XF32>(lds, K, m, 64 * g + k);
-      gsum[m * G + g] = s;
-    }
-  __syncthreads();
 }
 
-// One group's dot for the two weight rows of a lane and M input rows. The
-// x values of a 4-element chunk are loaded once and used by both rows.
-template <int K, int M, bool XF32>
-DEV void group_dot2(const unsigned char* lds, int g, const uint32_t (&w0)[8], const uint32_t (&w1)[8],
-                    uint32_t sb0, uint32_t sb1, const float* gsum, float* T0, float* T1) {
-  constexpr int G = K / 64;
-  float lo0[M], hi0[M], lo1[M], hi1[M];
+// Plain x (LOADX): raw loads and staging of input row m.
+template <int K, int M, int R>
+DEV void x_load(const LisaQmvParams& p, int m, ProRaw<R>& raw) {
+  using C = QmvCfg<K, M>;
+  const uint4* src = reinterpret_cast<const uint4*>(p.x_in + (size_t)m * K);
 #pragma unroll
-  for (int m = 0; m < M; ++m) { lo0[m] = 0.0f; hi0[m] = 0.0f; lo1[m] = 0.0f; hi1[m] = 0.0f; }
-  if constexpr (XF32) {
-    const float* xs = reinterpret_cast<const float*>(lds) + g * 64;
-#pragma unroll 4
-    for (int c = 0; c < 16; ++c) {
-      const int sh = 16 * (c & 1);
-      const uint32_t ml0 = w0[c >> 1] & 0x0f0f0f0fu, mh0 = w0[c >> 1] & 0xf0f0f0f0u;
-      const uint32_t ml1 = w1[c >> 1] & 0x0f0f0f0fu, mh1 = w1[c >> 1] & 0xf0f0f0f0u;
-      const float a0 = (float)((ml0 >> sh) & 0xffu), b0 = (float)((mh0 >> sh) & 0xffu);
-      const float a1 = (float)((ml0 >> (sh + 8)) & 0xffu), b1 = (float)((mh0 >> (sh + 8)) & 0xffu);
-      const float c0 = (float)((ml1 >> sh) & 0xffu), d0 = (float)((mh1 >> sh) & 0xffu);
-      const float c1 = (float)((ml1 >> (sh + 8)) & 0xffu), d1 = (float)((mh1 >> (sh + 8)) & 0xffu);
+  for (int i = 0; i < C::RX; ++i) raw.a[i] = src[min((int)threadIdx.x + 256 * i, C::NCH - 1)];
+}
+
+template <int K, int M, int R>
+DEV void x_process(unsigned char* lds, int m, const ProRaw<R>& raw) {
+  using C = QmvCfg<K, M>;
+  float* gsum = reinterpret_cast<float*>(lds + C::XBYTES);
 #pragma unroll
-      for (int m = 0; m < M; ++m) {
-        const float4 x4 = *reinterpret_cast<const float4*>(xs + (size_t)m * K + 4 * ((c + g) & 15));
-        lo0[m] = lisa_fma(x4.x, a0, lo0[m]);
-        hi0[m] = lisa_fma(x4.y, b0, hi0[m]);
-        lo0[m] = lisa_fma(x4.z, a1, lo0[m]);
-        hi0[m] = lisa_fma(x4.w, b1, hi0[m]);
-        lo1[m] = lisa_fma(x4.x, c0, lo1[m]);
-        hi1[m] = lisa_fma(x4.y, d0, hi1[m]);
-        lo1[m] = lisa_fma(x4.z, c1, lo1[m]);
-        hi1[m] = lisa_fma(x4.w, d1, hi1[m]);
+  for (int i = 0; i < C::RX; ++i) {
+    const int c = threadIdx.x + 256 * i;
+    const bool valid = c < C::NCH;
+    float x[8];
+    unpack_bf8(raw.a[i], x);
+    if (valid) put_chunk<K, M>(lds, m, 8 * c, x);
+    put_gsum<K, M>(gsum, m, 8 * c, valid, x);
+  }
+}
+
+template <int K, int M, int MODE, int R>
+DEV void pro_load(const LisaQmvParams& p, int m, ProRaw<R>& raw) {
+  if constexpr (MODE == LISA_PRO_LOADX) x_load<K, M, R>(p, m, raw);
+  else seg_load<MODE, 0, R>(p, m, raw);
+}
+
+// Stage x and X_g of all M rows. Row 0's first segment was loaded by the
+// caller (before the weight stream); the rest is loaded here.
+template <int K, int M, int MODE, int R>
+DEV void qmv_prologue(const LisaQmvParams& p, unsigned char* lds, ProRaw<R>& raw) {
+  if constexpr (MODE != LISA_PRO_LOADX) {
+    static_assert(K == LISA_HIDDEN * (MODE == LISA_PRO_MTPFC ? 2 : 1), "normalizing prologue of the wrong width");
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+      if (m > 0) seg_load<MODE, 0, R>(p, m, raw);
+      seg_process<K, M, MODE, 0, R>(p, lds, m, raw);
+      if constexpr (MODE == LISA_PRO_MTPFC) {
+        seg_load<MODE, 1, R>(p, m, raw);
+        seg_process<K, M, MODE, 1, R>(p, lds, m, raw);
       }
     }
   } else {
-    const uint16_t* xb = reinterpret_cast<const uint16_t*>(lds) + g * 64;
-#pragma unroll 2
-    for (int c = 0; c < 8; ++c) {
-      const uint32_t ml0 = w0[c] & 0x0f0f0f0fu, mh0 = w0[c] & 0xf0f0f0f0u;
-      const uint32_t ml1 = w1[c] & 0x0f0f0f0fu, mh1 = w1[c] & 0xf0f0f0f0u;
 #pragma unroll
-      for (int m = 0; m < M; ++m) {
-        const uint4 xv = *reinterpret_cast<const uint4*>(xb + (size_t)m * K + 8 * ((c + g) & 7));
-        const uint32_t xw[4] = {xv.x, xv.y, xv.z, xv.w};
-#pragma unroll
-        for (int b = 0; b < 4; ++b) {
-          const float xe = lo_bf(xw[b]), xo = hi_bf(xw[b]);
-          lo0[m] = lisa_fma(xe, (float)((ml0 >> (8 * b)) & 0xffu), lo0[m]);
-          hi0[m] = lisa_fma(xo, (float)((mh0 >> (8 * b)) & 0xffu), hi0[m]);
-          lo1[m] = lisa_fma(xe, (float)((ml1 >> (8 * b)) & 0xffu), lo1[m]);
-          hi1[m] = lisa_fma(xo, (float)((mh1 >> (8 * b)) & 0xffu), hi1[m]);
-        }
-      }
+    for (int m = 0; m < M; ++m) {
+      if (m > 0) x_load<K, M, R>(p, m, raw);
+      x_process<K, M, R>(lds, m, raw);
     }
   }
-  const float s0 = lo_bf(sb0), bb0 = hi_bf(sb0), s1 = lo_bf(sb1), bb1 = hi_bf(sb1);
-#pragma unroll
-  for (int m = 0; m < M; ++m) {
-    const float xg = gsum[m * G + g];
-    T0[m] = T0[m] + lisa_fma(s0, lo0[m] + hi0[m], bb0 * xg);
-    T1[m] = T1[m] + lisa_fma(s1, lo1[m] + hi1[m], bb1 * xg);
-  }
+  __syncthreads();
 }
 
 template <int M>
@@ -315,100 +378,195 @@ DEV bool better(float v, uint32_t i, float bv, uint32_t bi) {
   return (v > bv) || (v == bv && i < bi);
 }
 
-template <int K, int M, bool XF32>
-DEV void qmv_body(const LisaQmvParams& p, unsigned char* lds) {
-  constexpr int G = K / 64;
-  constexpr int ITER = G / 16;
-  static_assert(G % 16 == 0, "K must be a multiple of 1024");
-  qmv_prologue<K, M, XF32>(p, lds);
-  const float* gsum = reinterpret_cast<const float*>(lds + QmvLds<K, M, XF32>::XBYTES);
-  float* red = const_cast<float*>(gsum) + M * G;
+// The weights of a wave's group iterations for the two rows of a lane.
+template <int IMAX>
+struct Unit {
+  uint4 a0[IMAX], b0[IMAX], a1[IMAX], b1[IMAX];
+  uint32_t s0[IMAX], s1[IMAX];
+};
 
-  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+struct TileRef {
+  int e;
+  uint32_t r0, r1;
+  bool v0, v1;
+  const uint4 *wp0, *wp1;
+  const uint32_t *sp0, *sp1;
+};
+
+template <int K>
+DEV TileRef tile_ref(const LisaQmvParams& p, uint32_t tile, int rp) {
+  constexpr int G = K / 64;
+  TileRef t;
+  int e = 0;
+  while (e + 1 < (int)p.n_mats && tile >= p.tile_start[e + 1]) ++e;
+  t.e = e;
+  const uint32_t lt = tile - p.tile_start[e];
+  const uint32_t rows = p.mats[e].rows;
+  const uint32_t *w0, *w1, *s0, *s1;
+  if (p.mats[e].kind == LISA_EPI_GATEUP) {
+    t.r0 = t.r1 = lt * 4 + rp;
+    w0 = p.mats[e].w; s0 = p.mats[e].sb; w1 = p.mats[e].w2; s1 = p.mats[e].sb2;
+  } else {
+    t.r0 = lt * 8 + 2 * rp;
+    t.r1 = t.r0 + 1;
+    w0 = w1 = p.mats[e].w; s0 = s1 = p.mats[e].sb;
+  }
+  t.v0 = t.r0 < rows;
+  t.v1 = t.r1 < rows;
+  const uint32_t c0 = t.v0 ? t.r0 : rows - 1, c1 = t.v1 ? t.r1 : rows - 1;
+  t.wp0 = reinterpret_cast<const uint4*>(w0 + (size_t)c0 * (K / 8));
+  t.wp1 = reinterpret_cast<const uint4*>(w1 + (size_t)c1 * (K / 8));
+  t.sp0 = s0 + (size_t)c0 * G;
+  t.sp1 = s1 + (size_t)c1 * G;
+  return t;
+}
+
+// Every load is unconditional (iterations past the wave's range re-read its
+// last one) so the loads of a wave form one straight run.
+template <int K, int IMAX>
+DEV void load_unit(Unit<IMAX>& u, const TileRef& t, int it0, int it1, int li) {
+#pragma unroll
+  for (int i = 0; i < IMAX; ++i) {
+    const int ii = max(min(it0 + i, it1 - 1), 0);
+    const int g = 16 * ii + li;
+    u.a0[i] = t.wp0[2 * g];
+    u.b0[i] = t.wp0[2 * g + 1];
+    u.a1[i] = t.wp1[2 * g];
+    u.b1[i] = t.wp1[2 * g + 1];
+    u.s0[i] = t.sp0[g];
+    u.s1[i] = t.sp1[g];
+  }
+}
+
+// One group of the lane's two rows against the M staged x rows.
+template <int K, int M>
+DEV void group_dot2(const unsigned char* lds, int g, const uint4& a0, const uint4& b0, const uint4& a1,
+                    const uint4& b1, uint32_t sb0, uint32_t sb1, const float* gsum, float (&T0)[M],
+                    float (&T1)[M]) {
+  using C = QmvCfg<K, M>;
+  const uint32_t w0[8] = {a0.x, a0.y, a0.z, a0.w, b0.x, b0.y, b0.z, b0.w};
+  const uint32_t w1[8] = {a1.x, a1.y, a1.z, a1.w, b1.x, b1.y, b1.z, b1.w};
+  float lo0[M], hi0[M], lo1[M], hi1[M];
+#pragma unroll
+  for (int m = 0; m < M; ++m) { lo0[m] = 0.0f; hi0[m] = 0.0f; lo1[m] = 0.0f; hi1[m] = 0.0f; }
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    // nibble fields in place: e0|e4, e1|e5 (x16), e2|e6, e3|e7 (x16)
+    const uint32_t p0 = w0[j] & 0x000f000fu, p1 = w0[j] & 0x00f000f0u, t0 = w0[j] >> 8;
+    const uint32_t p2 = t0 & 0x000f000fu, p3 = t0 & 0x00f000f0u;
+    const uint32_t q0 = w1[j] & 0x000f000fu, q1 = w1[j] & 0x00f000f0u, t1 = w1[j] >> 8;
+    const uint32_t q2 = t1 & 0x000f000fu, q3 = t1 & 0x00f000f0u;
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+      float x[8];
+      if constexpr (C::XF32) {
+        const float* xs = reinterpret_cast<const float*>(lds) + (size_t)m * K + g * 64;
+        const float4 xa = *reinterpret_cast<const float4*>(xs + 4 * ((2 * j + g) & 15));
+        const float4 xb = *reinterpret_cast<const float4*>(xs + 4 * ((2 * j + 1 + g) & 15));
+        x[0] = xa.x; x[1] = xa.y; x[2] = xa.z; x[3] = xa.w;
+        x[4] = xb.x; x[5] = xb.y; x[6] = xb.z; x[7] = xb.w;
+      } else {
+        const uint16_t* xb = reinterpret_cast<const uint16_t*>(lds) + (size_t)m * K + g * 64;
+        unpack_bf8(*reinterpret_cast<const uint4*>(xb + 8 * ((j + g) & 7)), x);
+      }
+      lo0[m] = fmix_lo(x[0], p0, lo0[m]);
+      lo0[m] = fmix_lo(x[2], p2, lo0[m]);
+      lo0[m] = fmix_hi(x[4], p0, lo0[m]);
+      lo0[m] = fmix_hi(x[6], p2, lo0[m]);
+      hi0[m] = fmix_lo(x[1], p1, hi0[m]);
+      hi0[m] = fmix_lo(x[3], p3, hi0[m]);
+      hi0[m] = fmix_hi(x[5], p1, hi0[m]);
+      hi0[m] = fmix_hi(x[7], p3, hi0[m]);
+      lo1[m] = fmix_lo(x[0], q0, lo1[m]);
+      lo1[m] = fmix_lo(x[2], q2, lo1[m]);
+      lo1[m] = fmix_hi(x[4], q0, lo1[m]);
+      lo1[m] = fmix_hi(x[6], q2, lo1[m]);
+      hi1[m] = fmix_lo(x[1], q1, hi1[m]);
+      hi1[m] = fmix_lo(x[3], q3, hi1[m]);
+      hi1[m] = fmix_hi(x[5], q1, hi1[m]);
+      hi1[m] = fmix_hi(x[7], q3, hi1[m]);
+    }
+  }
+  const float s0 = lo_bf(sb0) * 16777216.0f, bb0 = hi_bf(sb0);
+  const float s1 = lo_bf(sb1) * 16777216.0f, bb1 = hi_bf(sb1);
+#pragma unroll
+  for (int m = 0; m < M; ++m) {
+    const float xg = gsum[m * C::G + g];
+    T0[m] = T0[m] + lisa_fma(s0, lo0[m] + hi0[m] * 0.0625f, bb0 * xg);
+    T1[m] = T1[m] + lisa_fma(s1, lo1[m] + hi1[m] * 0.0625f, bb1 * xg);
+  }
+}
+
+template <int K, int M, int MODE>
+DEV void qmv_body(const LisaQmvParams& p, unsigned char* lds) {
+  using C = QmvCfg<K, M>;
+  const float* gsum = reinterpret_cast<const float*>(lds + C::XBYTES);
+  float* red = const_cast<float*>(gsum) + M * C::G;
+  float* kred = red + 64;  // [4 waves][8 rows][M]
+
+  // wv is wave-uniform: keeping it scalar keeps the matrix lookup on scalar loads
+  const int tid = threadIdx.x, lane = tid & 63, wv = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int li = lane & 15, rp = lane >> 4;
   const uint32_t tiles = p.tile_start[p.n_mats];
+  const uint32_t tile = C::SPLIT ? blockIdx.x : blockIdx.x * 4 + wv;
+  const bool tile_ok = tile < tiles;
+  const int it0 = C::SPLIT ? (C::ITER * wv) / 4 : 0;
+  const int it1 = C::SPLIT ? (C::ITER * (wv + 1)) / 4 : C::ITER;
+  const TileRef tr = tile_ref<K>(p, tile_ok ? tile : tiles - 1, rp);
+
+  ProRaw<C::RR> raw;
+  // issue order: prologue loads, then the weight stream (the fences keep the
+  // scheduler from interleaving them, so the prologue waits only for its own)
+  pro_load<K, M, MODE, C::RR>(p, 0, raw);
+  __builtin_amdgcn_sched_barrier(0);
+  Unit<C::IMAX> u;
+  load_unit<K, C::IMAX>(u, tr, it0, it1, li);
+  __builtin_amdgcn_sched_barrier(0);
+  qmv_prologue<K, M, MODE, C::RR>(p, lds, raw);
+
+  float T0[M], T1[M];
+#pragma unroll
+  for (int m = 0; m < M; ++m) { T0[m] = 0.0f; T1[m] = 0.0f; }
+#pragma unroll
+  for (int i = 0; i < C::IMAX; ++i)
+    if (it0 + i < it1)
+      group_dot2<K, M>(lds, 16 * (it0 + i) + li, u.a0[i], u.b0[i], u.a1[i], u.b1[i], u.s0[i], u.s1[i], gsum, T0,
+                       T1);
+#pragma unroll
+  for (int m = 0; m < M; ++m) { T0[m] = tree16(T0[m]); T1[m] = tree16(T1[m]); }
+
+  bool active = tile_ok;
+  if constexpr (C::SPLIT) {
+    if (li == 0) {
+#pragma unroll
+      for (int m = 0; m < M; ++m) {
+        kred[(wv * 8 + 2 * rp) * M + m] = T0[m];
+        kred[(wv * 8 + 2 * rp + 1) * M + m] = T1[m];
+      }
+    }
+    __syncthreads();
+    if (wv == 0) {
+#pragma unroll
+      for (int m = 0; m < M; ++m) {
+        const int a = 2 * rp, b = 2 * rp + 1;
+        T0[m] = (kred[(0 * 8 + a) * M + m] + kred[(1 * 8 + a) * M + m]) +
+                (kred[(2 * 8 + a) * M + m] + kred[(3 * 8 + a) * M + m]);
+        T1[m] = (kred[(0 * 8 + b) * M + m] + kred[(1 * 8 + b) * M + m]) +
+                (kred[(2 * 8 + b) * M + m] + kred[(3 * 8 + b) * M + m]);
+      }
+    }
+    active = active && wv == 0;
+  }
+
   float best_v[M];
   uint32_t best_i[M];
 #pragma unroll
   for (int m = 0; m < M; ++m) { best_v[m] = -INFINITY; best_i[m] = 0xffffffffu; }
 
-  // ksplit == 1: each wave owns its own 8-row tile over the whole of K.
-  // ksplit == 4: the four waves share one 8-row tile; wave w walks the group
-  // iterations [ITER*w/4, ITER*(w+1)/4) and the wave results are combined as
-  // (W0 + W1) + (W2 + W3) by wave 0.
-  const bool split = p.ksplit == 4;
-  const uint32_t tstep = split ? gridDim.x : gridDim.x * 4;
-  const int it0 = split ? (ITER * wv) / 4 : 0, it1 = split ? (ITER * (wv + 1)) / 4 : ITER;
-  float* kred = red + 64;  // [4 waves][8 rows][M]
-  for (uint32_t tile = split ? blockIdx.x : blockIdx.x * 4 + wv; tile < tiles; tile += tstep) {
-    int e = 0;
-    while (e + 1 < (int)p.n_mats && tile >= p.tile_start[e + 1]) ++e;
-    const LisaQ4Mat mt = p.mats[e];
-    const uint32_t lt = tile - p.tile_start[e];
-    uint32_t r0, r1;
-    const uint32_t *w0, *w1, *s0, *s1;
-    if (mt.kind == LISA_EPI_GATEUP) {
-      r0 = r1 = lt * 4 + rp;
-      w0 = mt.w; s0 = mt.sb; w1 = mt.w2; s1 = mt.sb2;
-    } else {
-      r0 = lt * 8 + 2 * rp;
-      r1 = r0 + 1;
-      w0 = w1 = mt.w; s0 = s1 = mt.sb;
-    }
-    const bool v0 = r0 < mt.rows, v1 = r1 < mt.rows;
-    const uint32_t c0 = v0 ? r0 : mt.rows - 1, c1 = v1 ? r1 : mt.rows - 1;
-    const uint4* wp0 = reinterpret_cast<const uint4*>(w0 + (size_t)c0 * (K / 8));
-    const uint4* wp1 = reinterpret_cast<const uint4*>(w1 + (size_t)c1 * (K / 8));
-    const uint32_t* sp0 = s0 + (size_t)c0 * G;
-    const uint32_t* sp1 = s1 + (size_t)c1 * G;
-
-    float T0[M], T1[M];
-#pragma unroll
-    for (int m = 0; m < M; ++m) { T0[m] = 0.0f; T1[m] = 0.0f; }
-
-    if (it0 < it1) {
-      const int gf = 16 * it0 + li;
-      uint4 na0 = wp0[2 * gf], nb0 = wp0[2 * gf + 1], na1 = wp1[2 * gf], nb1 = wp1[2 * gf + 1];
-      uint32_t ns0 = sp0[gf], ns1 = sp1[gf];
-      for (int it = it0; it < it1; ++it) {
-        const int g = 16 * it + li;
-        const uint32_t cw0[8] = {na0.x, na0.y, na0.z, na0.w, nb0.x, nb0.y, nb0.z, nb0.w};
-        const uint32_t cw1[8] = {na1.x, na1.y, na1.z, na1.w, nb1.x, nb1.y, nb1.z, nb1.w};
-        const uint32_t q0 = ns0, q1 = ns1;
-        if (it + 1 < it1) {
-          const int gn = g + 16;
-          na0 = wp0[2 * gn]; nb0 = wp0[2 * gn + 1];
-          na1 = wp1[2 * gn]; nb1 = wp1[2 * gn + 1];
-          ns0 = sp0[gn]; ns1 = sp1[gn];
-        }
-        group_dot2<K, M, XF32>(lds, g, cw0, cw1, q0, q1, gsum, T0, T1);
-      }
-    }
-#pragma unroll
-    for (int m = 0; m < M; ++m) { T0[m] = tree16(T0[m]); T1[m] = tree16(T1[m]); }
-    if (split) {
-      if (li == 0) {
-#pragma unroll
-        for (int m = 0; m < M; ++m) {
-          kred[(wv * 8 + 2 * rp) * M + m] = T0[m];
-          kred[(wv * 8 + 2 * rp + 1) * M + m] = T1[m];
-        }
-      }
-      __syncthreads();
-      if (wv == 0) {
-#pragma unroll
-        for (int m = 0; m < M; ++m) {
-          const int a = 2 * rp, b = 2 * rp + 1;
-          T0[m] = (kred[(0 * 8 + a) * M + m] + kred[(1 * 8 + a) * M + m]) +
-                  (kred[(2 * 8 + a) * M + m] + kred[(3 * 8 + a) * M + m]);
-          T1[m] = (kred[(0 * 8 + b) * M + m] + kred[(1 * 8 + b) * M + m]) +
-                  (kred[(2 * 8 + b) * M + m] + kred[(3 * 8 + b) * M + m]);
-        }
-      }
-      __syncthreads();
-      if (wv != 0) continue;
-    }
-
+  if (active) {
+    const LisaQ4Mat& mt = p.mats[tr.e];
+    const uint32_t r0 = tr.r0, r1 = tr.r1;
+    const bool v0 = tr.v0, v1 = tr.v1;
     switch (mt.kind) {
       case LISA_EPI_STORE: {
         float* out = static_cast<float*>(mt.out);
@@ -439,13 +597,11 @@ DEV void qmv_body(const LisaQmvParams& p, unsigned char* lds) {
         float* out = static_cast<float*>(mt.out);
 #pragma unroll
         for (int m = 0; m < M; ++m) {
-          if (li == 2 * m && v0) {
-            out[(size_t)m * mt.rows + r0] = T0[m];
-            if (better(T0[m], r0, best_v[m], best_i[m])) { best_v[m] = T0[m]; best_i[m] = r0; }
-          }
-          if (li == 2 * m + 1 && v1) {
-            out[(size_t)m * mt.rows + r1] = T1[m];
-            if (better(T1[m], r1, best_v[m], best_i[m])) { best_v[m] = T1[m]; best_i[m] = r1; }
+          if (li == 2 * m && v0) out[(size_t)m * mt.rows + r0] = T0[m];
+          if (li == 2 * m + 1 && v1) out[(size_t)m * mt.rows + r1] = T1[m];
+          if (li == 0) {
+            if (v0 && better(T0[m], r0, best_v[m], best_i[m])) { best_v[m] = T0[m]; best_i[m] = r0; }
+            if (v1 && better(T1[m], r1, best_v[m], best_i[m])) { best_v[m] = T1[m]; best_i[m] = r1; }
           }
         }
         break;
@@ -454,14 +610,14 @@ DEV void qmv_body(const LisaQmvParams& p, unsigned char* lds) {
   }
 
   if (p.am_val) {
-    // workgroup-level (max, lowest index) per input row
+    // workgroup (max, lowest index) per input row
     __syncthreads();
-    float* cv = red;  // reuse: [M][256] would not fit; reduce per m sequentially
+    float* cv = red;
     uint32_t* ci = reinterpret_cast<uint32_t*>(red + 32);
+#pragma unroll
     for (int m = 0; m < M; ++m) {
       float v = best_v[m];
       uint32_t i = best_i[m];
-      // wave reduction
 #pragma unroll
       for (int msk = 1; msk < 64; msk <<= 1) {
         const float ov = __shfl_xor(v, msk, 64);
@@ -470,7 +626,7 @@ DEV void qmv_body(const LisaQmvParams& p, unsigned char* lds) {
       }
       if (lane == 0) { cv[wv] = v; ci[wv] = i; }
       __syncthreads();
-      if (threadIdx.x == 0) {
+      if (tid == 0) {
         float bv = cv[0];
         uint32_t bi = ci[0];
         for (int q = 1; q < 4; ++q)
@@ -483,21 +639,30 @@ DEV void qmv_body(const LisaQmvParams& p, unsigned char* lds) {
   }
 }
 
-#define QMV_KERNEL(K, M, XF32)                                                           \
-  extern "C" __global__ __launch_bounds__(256) void lisa_qmv_k##K##_m##M(LisaQmvParams p) { \
-    __shared__ __attribute__((aligned(16))) unsigned char lds[QmvLds<K, M, XF32>::BYTES];  \
-    qmv_body<K, M, XF32>(p, lds);                                                        \
+// One kernel per (K, M, prologue): lisa_qmv_k<K>_m<M>_<x|resnorm|embed|cast|norm|mtpfc>.
+#define QMV_KERNEL(K, M, MODE, NAME)                                                             \
+  extern "C" __global__ __launch_bounds__(256) void lisa_qmv_k##K##_m##M##_##NAME(LisaQmvParams p) { \
+    __shared__ __attribute__((aligned(16))) unsigned char lds[QmvCfg<K, M>::BYTES];                \
+    qmv_body<K, M, MODE>(p, lds);                                                                \
   }
 
-QMV_KERNEL(5120, 1, true)
-QMV_KERNEL(5120, 3, true)
-QMV_KERNEL(6144, 1, true)
-QMV_KERNEL(6144, 3, true)
-QMV_KERNEL(10240, 1, true)
-QMV_KERNEL(17408, 1, true)
-QMV_KERNEL(17408, 3, false)
-QMV_KERNEL(1024, 1, true)
-QMV_KERNEL(1024, 3, true)
+QMV_KERNEL(5120, 1, LISA_PRO_LOADX, x)
+QMV_KERNEL(5120, 1, LISA_PRO_RESNORM, resnorm)
+QMV_KERNEL(5120, 1, LISA_PRO_EMBED, embed)
+QMV_KERNEL(5120, 1, LISA_PRO_CAST, cast)
+QMV_KERNEL(5120, 1, LISA_PRO_NORM, norm)
+QMV_KERNEL(5120, 3, LISA_PRO_LOADX, x)
+QMV_KERNEL(5120, 3, LISA_PRO_RESNORM, resnorm)
+QMV_KERNEL(5120, 3, LISA_PRO_EMBED, embed)
+QMV_KERNEL(5120, 3, LISA_PRO_NORM, norm)
+QMV_KERNEL(6144, 1, LISA_PRO_LOADX, x)
+QMV_KERNEL(6144, 3, LISA_PRO_LOADX, x)
+QMV_KERNEL(10240, 1, LISA_PRO_LOADX, x)
+QMV_KERNEL(10240, 1, LISA_PRO_MTPFC, mtpfc)
+QMV_KERNEL(17408, 1, LISA_PRO_LOADX, x)
+QMV_KERNEL(17408, 3, LISA_PRO_LOADX, x)
+QMV_KERNEL(1024, 1, LISA_PRO_LOADX, x)
+QMV_KERNEL(1024, 3, LISA_PRO_LOADX, x)
 
 // ===========================================================================
 // GDN recurrence (gdn.metal:245-328) + gates (gdn.metal:170-205) + gated

@@ -93,7 +93,7 @@ struct LisaRunner {
   LisaDevice* dev = nullptr;
   LisaModule* mod = nullptr;
   // kernels
-  LisaFunction *qmv[2][5] = {};  // [m3][K index]
+  LisaFunction *qmv[2][5][6] = {};  // [m3][K index][prologue mode]
   LisaFunction *gdn[2] = {}, *attn_part[2] = {}, *attn_merge[2] = {}, *finalize = nullptr, *synth = nullptr;
   // memory
   LisaBuffer *weights = nullptr, *state = nullptr, *scratch = nullptr;
@@ -115,7 +115,6 @@ struct LisaRunner {
   int64_t verify_base = -1;
   uint32_t mtp_position = 0;
   LisaGraph* step_graph = nullptr;
-  uint32_t qmv_grid_cap = 1024;
   // per-launch event profiling of eager steps (lisa_runner_profile_step)
   bool profiling = false;
   std::vector<hipEvent_t> prof_events;
@@ -133,6 +132,18 @@ int k_index(uint32_t k) {
     case 1024: return 4;
     default: return -1;
   }
+}
+
+// q4 launch geometry: 8-row tiles (4 outputs for gate/up pairs); K = 5120 runs
+// one tile per wave (4 per workgroup), every other K splits each tile's group
+// iterations over the four waves of one workgroup.
+bool qmv_split(uint32_t k) { return k != LISA_HIDDEN; }
+
+uint32_t qmv_grid(uint32_t k, uint32_t tiles) { return qmv_split(k) ? tiles : (tiles + 3) / 4; }
+
+// workgroups of the lm_head launch = number of argmax partials per row
+int lm_head_grid(const LisaRunner* r) {
+  return (int)std::max<uint32_t>(1, qmv_grid(LISA_HIDDEN, ((uint32_t)r->cfg.vocab + 7) / 8));
 }
 
 int upload_u32(LisaRunner* r, uint32_t* dst, const uint32_t* src, size_t n) {
@@ -322,8 +333,8 @@ void plan_ctx(LisaRunner* r, Arena& A, Ctx& c, int rows) {
   c.part_o = A.take<float>((size_t)rows * LISA_ATT_QH * r->s_max * LISA_ATT_HD);
   c.part_ml = A.take<float>((size_t)rows * LISA_ATT_QH * r->s_max * 2);
   c.logits = A.take<float>((size_t)rows * r->cfg.vocab);
-  c.am_val = A.take<float>((size_t)rows * 4096);
-  c.am_idx = A.take<uint32_t>((size_t)rows * 4096);
+  c.am_val = A.take<float>((size_t)rows * lm_head_grid(r));
+  c.am_idx = A.take<uint32_t>((size_t)rows * lm_head_grid(r));
   c.xnorm = A.take<uint16_t>((size_t)rows * LISA_HIDDEN);
   c.cond = A.take<uint16_t>(LISA_HIDDEN);
   c.tokens = A.take<uint32_t>(4);
@@ -345,8 +356,9 @@ struct MatSpec {
 int launch_qmv(LisaRunner* r, int m_rows, uint32_t K, LisaQmvParams& p, const std::vector<MatSpec>& mats) {
   const int ki = k_index(K);
   if (ki < 0) return lisa_fail(LISA_E_ARG, "no q4 kernel for K=%u", K);
-  LisaFunction* fn = r->qmv[m_rows == 3 ? 1 : 0][ki];
-  if (!fn) return lisa_fail(LISA_E_ARG, "no q4 kernel for K=%u M=%d", K, m_rows);
+  if (p.pro_mode > LISA_PRO_MTPFC) return lisa_fail(LISA_E_ARG, "bad q4 prologue mode %u", p.pro_mode);
+  LisaFunction* fn = r->qmv[m_rows == 3 ? 1 : 0][ki][p.pro_mode];
+  if (!fn) return lisa_fail(LISA_E_ARG, "no q4 kernel for K=%u M=%d prologue %u", K, m_rows, p.pro_mode);
   p.n_mats = (uint32_t)mats.size();
   uint32_t tiles = 0, rows_total = 0;
   for (size_t e = 0; e < mats.size(); ++e) {
@@ -366,10 +378,9 @@ int launch_qmv(LisaRunner* r, int m_rows, uint32_t K, LisaQmvParams& p, const st
     rows_total += pair ? 2 * s.w->n : s.w->n;
   }
   p.tile_start[mats.size()] = tiles;
-  p.ksplit = rows_total <= 8192 ? 4 : 1;
-  uint32_t grid = p.ksplit == 4 ? tiles : (tiles + 3) / 4;
-  grid = std::max<uint32_t>(1, std::min(grid, r->qmv_grid_cap));
-  if (p.am_val && grid > 4096) grid = 4096;
+  (void)rows_total;
+  p.ksplit = qmv_split(K) ? 4 : 1;
+  const uint32_t grid = std::max<uint32_t>(1, qmv_grid(K, tiles));
   return lisa_launch(r->dev, fn, &p, sizeof p, grid, 1, 1, 256, 1, 1);
 }
 
@@ -429,13 +440,6 @@ int launch_lm_head(LisaRunner* r, Ctx& c, int m, const uint16_t* norm, uint16_t*
   p.am_val = c.am_val;
   p.am_idx = c.am_idx;
   return launch_qmv(r, m, LISA_HIDDEN, p, {{&r->head, nullptr, c.logits, LISA_EPI_ARGMAX}});
-}
-
-int lm_head_grid(LisaRunner* r) {
-  const uint32_t tiles = ((uint32_t)r->cfg.vocab + 7) / 8;
-  const bool split = (uint32_t)r->cfg.vocab <= 8192;
-  uint32_t grid = split ? tiles : (tiles + 3) / 4;
-  return (int)std::max<uint32_t>(1, std::min(std::min(grid, r->qmv_grid_cap), 4096u));
 }
 
 int launch_finalize(LisaRunner* r, Ctx& c, int m, bool feedback, uint32_t advance) {
@@ -639,16 +643,20 @@ extern "C" int lisa_runner_create(const LisaRunnerConfig* cfg, LisaRunner** out)
   if (cfg->capacity > 64 * 1024) return lisa_fail(LISA_E_ARG, "KV capacity above 65536 is not supported");
   std::unique_ptr<LisaRunner> r(new LisaRunner());
   r->cfg = *cfg;
-  if (const char* g = std::getenv("LISA_QMV_GRID")) r->qmv_grid_cap = (uint32_t)std::max(1, std::atoi(g));
   LISA_TRY(lisa_device_create(cfg->device, &r->dev));
   LISA_TRY(lisa_module_load_default(r->dev, &r->mod));
+  // lisa_qmv_k<K>_m<M>_<prologue>; combinations the module does not hold stay null
   static const char* knames[5] = {"5120", "6144", "10240", "17408", "1024"};
+  static const char* pnames[6] = {"x", "resnorm", "embed", "cast", "norm", "mtpfc"};
   for (int mi = 0; mi < 2; ++mi)
-    for (int ki = 0; ki < 5; ++ki) {
-      const std::string name = std::string("lisa_qmv_k") + knames[ki] + (mi ? "_m3" : "_m1");
-      LisaFunction* f = nullptr;
-      if (lisa_function_get(r->mod, name.c_str(), &f) == LISA_OK) r->qmv[mi][ki] = f;
-    }
+    for (int ki = 0; ki < 5; ++ki)
+      for (int pi = 0; pi < 6; ++pi) {
+        const std::string name = std::string("lisa_qmv_k") + knames[ki] + (mi ? "_m3_" : "_m1_") + pnames[pi];
+        hipFunction_t hf;
+        if (hipModuleGetFunction(&hf, r->mod->mod, name.c_str()) == hipSuccess)
+          r->qmv[mi][ki][pi] = new LisaFunction{hf, name};
+      }
+  (void)hipGetLastError();  // the probes of absent combinations leave an error behind
   for (int mi = 0; mi < 2; ++mi) {
     const char* sfx = mi ? "_m3" : "_m1";
     LISA_TRY(lisa_function_get(r->mod, (std::string("lisa_gdn_recurrence") + sfx).c_str(), &r->gdn[mi]));
@@ -692,6 +700,12 @@ extern "C" void lisa_runner_free(LisaRunner* r) {
   if (!r) return;
   if (r->dev) (void)hipStreamSynchronize(r->dev->stream);
   lisa_graph_free(r->step_graph);
+  for (auto& a : r->qmv)
+    for (auto& b : a)
+      for (LisaFunction* f : b) delete f;
+  for (LisaFunction* f : {r->gdn[0], r->gdn[1], r->attn_part[0], r->attn_part[1], r->attn_merge[0], r->attn_merge[1],
+                          r->finalize, r->synth})
+    delete f;
   lisa_buffer_free(r->scratch);
   lisa_buffer_free(r->state);
   lisa_buffer_free(r->weights);

@@ -46,6 +46,34 @@ float tree_xor(float* v, int n) {
   return v[0];
 }
 
+// Ascending-distance butterfly: pairs at distance 1, then 2, 4, ..., n/2.
+float tree_asc(float* v, int n) {
+  for (int m = 1; m < n; m <<= 1) {
+    float t[64];
+    for (int i = 0; i < n; ++i) t[i] = v[i] + v[i ^ m];
+    std::memcpy(v, t, sizeof(float) * n);
+  }
+  return v[0];
+}
+
+// Sum of squares of `cols` values (multiple of 8) as the q4 prologue of the
+// HIP path computes it: thread t of 256 owns the 8-element chunks t, t+256, ...
+// and sums their squares in element order; tree64 per wave of 64 threads;
+// (W0 + W1) + (W2 + W3). Same statistic as norm.metal:10-47, different
+// element-to-thread assignment.
+float sumsq_chunks8(const float* x, int cols) {
+  float lanes[256];
+  for (int t = 0; t < 256; ++t) {
+    float s = 0.0f;
+    for (int c = t; c < cols / 8; c += 256)
+      for (int e = 0; e < 8; ++e) s = s + x[8 * c + e] * x[8 * c + e];
+    lanes[t] = s;
+  }
+  float w[4];
+  for (int q = 0; q < 4; ++q) w[q] = tree_xor(lanes + 64 * q, 64);
+  return (w[0] + w[1]) + (w[2] + w[3]);
+}
+
 // Sum of squares of `cols` values (multiple of 256) with the rows-of-256 tree.
 float sumsq_rows256(const float* x, int cols) {
   float lanes[256];
@@ -69,7 +97,7 @@ float sumsq_tree128(const float* v) {
 // RMSNorm of a row of f32 (bf16-valued) inputs; norm.metal:10-47:
 // inv = rsqrt(sum/cols + eps), y = bf16(x * inv * w).
 void rms_norm_f(const float* x, const uint16_t* w, int cols, uint16_t* out) {
-  const float ss = sumsq_rows256(x, cols);
+  const float ss = sumsq_chunks8(x, cols);
   const float inv = lisa_rsqrt(ss / (float)cols + LISA_EPS);
   for (int j = 0; j < cols; ++j) out[j] = tobf((x[j] * inv) * bf(w[j]));
 }
@@ -79,26 +107,31 @@ void rms_norm_f(const float* x, const uint16_t* w, int cols, uint16_t* out) {
 //   acc_lo = fma chain over the low nibbles  (x[k_even] * q)
 //   acc_hi = fma chain over the high nibbles (x[k_odd]/16 * (byte & 0xf0)),
 //            which is the reference's own odd-nibble trick (qmv.metal:30-36,49)
-//   G = acc_lo + acc_hi;  P_g = fma(scale, G, bias * X_g), X_g = sum of the
-//   group's 64 x values in ascending order.
+//   G = acc_lo + acc_hi / 16;  P_g = fma(scale, G, bias * X_g), X_g = the
+//   ascending-distance tree64 of the group's 64 x values.
+// Both chains are evaluated with the nibble factors scaled by 2^-24 (q * 2^-24
+// and 16q * 2^-24, the values the HIP path reads as f16 subnormals) and the
+// scale multiplied by 2^24; the scaling is exact, so outside subnormal ranges
+// this is the unscaled arithmetic, and inside them it is still what the HIP
+// path computes.
 // The 16 lanes of a row-group accumulate P over g = 16i + lane (ascending i),
 // then tree16 (the simd_sum of qmv.metal:71-75 with 16 lanes).
 struct XPrep {
-  std::vector<float> xs;  // x with odd positions divided by 16 (exact)
+  std::vector<float> xs;  // x as f32
   std::vector<float> gsum;
 };
+
+constexpr float kNibScale = 0x1p-24f;
+constexpr float kScaleUp = 0x1p24f;
 
 void prep_x(const uint16_t* x, int k, XPrep& p) {
   p.xs.resize(k);
   p.gsum.resize(k / 64);
-  for (int i = 0; i < k; ++i) {
-    const float v = bf(x[i]);
-    p.xs[i] = (i & 1) ? v / 16.0f : v;
-  }
+  for (int i = 0; i < k; ++i) p.xs[i] = bf(x[i]);
   for (int g = 0; g < k / 64; ++g) {
-    float s = 0.0f;
-    for (int i = 0; i < 64; ++i) s = s + bf(x[64 * g + i]);
-    p.gsum[g] = s;
+    float v[64];
+    for (int i = 0; i < 64; ++i) v[i] = bf(x[64 * g + i]);
+    p.gsum[g] = tree_asc(v, 64);
   }
 }
 
@@ -108,12 +141,12 @@ inline float group_partial(const float* xs, const uint32_t* w8, float scale, flo
     const uint32_t word = w8[j];
     for (int b = 0; b < 4; ++b) {
       const uint32_t byte = (word >> (8 * b)) & 0xffu;
-      acc_lo = lisa_fma(xs[8 * j + 2 * b], (float)(byte & 0x0fu), acc_lo);
-      acc_hi = lisa_fma(xs[8 * j + 2 * b + 1], (float)(byte & 0xf0u), acc_hi);
+      acc_lo = lisa_fma(xs[8 * j + 2 * b], (float)(byte & 0x0fu) * kNibScale, acc_lo);
+      acc_hi = lisa_fma(xs[8 * j + 2 * b + 1], (float)(byte & 0xf0u) * kNibScale, acc_hi);
     }
   }
-  const float g = acc_lo + acc_hi;
-  return lisa_fma(scale, g, bias * xsum);
+  const float g = acc_lo + acc_hi * 0.0625f;
+  return lisa_fma(scale * kScaleUp, g, bias * xsum);
 }
 
 // ksplit = 1: lane l sums its groups over all iterations, tree16.
@@ -157,7 +190,7 @@ void q4_rows8(const XPrep& xp, const uint32_t* w, const uint16_t* s, const uint1
         __m256 lo = _mm256_setzero_ps(), hi = _mm256_setzero_ps();
         alignas(32) float sc[8], bi[8];
         for (int r = 0; r < 8; ++r) {
-          sc[r] = bf(s[(size_t)(row0 + r) * groups + g]);
+          sc[r] = bf(s[(size_t)(row0 + r) * groups + g]) * kScaleUp;
           bi[r] = bf(b[(size_t)(row0 + r) * groups + g]);
         }
         const float* xs = &xp.xs[64 * g];
@@ -167,13 +200,15 @@ void q4_rows8(const XPrep& xp, const uint32_t* w, const uint16_t* s, const uint1
           const __m256i wv = _mm256_load_si256((const __m256i*)wd);
           for (int bb = 0; bb < 4; ++bb) {
             const __m256i byte = _mm256_and_si256(_mm256_srli_epi32(wv, 8 * bb), _mm256_set1_epi32(0xff));
-            const __m256 qlo = _mm256_cvtepi32_ps(_mm256_and_si256(byte, _mm256_set1_epi32(0x0f)));
-            const __m256 qhi = _mm256_cvtepi32_ps(_mm256_and_si256(byte, _mm256_set1_epi32(0xf0)));
+            const __m256 qlo = _mm256_mul_ps(_mm256_cvtepi32_ps(_mm256_and_si256(byte, _mm256_set1_epi32(0x0f))),
+                                             _mm256_set1_ps(kNibScale));
+            const __m256 qhi = _mm256_mul_ps(_mm256_cvtepi32_ps(_mm256_and_si256(byte, _mm256_set1_epi32(0xf0))),
+                                             _mm256_set1_ps(kNibScale));
             lo = _mm256_fmadd_ps(_mm256_set1_ps(xs[8 * j + 2 * bb]), qlo, lo);
             hi = _mm256_fmadd_ps(_mm256_set1_ps(xs[8 * j + 2 * bb + 1]), qhi, hi);
           }
         }
-        const __m256 gv = _mm256_add_ps(lo, hi);
+        const __m256 gv = _mm256_add_ps(lo, _mm256_mul_ps(hi, _mm256_set1_ps(0.0625f)));
         const __m256 pp = _mm256_fmadd_ps(_mm256_load_ps(sc), gv,
                                           _mm256_mul_ps(_mm256_load_ps(bi), _mm256_set1_ps(xp.gsum[g])));
         t = _mm256_add_ps(t, pp);
@@ -258,14 +293,12 @@ std::vector<uint16_t> make_norm(uint64_t seed, int scope, int kind, int n) {
   return make_vec(seed, scope, kind, n, 0.9f, 1.1f);
 }
 
-// The HIP launch splits K across the four waves of a workgroup when the launch
-// has at most 8192 virtual rows; `launch_rows` is the row total of the launch
-// this matrix is part of.
-int ksplit_for(int launch_rows) { return launch_rows <= 8192 ? 4 : 1; }
+// The HIP launch splits the group iterations of a tile across the four waves
+// of a workgroup for every K except the 5120-wide inputs.
+int ksplit_for(int k) { return k == LISA_HIDDEN ? 1 : 4; }
 
-void q4_apply(const Q4& q, const std::vector<XPrep>& xp, int m_rows, int launch_rows, float* out) {
-  q4_linear_prepped(xp.data(), m_rows, q.w.data(), q.s.data(), q.b.data(), q.n, q.k, ksplit_for(launch_rows),
-                    out);
+void q4_apply(const Q4& q, const std::vector<XPrep>& xp, int m_rows, float* out) {
+  q4_linear_prepped(xp.data(), m_rows, q.w.data(), q.s.data(), q.b.data(), q.n, q.k, ksplit_for(q.k), out);
 }
 
 }  // namespace
@@ -635,14 +668,14 @@ static void residual_rows(const std::vector<float>& h, const std::vector<float>&
 static void mlp_block(const Q4& gate, const Q4& up, const Q4& down, const std::vector<XPrep>& xp,
                       int m, std::vector<float>& branch) {
   std::vector<float> g((size_t)m * LISA_INTER), u((size_t)m * LISA_INTER);
-  q4_apply(gate, xp, m, 2 * LISA_INTER, g.data());
-  q4_apply(up, xp, m, 2 * LISA_INTER, u.data());
+  q4_apply(gate, xp, m, g.data());
+  q4_apply(up, xp, m, u.data());
   std::vector<uint16_t> act((size_t)m * LISA_INTER);
   orc_silu_mul(g.data(), u.data(), m * LISA_INTER, act.data());
   std::vector<XPrep> ap;
   prep_rows(act, m, LISA_INTER, ap);
   branch.resize((size_t)m * LISA_HIDDEN);
-  q4_apply(down, ap, m, LISA_HIDDEN, branch.data());
+  q4_apply(down, ap, m, branch.data());
 }
 
 static void attention_block(const Q4& q, const Q4& k, const Q4& v, const Q4& o,
@@ -651,17 +684,16 @@ static void attention_block(const Q4& q, const Q4& k, const Q4& v, const Q4& o,
                             const std::vector<XPrep>& xp, int m, std::vector<float>& branch) {
   std::vector<float> qp((size_t)m * LISA_ATT_Q_OUT), kr((size_t)m * LISA_ATT_KV_OUT),
       vr((size_t)m * LISA_ATT_KV_OUT);
-  const int att_rows = LISA_ATT_Q_OUT + 2 * LISA_ATT_KV_OUT;
-  q4_apply(q, xp, m, att_rows, qp.data());
-  q4_apply(k, xp, m, att_rows, kr.data());
-  q4_apply(v, xp, m, att_rows, vr.data());
+  q4_apply(q, xp, m, qp.data());
+  q4_apply(k, xp, m, kr.data());
+  q4_apply(v, xp, m, vr.data());
   std::vector<uint16_t> gated((size_t)m * LISA_ATT_OUT);
   orc_attention(qp.data(), kr.data(), vr.data(), qn.data(), kn.data(), kc, vc, capacity, base, m,
                 gated.data());
   std::vector<XPrep> gp;
   prep_rows(gated, m, LISA_ATT_OUT, gp);
   branch.resize((size_t)m * LISA_HIDDEN);
-  q4_apply(o, gp, m, LISA_HIDDEN, branch.data());
+  q4_apply(o, gp, m, branch.data());
 }
 
 extern "C" {
@@ -815,11 +847,10 @@ int orc_model_forward(OrcModel* M, const uint32_t* tokens, int m, int capture, u
       const int si = l.state_index;
       std::vector<float> qkv((size_t)m * LISA_GDN_CONV_DIM), z((size_t)m * LISA_GDN_VALUE_DIM),
           a((size_t)m * LISA_GDN_VH), b((size_t)m * LISA_GDN_VH);
-      const int gdn_rows = LISA_GDN_CONV_DIM + LISA_GDN_VALUE_DIM + 2 * LISA_GDN_VH;
-      q4_apply(l.qkv, xp, m, gdn_rows, qkv.data());
-      q4_apply(l.z, xp, m, gdn_rows, z.data());
-      q4_apply(l.a, xp, m, gdn_rows, a.data());
-      q4_apply(l.b, xp, m, gdn_rows, b.data());
+      q4_apply(l.qkv, xp, m, qkv.data());
+      q4_apply(l.z, xp, m, z.data());
+      q4_apply(l.a, xp, m, a.data());
+      q4_apply(l.b, xp, m, b.data());
       std::vector<float> conv_out((size_t)m * LISA_GDN_CONV_DIM);
       std::vector<uint16_t> cslots;
       if (capture) cslots.resize((size_t)m * 3 * LISA_GDN_CONV_DIM);
@@ -843,7 +874,7 @@ int orc_model_forward(OrcModel* M, const uint32_t* tokens, int m, int capture, u
       std::vector<XPrep> gp;
       prep_rows(gated, m, LISA_GDN_VALUE_DIM, gp);
       B.resize((size_t)m * LISA_HIDDEN);
-      q4_apply(l.out, gp, m, LISA_HIDDEN, B.data());
+      q4_apply(l.out, gp, m, B.data());
     } else {
       const size_t off = (size_t)l.cache_index * LISA_ATT_KVH * M->capacity * LISA_ATT_HD;
       attention_block(l.q, l.k, l.v, l.o, l.q_norm, l.k_norm, &M->key_cache[off],
@@ -856,7 +887,7 @@ int orc_model_forward(OrcModel* M, const uint32_t* tokens, int m, int capture, u
   }
   norm_rows(H, m, M->final_norm, xp);
   std::vector<float> logits((size_t)m * M->vocab);
-  q4_apply(M->head, xp, m, M->vocab, logits.data());
+  q4_apply(M->head, xp, m, logits.data());
   for (int t = 0; t < m; ++t) {
     if (argmax_out) argmax_out[t] = orc_argmax(&logits[(size_t)t * M->vocab], M->vocab);
   }
@@ -895,7 +926,7 @@ int orc_mtp_forward(OrcModel* M, uint32_t token, const uint16_t* cond, uint32_t*
   std::vector<XPrep> xp(1);
   prep_x(x.data(), 2 * LISA_HIDDEN, xp[0]);
   std::vector<float> fc(LISA_HIDDEN);
-  q4_apply(t.fc, xp, 1, LISA_HIDDEN, fc.data());
+  q4_apply(t.fc, xp, 1, fc.data());
   std::vector<float> H(LISA_HIDDEN), R, B;
   for (int c = 0; c < LISA_HIDDEN; ++c) H[c] = bfr(fc[c]);  // f32_to_bf16 (norm.metal:132-137)
   norm_rows(H, 1, t.input_norm, xp);
@@ -908,7 +939,7 @@ int orc_mtp_forward(OrcModel* M, uint32_t token, const uint16_t* cond, uint32_t*
   std::vector<uint16_t> xn;
   norm_rows(H, 1, t.final_norm, xp, &xn);
   std::vector<float> logits(M->vocab);
-  q4_apply(M->head, xp, 1, M->vocab, logits.data());
+  q4_apply(M->head, xp, 1, logits.data());
   if (argmax_out) *argmax_out = orc_argmax(logits.data(), M->vocab);
   if (normalized_out) std::memcpy(normalized_out, xn.data(), 2 * LISA_HIDDEN);
   t.position += 1;

@@ -62,11 +62,15 @@ class DevQ4:
         self.w, self.s, self.b = w, s, b
 
 
-def launch_qmv(pkg, dev, K, M, params, mats, grid_cap=1024):
+PROLOGUE_NAMES = ["x", "resnorm", "embed", "cast", "norm", "mtpfc"]
+
+
+def launch_qmv(pkg, dev, K, M, params, mats):
     """Restates launch_qmv of lisa-rs_amd/csrc/runner.cpp. mats: list of
-    (DevQ4, DevQ4-or-None, out_ptr, kind)."""
+    (DevQ4, DevQ4-or-None, out_ptr, kind). One 8-row tile per wave (K = 5120,
+    four tiles per workgroup) or per workgroup with the group iterations split
+    over its four waves (every other K)."""
     tiles = 0
-    rows_total = 0
     for e, (q, q2, out, kind) in enumerate(mats):
         m = params.mats[e]
         m.w, m.sb = q.wbuf.ptr, q.sbbuf.ptr
@@ -78,11 +82,10 @@ def launch_qmv(pkg, dev, K, M, params, mats, grid_cap=1024):
         params.tile_start[e] = tiles
         pair = kind == pkg.EPI_GATEUP
         tiles += (q.n + 3) // 4 if pair else (q.n + 7) // 8
-        rows_total += 2 * q.n if pair else q.n
     params.tile_start[len(mats)] = tiles
     params.n_mats = len(mats)
-    params.ksplit = 4 if rows_total <= 8192 else 1
-    grid = tiles if params.ksplit == 4 else (tiles + 3) // 4
-    grid = max(1, min(grid, grid_cap))
-    dev.dispatch(f"lisa_qmv_k{K}_m{M}", params, (grid,), (256,))
+    params.ksplit = 1 if K == 5120 else 4
+    grid = max(1, tiles if params.ksplit == 4 else (tiles + 3) // 4)
+    name = f"lisa_qmv_k{K}_m{M}_{PROLOGUE_NAMES[params.pro_mode]}"
+    dev.dispatch(name, params, (grid,), (256,))
     return params.ksplit, grid
