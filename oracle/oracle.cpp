@@ -774,6 +774,7 @@ OrcModel* orc_model_create(int layers, int vocab, int capacity, uint64_t seed, i
 void orc_model_free(OrcModel* m) { delete m; }
 uint32_t orc_model_position(const OrcModel* m) { return m->position; }
 int orc_threads(void) { return omp_get_max_threads(); }
+int orc_layer_is_attention(int layer) { return lisa_layer_is_attention(layer); }
 uint32_t orc_mtp_position(const OrcModel* m) { return m->mtp.position; }
 
 void orc_model_reset(OrcModel* M) {

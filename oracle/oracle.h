@@ -96,6 +96,9 @@ void orc_model_free(OrcModel* m);
 uint32_t orc_model_position(const OrcModel* m);
 /* OpenMP threads the oracle runs on. */
 int orc_threads(void);
+
+/* Layer schedule of the hybrid stack (src/model/mod.rs:16-22). */
+int orc_layer_is_attention(int layer);
 /* Fill recurrent state, conv history and the first `filled` KV positions with
  * synthetic values and set position = filled (the bench's 4k-context start). */
 void orc_model_fill_state(OrcModel* m, uint32_t filled, uint64_t seed);

@@ -31,6 +31,7 @@ _SIGS = {
     "orc_model_free": (None, [_P]),
     "orc_model_position": (C.c_uint32, [_P]),
     "orc_threads": (C.c_int, []),
+    "orc_layer_is_attention": (C.c_int, [C.c_int]),
     "orc_model_fill_state": (None, [_P, C.c_uint32, C.c_uint64]),
     "orc_model_reset": (None, [_P]),
     "orc_model_forward": (C.c_int, [_P, _P, C.c_int, C.c_int, _P, _P, _P]),
@@ -95,6 +96,10 @@ def math(fn: str, x):
 
 def threads():
     return int(lib().orc_threads())
+
+
+def layer_is_attention(i):
+    return bool(lib().orc_layer_is_attention(i))
 
 
 def argmax(v):
