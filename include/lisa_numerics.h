@@ -38,12 +38,28 @@ LISA_HD float lisa_bf16_to_f32(uint16_t h) { return lisa_u2f((uint32_t)h << 16);
 /* f32 -> bf16 bits, round to nearest even; NaN stays NaN (quieted).
  * This is the in-kernel `bfloat(x)` conversion of the Metal shaders, which the
  * reference's own test models as RNE (tests/gdn_state.rs:7-11). */
+#if defined(__HIP_DEVICE_COMPILE__)
+/* gfx950 converts in hardware (v_cvt_pk_bf16_f32, round to nearest even). It
+ * equals the bit arithmetic below for every non-NaN f32 and keeps NaN a NaN
+ * (checked over all 2^32 inputs on an MI355X); only NaN payloads may differ. */
+LISA_HD uint16_t lisa_f32_to_bf16(float x) { return __builtin_bit_cast(uint16_t, (__bf16)x); }
+/* Two values packed lo | hi << 16 in one instruction. */
+LISA_HD uint32_t lisa_f32x2_to_bf16x2(float lo, float hi) {
+  uint32_t r;
+  asm("v_cvt_pk_bf16_f32 %0, %1, %2" : "=v"(r) : "v"(lo), "v"(hi));
+  return r;
+}
+#else
 LISA_HD uint16_t lisa_f32_to_bf16(float x) {
   uint32_t u = lisa_f2u(x);
   if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x0040u);
   u += 0x7fffu + ((u >> 16) & 1u);
   return (uint16_t)(u >> 16);
 }
+LISA_HD uint32_t lisa_f32x2_to_bf16x2(float lo, float hi) {
+  return (uint32_t)lisa_f32_to_bf16(lo) | ((uint32_t)lisa_f32_to_bf16(hi) << 16);
+}
+#endif
 
 /* float(bfloat(x)): round an f32 to the nearest bf16 value, kept as f32. */
 LISA_HD float lisa_bf16r(float x) { return lisa_bf16_to_f32(lisa_f32_to_bf16(x)); }

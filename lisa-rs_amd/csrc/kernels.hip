@@ -102,8 +102,10 @@ DEV float hi_bf(uint32_t u) { return __uint_as_float(u & 0xffff0000u); }
 // waits for weights), and the dispatcher balances the tail.
 //
 // x lives in LDS (f32, or bf16 for K = 17408), one copy per input row, in
-// 64-element groups whose 16-byte chunks are rotated by the group index so
-// the 16 lanes of a row-group read distinct banks. X_g follows it.
+// 64-element groups padded to 272 (f32) or 144 (bf16) bytes: the 16 lanes of a
+// row-group read 16 consecutive groups at the same offset, and the padding
+// puts them on disjoint banks, so every read address is a per-lane base plus
+// an immediate. X_g follows it.
 
 template <int K, int M>
 struct QmvCfg {
@@ -116,7 +118,9 @@ struct QmvCfg {
   static constexpr int RX = (NCH + 255) / 256;      // chunk rounds per thread (plain x)
   static constexpr bool NORMK = (K == LISA_HIDDEN || K == 2 * LISA_HIDDEN);
   static constexpr int RR = (NORMK && RX < 3) ? 3 : RX;
-  static constexpr int XBYTES = M * K * (XF32 ? 4 : 2);
+  static constexpr int GSTRIDE = XF32 ? 272 : 144;  // bytes per padded 64-group
+  static constexpr int ROWBYTES = G * GSTRIDE;
+  static constexpr int XBYTES = M * ROWBYTES;
   static constexpr int GBYTES = M * G * 4;
   static constexpr int RBYTES = 64 * 4;
   static constexpr int KBYTES = 4 * 8 * M * 4;
@@ -140,21 +144,27 @@ DEV float h16(uint32_t bits16) {
 DEV float fmix_lo(float x, uint32_t p, float acc) { return __builtin_fmaf(x, h16(p & 0xffffu), acc); }
 DEV float fmix_hi(float x, uint32_t p, float acc) { return __builtin_fmaf(x, h16(p >> 16), acc); }
 
+// Eight bf16-valued floats packed as bf16 pairs (exact: the values are bf16 already).
+DEV uint4 pack_bf8(const float (&v)[8]) {
+  return make_uint4(lisa_f32x2_to_bf16x2(v[0], v[1]), lisa_f32x2_to_bf16x2(v[2], v[3]),
+                    lisa_f32x2_to_bf16x2(v[4], v[5]), lisa_f32x2_to_bf16x2(v[6], v[7]));
+}
+
+DEV void unpack_bf8(const uint4& u, float (&v)[8]) {
+  v[0] = lo_bf(u.x); v[1] = hi_bf(u.x); v[2] = lo_bf(u.y); v[3] = hi_bf(u.y);
+  v[4] = lo_bf(u.z); v[5] = hi_bf(u.z); v[6] = lo_bf(u.w); v[7] = hi_bf(u.w);
+}
+
 template <int K, int M>
 DEV void put_chunk(unsigned char* lds, int m, int k0, const float (&x)[8]) {
+  using C = QmvCfg<K, M>;
   const int g = k0 >> 6, j = (k0 >> 3) & 7;
-  if constexpr (QmvCfg<K, M>::XF32) {
-    float* xs = reinterpret_cast<float*>(lds) + (size_t)m * K + g * 64;
-    *reinterpret_cast<float4*>(xs + 4 * ((2 * j + g) & 15)) = make_float4(x[0], x[1], x[2], x[3]);
-    *reinterpret_cast<float4*>(xs + 4 * ((2 * j + 1 + g) & 15)) = make_float4(x[4], x[5], x[6], x[7]);
+  unsigned char* base = lds + m * C::ROWBYTES + g * C::GSTRIDE;
+  if constexpr (C::XF32) {
+    *reinterpret_cast<float4*>(base + 32 * j) = make_float4(x[0], x[1], x[2], x[3]);
+    *reinterpret_cast<float4*>(base + 32 * j + 16) = make_float4(x[4], x[5], x[6], x[7]);
   } else {
-    uint16_t* xb = reinterpret_cast<uint16_t*>(lds) + (size_t)m * K + g * 64;
-    uint4 v;
-    v.x = (__float_as_uint(x[0]) >> 16) | (__float_as_uint(x[1]) & 0xffff0000u);
-    v.y = (__float_as_uint(x[2]) >> 16) | (__float_as_uint(x[3]) & 0xffff0000u);
-    v.z = (__float_as_uint(x[4]) >> 16) | (__float_as_uint(x[5]) & 0xffff0000u);
-    v.w = (__float_as_uint(x[6]) >> 16) | (__float_as_uint(x[7]) & 0xffff0000u);
-    *reinterpret_cast<uint4*>(xb + 8 * ((j + g) & 7)) = v;
+    *reinterpret_cast<uint4*>(base + 16 * j) = pack_bf8(x);
   }
 }
 
@@ -170,10 +180,6 @@ DEV void put_gsum(float* gsum, int m, int k0, bool valid, const float (&x)[8]) {
   if (valid && ((k0 >> 3) & 7) == 0) gsum[m * QmvCfg<K, M>::G + (k0 >> 6)] = s;
 }
 
-DEV void unpack_bf8(const uint4& u, float (&v)[8]) {
-  v[0] = lo_bf(u.x); v[1] = hi_bf(u.x); v[2] = lo_bf(u.y); v[3] = hi_bf(u.y);
-  v[4] = lo_bf(u.z); v[5] = hi_bf(u.z); v[6] = lo_bf(u.w); v[7] = hi_bf(u.w);
-}
 
 // RMSNorm statistic of one 5120-wide segment from each thread's partial sum of
 // squares: tree64 per wave, then (W0 + W1) + (W2 + W3).
@@ -272,20 +278,10 @@ DEV void seg_process(const LisaQmvParams& p, unsigned char* lds, int m, const Pr
     put_gsum<K, M>(gsum, m, k0, valid, x);
     if (valid && writer) {
       if (MODE != LISA_PRO_MTPFC && p.r_out) {
-        uint4 o;
-        o.x = (__float_as_uint(v[i][0]) >> 16) | (__float_as_uint(v[i][1]) & 0xffff0000u);
-        o.y = (__float_as_uint(v[i][2]) >> 16) | (__float_as_uint(v[i][3]) & 0xffff0000u);
-        o.z = (__float_as_uint(v[i][4]) >> 16) | (__float_as_uint(v[i][5]) & 0xffff0000u);
-        o.w = (__float_as_uint(v[i][6]) >> 16) | (__float_as_uint(v[i][7]) & 0xffff0000u);
-        reinterpret_cast<uint4*>(p.r_out + (size_t)m * LISA_HIDDEN)[c] = o;
+        reinterpret_cast<uint4*>(p.r_out + (size_t)m * LISA_HIDDEN)[c] = pack_bf8(v[i]);
       }
       if (p.x_out) {
-        uint4 o;
-        o.x = (__float_as_uint(x[0]) >> 16) | (__float_as_uint(x[1]) & 0xffff0000u);
-        o.y = (__float_as_uint(x[2]) >> 16) | (__float_as_uint(x[3]) & 0xffff0000u);
-        o.z = (__float_as_uint(x[4]) >> 16) | (__float_as_uint(x[5]) & 0xffff0000u);
-        o.w = (__float_as_uint(x[6]) >> 16) | (__float_as_uint(x[7]) & 0xffff0000u);
-        reinterpret_cast<uint4*>(p.x_out + (size_t)m * K + SEG * LISA_HIDDEN)[c] = o;
+        reinterpret_cast<uint4*>(p.x_out + (size_t)m * K + SEG * LISA_HIDDEN)[c] = pack_bf8(x);
       }
     }
   }
@@ -459,15 +455,14 @@ DEV void group_dot2(const unsigned char* lds, int g, const uint4& a0, const uint
 #pragma unroll
     for (int m = 0; m < M; ++m) {
       float x[8];
+      const unsigned char* base = lds + m * C::ROWBYTES + g * C::GSTRIDE;
       if constexpr (C::XF32) {
-        const float* xs = reinterpret_cast<const float*>(lds) + (size_t)m * K + g * 64;
-        const float4 xa = *reinterpret_cast<const float4*>(xs + 4 * ((2 * j + g) & 15));
-        const float4 xb = *reinterpret_cast<const float4*>(xs + 4 * ((2 * j + 1 + g) & 15));
+        const float4 xa = *reinterpret_cast<const float4*>(base + 32 * j);
+        const float4 xb = *reinterpret_cast<const float4*>(base + 32 * j + 16);
         x[0] = xa.x; x[1] = xa.y; x[2] = xa.z; x[3] = xa.w;
         x[4] = xb.x; x[5] = xb.y; x[6] = xb.z; x[7] = xb.w;
       } else {
-        const uint16_t* xb = reinterpret_cast<const uint16_t*>(lds) + (size_t)m * K + g * 64;
-        unpack_bf8(*reinterpret_cast<const uint4*>(xb + 8 * ((j + g) & 7)), x);
+        unpack_bf8(*reinterpret_cast<const uint4*>(base + 16 * j), x);
       }
       lo0[m] = fmix_lo(x[0], p0, lo0[m]);
       lo0[m] = fmix_lo(x[2], p2, lo0[m]);
@@ -497,7 +492,8 @@ DEV void group_dot2(const unsigned char* lds, int g, const uint4& a0, const uint
   }
 }
 
-template <int K, int M, int MODE>
+// EPI: the epilogue of every matrix of the launch, or -1 to read it per tile.
+template <int K, int M, int MODE, int EPI>
 DEV void qmv_body(const LisaQmvParams& p, unsigned char* lds) {
   using C = QmvCfg<K, M>;
   const float* gsum = reinterpret_cast<const float*>(lds + C::XBYTES);
@@ -567,7 +563,7 @@ DEV void qmv_body(const LisaQmvParams& p, unsigned char* lds) {
     const LisaQ4Mat& mt = p.mats[tr.e];
     const uint32_t r0 = tr.r0, r1 = tr.r1;
     const bool v0 = tr.v0, v1 = tr.v1;
-    switch (mt.kind) {
+    switch (EPI >= 0 ? (uint32_t)EPI : mt.kind) {
       case LISA_EPI_STORE: {
         float* out = static_cast<float*>(mt.out);
 #pragma unroll
@@ -639,11 +635,19 @@ DEV void qmv_body(const LisaQmvParams& p, unsigned char* lds) {
   }
 }
 
-// One kernel per (K, M, prologue): lisa_qmv_k<K>_m<M>_<x|resnorm|embed|cast|norm|mtpfc>.
+// One kernel per (K, M, prologue): lisa_qmv_k<K>_m<M>_<x|resnorm|embed|cast|norm|mtpfc>,
+// plus variants whose epilogue is fixed at compile time:
+// lisa_qmv_k5120_m<M>_resnorm_<gateup|argmax> (MLP gate/up, lm_head).
 #define QMV_KERNEL(K, M, MODE, NAME)                                                             \
   extern "C" __global__ __launch_bounds__(256) void lisa_qmv_k##K##_m##M##_##NAME(LisaQmvParams p) { \
     __shared__ __attribute__((aligned(16))) unsigned char lds[QmvCfg<K, M>::BYTES];                \
-    qmv_body<K, M, MODE>(p, lds);                                                                \
+    qmv_body<K, M, MODE, -1>(p, lds);                                                            \
+  }
+#define QMV_KERNEL_EPI(K, M, MODE, NAME, EPI, ENAME)                                             \
+  extern "C" __global__ __launch_bounds__(256) void lisa_qmv_k##K##_m##M##_##NAME##_##ENAME(       \
+      LisaQmvParams p) {                                                                         \
+    __shared__ __attribute__((aligned(16))) unsigned char lds[QmvCfg<K, M>::BYTES];                \
+    qmv_body<K, M, MODE, EPI>(p, lds);                                                           \
   }
 
 QMV_KERNEL(5120, 1, LISA_PRO_LOADX, x)
@@ -663,6 +667,10 @@ QMV_KERNEL(17408, 1, LISA_PRO_LOADX, x)
 QMV_KERNEL(17408, 3, LISA_PRO_LOADX, x)
 QMV_KERNEL(1024, 1, LISA_PRO_LOADX, x)
 QMV_KERNEL(1024, 3, LISA_PRO_LOADX, x)
+QMV_KERNEL_EPI(5120, 1, LISA_PRO_RESNORM, resnorm, LISA_EPI_GATEUP, gateup)
+QMV_KERNEL_EPI(5120, 3, LISA_PRO_RESNORM, resnorm, LISA_EPI_GATEUP, gateup)
+QMV_KERNEL_EPI(5120, 1, LISA_PRO_RESNORM, resnorm, LISA_EPI_ARGMAX, argmax)
+QMV_KERNEL_EPI(5120, 3, LISA_PRO_RESNORM, resnorm, LISA_EPI_ARGMAX, argmax)
 
 // ===========================================================================
 // GDN recurrence (gdn.metal:245-328) + gates (gdn.metal:170-205) + gated
@@ -927,18 +935,32 @@ extern "C" __global__ __launch_bounds__(256) void lisa_attn_merge_m3(LisaAttnPar
 // ===========================================================================
 // argmax finish (runner.rs:1077-1095 on the device) + step bookkeeping
 // ===========================================================================
-extern "C" __global__ __launch_bounds__(256) void lisa_step_finalize(LisaFinalizeParams p) {
-  __shared__ float cv[4];
-  __shared__ uint32_t ci[4];
+// 1024 threads; every thread keeps eight independent partial loads in flight
+// per pass. (max, lowest index) is a total order on non-NaN values, so the
+// result does not depend on the reduction order.
+extern "C" __global__ __launch_bounds__(1024) void lisa_step_finalize(LisaFinalizeParams p) {
+  __shared__ float cv[16];
+  __shared__ uint32_t ci[16];
   __shared__ uint32_t res[4];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const uint32_t n = p.n_part;
   for (uint32_t m = 0; m < p.m_rows; ++m) {
+    const float* av = p.am_val + (size_t)m * n;
+    const uint32_t* ai = p.am_idx + (size_t)m * n;
     float v = -INFINITY;
     uint32_t i = 0xffffffffu;
-    for (uint32_t j = tid; j < p.n_part; j += 256) {
-      const float ov = p.am_val[(size_t)m * p.n_part + j];
-      const uint32_t oi = p.am_idx[(size_t)m * p.n_part + j];
-      if (better(ov, oi, v, i)) { v = ov; i = oi; }
+    for (uint32_t j0 = 0; j0 < n; j0 += 8 * 1024) {
+      float ov[8];
+      uint32_t oi[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const uint32_t j = min(j0 + (uint32_t)(u * 1024 + tid), n - 1);
+        ov[u] = av[j];
+        oi[u] = ai[j];
+      }
+#pragma unroll
+      for (int u = 0; u < 8; ++u)
+        if (j0 + (uint32_t)(u * 1024 + tid) < n && better(ov[u], oi[u], v, i)) { v = ov[u]; i = oi[u]; }
     }
     for (int msk = 1; msk < 64; msk <<= 1) {
       const float ov = __shfl_xor(v, msk, 64);
@@ -950,7 +972,7 @@ extern "C" __global__ __launch_bounds__(256) void lisa_step_finalize(LisaFinaliz
     if (tid == 0) {
       float bv = cv[0];
       uint32_t bi = ci[0];
-      for (int q = 1; q < 4; ++q)
+      for (int q = 1; q < 16; ++q)
         if (better(cv[q], ci[q], bv, bi)) { bv = cv[q]; bi = ci[q]; }
       if (bi == 0xffffffffu) bi = 0;
       res[m & 3] = bi;

@@ -94,6 +94,7 @@ struct LisaRunner {
   LisaModule* mod = nullptr;
   // kernels
   LisaFunction *qmv[2][5][6] = {};  // [m3][K index][prologue mode]
+  LisaFunction *qmv_epi[2][6][4] = {};  // K = 5120 with a fixed epilogue: [m3][prologue][epilogue]
   LisaFunction *gdn[2] = {}, *attn_part[2] = {}, *attn_merge[2] = {}, *finalize = nullptr, *synth = nullptr;
   // memory
   LisaBuffer *weights = nullptr, *state = nullptr, *scratch = nullptr;
@@ -358,6 +359,12 @@ int launch_qmv(LisaRunner* r, int m_rows, uint32_t K, LisaQmvParams& p, const st
   if (ki < 0) return lisa_fail(LISA_E_ARG, "no q4 kernel for K=%u", K);
   if (p.pro_mode > LISA_PRO_MTPFC) return lisa_fail(LISA_E_ARG, "bad q4 prologue mode %u", p.pro_mode);
   LisaFunction* fn = r->qmv[m_rows == 3 ? 1 : 0][ki][p.pro_mode];
+  // a launch whose matrices all share one epilogue uses the specialized kernel when there is one
+  bool same_kind = !mats.empty();
+  for (const MatSpec& s : mats) same_kind = same_kind && s.kind == mats[0].kind;
+  if (K == LISA_HIDDEN && same_kind && mats[0].kind < 4) {
+    if (LisaFunction* f = r->qmv_epi[m_rows == 3 ? 1 : 0][p.pro_mode][mats[0].kind]) fn = f;
+  }
   if (!fn) return lisa_fail(LISA_E_ARG, "no q4 kernel for K=%u M=%d prologue %u", K, m_rows, p.pro_mode);
   p.n_mats = (uint32_t)mats.size();
   uint32_t tiles = 0, rows_total = 0;
@@ -455,7 +462,7 @@ int launch_finalize(LisaRunner* r, Ctx& c, int m, bool feedback, uint32_t advanc
   f.m_rows = (uint32_t)m;
   f.pos_advance = advance;
   f.history_cap = kHistoryCap;
-  return lisa_launch(r->dev, r->finalize, &f, sizeof f, 1, 1, 1, 256, 1, 1);
+  return lisa_launch(r->dev, r->finalize, &f, sizeof f, 1, 1, 1, 1024, 1, 1);
 }
 
 // One target forward of m rows (runner.rs:555-591 for m=1, 866-909 for m=3).
@@ -655,6 +662,12 @@ extern "C" int lisa_runner_create(const LisaRunnerConfig* cfg, LisaRunner** out)
         hipFunction_t hf;
         if (hipModuleGetFunction(&hf, r->mod->mod, name.c_str()) == hipSuccess)
           r->qmv[mi][ki][pi] = new LisaFunction{hf, name};
+        static const char* enames[4] = {"store", "gateup", "conv", "argmax"};
+        for (int ei = 0; ki == 0 && ei < 4; ++ei) {
+          const std::string en = name + "_" + enames[ei];
+          if (hipModuleGetFunction(&hf, r->mod->mod, en.c_str()) == hipSuccess)
+            r->qmv_epi[mi][pi][ei] = new LisaFunction{hf, en};
+        }
       }
   (void)hipGetLastError();  // the probes of absent combinations leave an error behind
   for (int mi = 0; mi < 2; ++mi) {
@@ -701,6 +714,9 @@ extern "C" void lisa_runner_free(LisaRunner* r) {
   if (r->dev) (void)hipStreamSynchronize(r->dev->stream);
   lisa_graph_free(r->step_graph);
   for (auto& a : r->qmv)
+    for (auto& b : a)
+      for (LisaFunction* f : b) delete f;
+  for (auto& a : r->qmv_epi)
     for (auto& b : a)
       for (LisaFunction* f : b) delete f;
   for (LisaFunction* f : {r->gdn[0], r->gdn[1], r->attn_part[0], r->attn_part[1], r->attn_merge[0], r->attn_merge[1],
