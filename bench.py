@@ -11,8 +11,12 @@ hipGraph replay per token (the loop of the reference's src/cli/run.rs:69-73).
 
 Timed region: K graph replays bracketed by device synchronization and HIP
 events on the runner's stream. After it, an eager profile pass times every
-launch with HIP events (per-kind averages; the dominant kernel — MLP gate/up —
-gives the roofline object). The CPU baseline is the oracle (a C++ scalar/AVX2
+launch with start/stop events attached to the dispatch itself
+(hipExtModuleLaunchKernel, the kernel's execution window as a kernel trace
+reports it); per-kind averages; the dominant kernel, MLP gate/up, gives the
+roofline object. Its HBM traffic comes from the FETCH_SIZE / WRITE_SIZE
+counter summary committed in profiles/ (scaled by the same counters on a plain
+copy kernel, `--calibrate-copy`). The CPU baseline is the oracle (a C++ scalar/AVX2
 + OpenMP restatement of the same arithmetic) decoding a bounded sample of the
 same workload (same weights, context and first token) on the host cores;
 its tokens must equal the GPU's (argmax-exact).
@@ -35,6 +39,8 @@ CTX_SEED = 0x4C1A
 FIRST_TOKEN = 2005  # the reference CLI's default prompt token (src/cli/run.rs:177)
 CTX = 4096
 HBM_PEAK_GBS = 8000.0
+ROOFLINE_KERNEL = "lisa_qmv_k5120_m1_resnorm_gateup"
+TRAFFIC_SUMMARY = ROOT / "profiles" / "qmv_gateup_traffic.txt"
 
 HIDDEN, INTER, VOCAB, LAYERS = 5120, 17408, 248320, 64
 
@@ -73,6 +79,33 @@ def gate_up_bytes():
     return 2 * q4_bytes(INTER, HIDDEN) + HIDDEN * (2 + 4 + 2 + 2) + INTER * 2
 
 
+def traffic_per_launch():
+    """HBM bytes per gate/up launch from the committed counter summary
+    ("traffic_bytes: N" line), or None when there is none."""
+    try:
+        for line in TRAFFIC_SUMMARY.read_text().splitlines():
+            if line.startswith("traffic_bytes:"):
+                return int(float(line.split(":", 1)[1]))
+    except OSError:
+        pass
+    return None
+
+
+def calibrate_copy(mb):
+    """Plain device copy of `mb` MiB (lisa_copy_bytes), the reference point of
+    the HBM traffic counters: run it under rocprofv3 --pmc FETCH_SIZE (then
+    WRITE_SIZE) and divide the known bytes by what the counter reads."""
+    pkg = load("lisa_rs_amd", ROOT / "lisa-rs_amd" / "__init__.py", ROOT / "lisa-rs_amd")
+    dev = pkg.Device(0)
+    n = mb << 20
+    src, dst = dev.buffer(n), dev.buffer(n)
+    p = pkg.CopyParams(src.ptr, dst.ptr, n // 16)
+    for _ in range(5):
+        dev.dispatch("lisa_copy_bytes", p, (1024,), (256,))
+    print(json.dumps({"calibration": "lisa_copy_bytes", "bytes_read": n, "bytes_written": n, "dispatches": 5}),
+          flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -81,7 +114,12 @@ def main():
     ap.add_argument("--cpu-steps", type=int, default=2)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--profile-steps", type=int, default=4)
+    ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
+                    help="only run the plain copy kernel over MIB MiB (counter calibration)")
     args = ap.parse_args()
+    if args.calibrate_copy:
+        calibrate_copy(args.calibrate_copy)
+        return
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); "
               "the decode path has no multi-GPU mode", file=sys.stderr)
@@ -133,6 +171,7 @@ def main():
     gu_avg_s = gu_ms / gu_n / 1e3
     gu_gbs = gate_up_bytes() / gu_avg_s / 1e9
     print(f"[bench] profile per token (us): {kernels_us}", file=sys.stderr, flush=True)
+    traffic = traffic_per_launch()
     runner.close()
 
     result = {
@@ -156,8 +195,8 @@ def main():
         "roofline_fraction": round(gbps / HBM_PEAK_GBS, 4),
         "target_decode_tok_s": round(tok_s, 3),
         "roofline": {"bound": "hbm", "achieved": round(gu_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(gu_gbs / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "lisa_qmv_k5120_m1 (MLP gate/up + SwiGLU)",
+                     "frac": round(gu_gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
+                     "kernel": ROOFLINE_KERNEL + " (MLP gate/up + SwiGLU)",
                      "bytes_per_launch": gate_up_bytes(), "avg_launch_us": round(gu_avg_s * 1e6, 2)},
         "kernels_us_per_token": kernels_us,
     }

@@ -157,4 +157,13 @@ typedef struct LisaSynthParams {
   uint32_t filled;
 } LisaSynthParams;
 
+/* ---- device copy (norm.metal:109-130 copy_bytes) ---------------------------
+ * Kernel: lisa_copy_bytes, grid-stride over 16-byte units; src and dst 16-byte
+ * aligned. Also the plain-copy reference of the HBM traffic counters. */
+typedef struct LisaCopyParams {
+  const void* src;
+  void* dst;
+  uint64_t n16; /* 16-byte units */
+} LisaCopyParams;
+
 #endif /* LISA_KERNELS_H */

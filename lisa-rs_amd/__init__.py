@@ -94,6 +94,10 @@ class SynthParams(C.Structure):
                 ("capacity", C.c_uint32), ("filled", C.c_uint32)]
 
 
+class CopyParams(C.Structure):
+    _fields_ = [("src", C.c_uint64), ("dst", C.c_uint64), ("n16", C.c_uint64)]
+
+
 class RunnerConfig(C.Structure):
     _fields_ = [("layers", C.c_int32), ("vocab", C.c_int32), ("capacity", C.c_int32), ("with_mtp", C.c_int32),
                 ("seed", C.c_uint64), ("use_graph", C.c_int32), ("device", C.c_int32)]

@@ -9,12 +9,23 @@
 #include <string>
 #include <vector>
 
+// One timed launch of an eager profile pass: start/stop events attached to the
+// kernel dispatch itself (hipExtModuleLaunchKernel), so the interval is the
+// kernel's execution, as a kernel trace reports it.
+struct LisaProfRec {
+  int kind;
+  hipEvent_t start, stop;
+};
+
 struct LisaDevice {
   int ordinal = 0;
   hipStream_t stream = nullptr;
   std::string name, arch;
   uint64_t total_mem = 0;
   int cu_count = 0;
+  // set while a profile pass runs: every lisa_launch is timed and tagged
+  std::vector<LisaProfRec>* prof = nullptr;
+  int prof_kind = -1;
 };
 
 struct LisaBuffer {

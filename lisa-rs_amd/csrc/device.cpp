@@ -13,6 +13,15 @@
 #include <vector>
 
 #include "bridge.h"
+
+// From hip/hip_ext.h (C linkage in libamdhip64); declared here because the
+// header's template helpers do not compile with the host C++ compiler.
+extern "C" hipError_t hipExtModuleLaunchKernel(hipFunction_t f, uint32_t globalWorkSizeX, uint32_t globalWorkSizeY,
+                                               uint32_t globalWorkSizeZ, uint32_t localWorkSizeX,
+                                               uint32_t localWorkSizeY, uint32_t localWorkSizeZ,
+                                               size_t sharedMemBytes, hipStream_t hStream, void** kernelParams,
+                                               void** extra, hipEvent_t startEvent, hipEvent_t stopEvent,
+                                               uint32_t flags);
 #include "lisa_hip.h"
 
 namespace {
@@ -243,6 +252,17 @@ int lisa_launch(LisaDevice* d, LisaFunction* f, const void* params, size_t len, 
   (void)len;
   if (!gx || !gy || !gz) return LISA_OK;
   void* args[1] = {const_cast<void*>(params)};
+  if (d->prof) {
+    LisaProfRec rec{d->prof_kind, nullptr, nullptr};
+    LISA_TRY(lisa_hip_check(hipEventCreate(&rec.start), "hipEventCreate"));
+    LISA_TRY(lisa_hip_check(hipEventCreate(&rec.stop), "hipEventCreate"));
+    d->prof->push_back(rec);
+    // global work sizes are in work-items
+    const hipError_t e = hipExtModuleLaunchKernel(f->fn, gx * tx, gy * ty, gz * tz, tx, ty, tz, 0, d->stream, args,
+                                                  nullptr, rec.start, rec.stop, 0);
+    if (e != hipSuccess) return lisa_fail((int)e, "launch %s: %s", f->name.c_str(), hipGetErrorString(e));
+    return LISA_OK;
+  }
   const hipError_t e = hipModuleLaunchKernel(f->fn, gx, gy, gz, tx, ty, tz, 0, d->stream, args, nullptr);
   if (e != hipSuccess) return lisa_fail((int)e, "launch %s: %s", f->name.c_str(), hipGetErrorString(e));
   return LISA_OK;

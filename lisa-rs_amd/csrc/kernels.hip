@@ -10,6 +10,7 @@
 //   lisa_attn_merge_*     flash merge of the slices + output gate [F14]
 //   lisa_step_finalize    argmax finish + device-side token/position feedback [F5]
 //   lisa_synth_fill       seeded synthetic tensors
+//   lisa_copy_bytes       device-to-device copy
 //
 // Numerics: every expression below is written in the evaluation order the CPU
 // oracle (oracle/oracle.cpp) restates, with the helpers of lisa_numerics.h;
@@ -989,6 +990,16 @@ extern "C" __global__ __launch_bounds__(1024) void lisa_step_finalize(LisaFinali
     }
     if (p.pos) *p.pos = *p.pos + p.pos_advance;
   }
+}
+
+// ===========================================================================
+// device copy
+// ===========================================================================
+extern "C" __global__ __launch_bounds__(256) void lisa_copy_bytes(LisaCopyParams p) {
+  const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+  const uint4* src = static_cast<const uint4*>(p.src);
+  uint4* dst = static_cast<uint4*>(p.dst);
+  for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < p.n16; i += stride) dst[i] = src[i];
 }
 
 // ===========================================================================

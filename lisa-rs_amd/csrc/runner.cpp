@@ -116,10 +116,8 @@ struct LisaRunner {
   int64_t verify_base = -1;
   uint32_t mtp_position = 0;
   LisaGraph* step_graph = nullptr;
-  // per-launch event profiling of eager steps (lisa_runner_profile_step)
-  bool profiling = false;
-  std::vector<hipEvent_t> prof_events;
-  std::vector<int> prof_kinds;
+  // per-launch timing of eager steps (lisa_runner_profile_step)
+  std::vector<LisaProfRec> prof;
 };
 
 namespace {
@@ -569,13 +567,9 @@ int encode_mtp(LisaRunner* r, const uint16_t* cond) {
 }
 
 // Launch-kind tags of the per-kernel profile (LISA_KIND_* in lisa_hip.h).
+// Tags the launches that follow (until the next mark) with a profile kind.
 int prof_mark(LisaRunner* r, int kind) {
-  if (!r->profiling) return LISA_OK;
-  hipEvent_t e;
-  LISA_TRY(lisa_hip_check(hipEventCreate(&e), "hipEventCreate"));
-  LISA_TRY(lisa_hip_check(hipEventRecord(e, r->dev->stream), "hipEventRecord"));
-  r->prof_events.push_back(e);
-  r->prof_kinds.push_back(kind);
+  r->dev->prof_kind = kind;
   return LISA_OK;
 }
 
@@ -834,22 +828,25 @@ extern "C" int lisa_runner_profile_step(LisaRunner* r, uint32_t token, int32_t s
   }
   Ctx& c = r->tgt;
   LISA_TRY(upload_u32(r, c.tokens, &token, 1));
-  r->profiling = true;
+  r->prof.clear();
+  r->dev->prof = &r->prof;
   int rc = LISA_OK;
   for (int s = 0; s < steps && !rc; ++s) rc = encode_target(r, 1, false, true);
-  r->profiling = false;
+  r->dev->prof = nullptr;
+  r->dev->prof_kind = -1;
   if (!rc) rc = sync(r);
-  for (size_t i = 0; !rc && i + 1 < r->prof_events.size(); ++i) {
-    const int kind = r->prof_kinds[i];
-    if (kind < 0 || kind >= LISA_KIND_COUNT) continue;
+  for (const LisaProfRec& rec : r->prof) {
+    if (rc || rec.kind < 0 || rec.kind >= LISA_KIND_COUNT) continue;
     float ms = 0.0f;
-    rc = lisa_hip_check(hipEventElapsedTime(&ms, r->prof_events[i], r->prof_events[i + 1]), "hipEventElapsedTime");
-    kind_ms[kind] += ms;
-    kind_count[kind] += 1;
+    rc = lisa_hip_check(hipEventElapsedTime(&ms, rec.start, rec.stop), "hipEventElapsedTime");
+    kind_ms[rec.kind] += ms;
+    kind_count[rec.kind] += 1;
   }
-  for (hipEvent_t e : r->prof_events) (void)hipEventDestroy(e);
-  r->prof_events.clear();
-  r->prof_kinds.clear();
+  for (const LisaProfRec& rec : r->prof) {
+    (void)hipEventDestroy(rec.start);
+    (void)hipEventDestroy(rec.stop);
+  }
+  r->prof.clear();
   if (rc) return rc;
   r->position += (uint32_t)steps;
   return LISA_OK;
