@@ -145,7 +145,8 @@ int lisa_runner_forward_token_with_hidden(LisaRunner* r, uint32_t token, uint32_
 int lisa_runner_decode_greedy(LisaRunner* r, uint32_t token, int32_t steps, uint32_t* tokens_out);
 
 /* Per-kernel profile of `steps` eager M=1 steps from `token`: every launch is
- * bracketed by hipEvents on the device stream; kind_ms[k] / kind_count[k]
+ * timed by start/stop events attached to its dispatch (the kernel's execution
+ * window, as a kernel trace reports it); kind_ms[k] / kind_count[k]
  * receive the summed duration (ms) and number of launches of kind k. The
  * diagnostic counterpart of profile_token_m1_diagnostic (runner.rs:660-730). */
 enum {

@@ -86,7 +86,7 @@ static inline uint64_t lisa_tensor_id(int scope, int kind, int part) {
 }
 
 /* Builder-chosen distributions (BASELINE configs 0-2 fix the q4 ones):
- * q4 scales ~U(0.005,0.02), biases ~U(-0.1,0.1), nibbles uniform; RMSNorm
+ * q4 scales ~U(0.005,0.02), nibbles uniform, biases zero-mean (below); RMSNorm
  * gains 1+U(-0.1,0.1); conv1d weights U(-0.5,0.5); A_log U(-2,0);
  * dt_bias U(-1,1); GDN state N(0,0.01); conv history, KV cache and
  * activations N(0,1). */
@@ -94,5 +94,14 @@ static inline uint64_t lisa_tensor_id(int scope, int kind, int part) {
 #define LISA_SCALE_HI 0.02f
 #define LISA_BIAS_LO -0.1f
 #define LISA_BIAS_HI 0.1f
+
+/* Bias of a synthetic model group: zero-mean groups like an MLX-quantized
+ * checkpoint, b = bf16(s * (u - 7.5)) with s the group's bf16 scale and
+ * u ~ U(-1, 1) from the bias stream, so q*s + b spans [s(u-7.5), s(u+7.5)].
+ * (BASELINE config 0's biases U(-0.1, 0.1) give every weight a mean of about
+ * +0.09 and a logit vector dominated by one common-mode direction; the
+ * single-kernel tests keep those.) */
+#define LISA_MODEL_BIAS_CENTER 7.5f
+#define LISA_MODEL_BIAS_SPREAD 1.0f
 
 #endif /* LISA_MODEL_H */

@@ -1020,7 +1020,8 @@ extern "C" __global__ __launch_bounds__(256) void lisa_synth_fill(LisaSynthParam
         break;
       case LISA_FILL_SB: {
         const uint16_t s = lisa_f32_to_bf16(lisa_synth_value(p.key, i, LISA_DIST_UNIFORM, LISA_SCALE_LO, LISA_SCALE_HI));
-        const uint16_t b = lisa_f32_to_bf16(lisa_synth_value(p.key2, i, LISA_DIST_UNIFORM, LISA_BIAS_LO, LISA_BIAS_HI));
+        const float u = lisa_synth_value(p.key2, i, LISA_DIST_UNIFORM, -LISA_MODEL_BIAS_SPREAD, LISA_MODEL_BIAS_SPREAD);
+        const uint16_t b = lisa_f32_to_bf16(lisa_bf16_to_f32(s) * (u - LISA_MODEL_BIAS_CENTER));
         static_cast<uint32_t*>(p.out)[i] = (uint32_t)s | ((uint32_t)b << 16);
         break;
       }

@@ -278,8 +278,11 @@ Q4 make_q4(uint64_t seed, int scope, int kind, int n, int k) {
   synth_words(seed, lisa_tensor_id(scope, kind, 0), q.w.size(), q.w.data());
   synth_bf16(seed, lisa_tensor_id(scope, kind, 1), LISA_DIST_UNIFORM, LISA_SCALE_LO, LISA_SCALE_HI,
              q.s.size(), q.s.data());
-  synth_bf16(seed, lisa_tensor_id(scope, kind, 2), LISA_DIST_UNIFORM, LISA_BIAS_LO, LISA_BIAS_HI,
-             q.b.size(), q.b.data());
+  // zero-mean groups: b = bf16(s * (u - 7.5)), u ~ U(-1, 1) from the bias stream
+  std::vector<float> u(q.b.size());
+  synth_f32(seed, lisa_tensor_id(scope, kind, 2), LISA_DIST_UNIFORM, -LISA_MODEL_BIAS_SPREAD, LISA_MODEL_BIAS_SPREAD,
+            u.size(), u.data());
+  for (size_t i = 0; i < u.size(); ++i) q.b[i] = tobf(bf(q.s[i]) * (u[i] - LISA_MODEL_BIAS_CENTER));
   return q;
 }
 

@@ -80,6 +80,26 @@ def q4_linear(x_bf16, w, scales, biases, n, k, m=1, ksplit=1):
     return out.reshape(m, n)
 
 
+def residual(x_bf16, o_f32):
+    x = _c(x_bf16, np.uint16)
+    out = np.empty_like(x)
+    lib().orc_residual(p(x), p(_c(o_f32, np.float32)), x.size, p(out))
+    return out
+
+
+def embed(w, scales, biases, token, hidden=5120):
+    out = np.empty(hidden, np.uint16)
+    lib().orc_embed(p(_c(w, np.uint32)), p(_c(scales, np.uint16)), p(_c(biases, np.uint16)), token, hidden, p(out))
+    return out
+
+
+def silu_mul(g_f32, u_f32):
+    g = _c(g_f32, np.float32)
+    out = np.empty(g.size, np.uint16)
+    lib().orc_silu_mul(p(g), p(_c(u_f32, np.float32)), g.size, p(out))
+    return out
+
+
 def rms_norm(x_bf16, w_bf16):
     x = _c(x_bf16, np.uint16)
     out = np.empty_like(x)
