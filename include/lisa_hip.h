@@ -165,6 +165,15 @@ enum {
 };
 int lisa_runner_profile_step(LisaRunner* r, uint32_t token, int32_t steps, float* kind_ms, int32_t* kind_count);
 
+/* forward_prefill_with_progress (runner.rs:2129-2230): the `n` prompt tokens
+ * in chunks of `chunk` rows (<= 512, the reference's PREFILL_BATCH; 0 = 512)
+ * with q4 GEMMs (bf16 MFMA), batched GDN and attention; GDN/conv state and KV
+ * carry across chunks. argmax_out[n] (nullable) gets each position's greedy
+ * token, hidden_out (nullable) f32[n][5120] the hidden before the final norm.
+ * position += n. */
+int lisa_runner_forward_prefill(LisaRunner* r, const uint32_t* tokens, int32_t n, int32_t chunk,
+                                uint32_t* argmax_out, float* hidden_out);
+
 /* verify_block3_decode (runner.rs:734-909): M=3 pass with GDN/conv capture;
  * argmax[3]; hidden (nullable) f32[3][5120]; logits (nullable) f32[3][vocab].
  * position += 3 until commit. */

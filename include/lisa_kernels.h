@@ -97,7 +97,7 @@ typedef struct LisaGdnParams {
   float* y_out;    /* nullable: pre-norm readout [M][6144] */
   float q_scale, k_scale;
   uint32_t capture;
-  uint32_t pad0;
+  uint32_t m_rows; /* lisa_gdn_recurrence_rows: number of rows (time steps) */
 } LisaGdnParams;
 
 /* ---- split-K decode attention --------------------------------------------
@@ -117,6 +117,11 @@ typedef struct LisaAttnParams {
   uint16_t* gated;     /* [M][6144] bf16 */
   uint32_t capacity;
   uint32_t s_max;
+  /* *_rows (prefill) kernels: normalized rotated queries bf16 [m][24][256]
+   * written by lisa_attn_store_rows, and the row count */
+  uint16_t* query;
+  uint32_t m_rows;
+  uint32_t pad0;
 } LisaAttnParams;
 
 /* ---- argmax finish + device-side step bookkeeping ------------------------
@@ -156,6 +161,55 @@ typedef struct LisaSynthParams {
   uint32_t capacity;
   uint32_t filled;
 } LisaSynthParams;
+
+/* ---- batched prefill ------------------------------------------------------
+ * lisa_q4_gemm: C[m][n] (f32, row stride ldc) = A[m][k] (bf16) . deq(W)[n][k]
+ * with deq = bf16(fma(scale, q, bias)) (gemm.metal:238-266), bf16 MFMA with f32
+ * accumulation. Grid (ceil(n/128), ceil(m/128)) x 256; k multiple of 64. */
+typedef struct LisaGemmParams {
+  const uint16_t* a;
+  const uint32_t* w;
+  const uint32_t* sb;
+  float* c;
+  uint32_t m, n, k, ldc;
+} LisaGemmParams;
+
+/* lisa_rows: per-row kernels of the prefill, grid (x, m) x 256. */
+enum {
+  LISA_ROWS_EMBED = 0,   /* r_out[t] = q4 embedding row of tokens[t] (bf16) */
+  LISA_ROWS_NORM = 1,    /* x_out[t] = RMSNorm(h_in[t]) */
+  LISA_ROWS_RESNORM = 2, /* r = bf16(h_in + bf16(o_in)) -> r_out; x_out = RMSNorm(r) */
+  LISA_ROWS_SILU = 3,    /* act[t][j] = bf16(silu(bf16 g) * bf16 u), j < width */
+  LISA_ROWS_ARGMAX = 4   /* argmax_out[t] = argmax over logits[t][0..vocab) (lowest index) */
+};
+typedef struct LisaRowsParams {
+  const uint16_t* h_in;
+  const float* o_in;
+  const uint16_t* norm_w;
+  uint16_t* r_out;
+  uint16_t* x_out;
+  const uint32_t* tokens;
+  const uint32_t* emb_w;
+  const uint32_t* emb_sb;
+  const float* g_in;
+  const float* u_in;
+  uint16_t* act_out;
+  const float* logits;
+  uint32_t* argmax_out;
+  uint32_t width; /* SILU row width; ARGMAX vocabulary */
+  uint32_t mode;
+} LisaRowsParams;
+
+/* lisa_gdn_conv_rows: causal conv + SiLU over m rows per channel with the
+ * carried history, grid ceil(10240/256) x 256. */
+typedef struct LisaConvRowsParams {
+  const float* qkv;        /* f32 [m][10240] */
+  const uint16_t* conv_w;  /* bf16 [10240][4] */
+  uint16_t* conv_state;    /* bf16 [3][10240], updated */
+  float* conv_out;         /* f32 [m][10240] */
+  uint32_t m_rows;
+  uint32_t pad0;
+} LisaConvRowsParams;
 
 /* ---- device copy (norm.metal:109-130 copy_bytes) ---------------------------
  * Kernel: lisa_copy_bytes, grid-stride over 16-byte units; src and dst 16-byte

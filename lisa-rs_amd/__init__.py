@@ -78,14 +78,35 @@ class GdnParams(C.Structure):
                 ("a_log", C.c_uint64), ("dt_bias", C.c_uint64), ("norm_w", C.c_uint64),
                 ("state", C.c_uint64), ("slots", C.c_uint64), ("slot_stride", C.c_uint64),
                 ("gated", C.c_uint64), ("y_out", C.c_uint64), ("q_scale", C.c_float), ("k_scale", C.c_float),
-                ("capture", C.c_uint32), ("pad0", C.c_uint32)]
+                ("capture", C.c_uint32), ("m_rows", C.c_uint32)]
 
 
 class AttnParams(C.Structure):
     _fields_ = [("q_proj", C.c_uint64), ("k_raw", C.c_uint64), ("v_raw", C.c_uint64),
                 ("q_norm_w", C.c_uint64), ("k_norm_w", C.c_uint64), ("key_cache", C.c_uint64),
                 ("value_cache", C.c_uint64), ("part_o", C.c_uint64), ("part_ml", C.c_uint64),
-                ("pos", C.c_uint64), ("gated", C.c_uint64), ("capacity", C.c_uint32), ("s_max", C.c_uint32)]
+                ("pos", C.c_uint64), ("gated", C.c_uint64), ("capacity", C.c_uint32), ("s_max", C.c_uint32),
+                ("query", C.c_uint64), ("m_rows", C.c_uint32), ("pad0", C.c_uint32)]
+
+
+class GemmParams(C.Structure):
+    _fields_ = [("a", C.c_uint64), ("w", C.c_uint64), ("sb", C.c_uint64), ("c", C.c_uint64),
+                ("m", C.c_uint32), ("n", C.c_uint32), ("k", C.c_uint32), ("ldc", C.c_uint32)]
+
+
+ROWS_EMBED, ROWS_NORM, ROWS_RESNORM, ROWS_SILU, ROWS_ARGMAX = range(5)
+
+
+class RowsParams(C.Structure):
+    _fields_ = [("h_in", C.c_uint64), ("o_in", C.c_uint64), ("norm_w", C.c_uint64), ("r_out", C.c_uint64),
+                ("x_out", C.c_uint64), ("tokens", C.c_uint64), ("emb_w", C.c_uint64), ("emb_sb", C.c_uint64),
+                ("g_in", C.c_uint64), ("u_in", C.c_uint64), ("act_out", C.c_uint64), ("logits", C.c_uint64),
+                ("argmax_out", C.c_uint64), ("width", C.c_uint32), ("mode", C.c_uint32)]
+
+
+class ConvRowsParams(C.Structure):
+    _fields_ = [("qkv", C.c_uint64), ("conv_w", C.c_uint64), ("conv_state", C.c_uint64), ("conv_out", C.c_uint64),
+                ("m_rows", C.c_uint32), ("pad0", C.c_uint32)]
 
 
 class SynthParams(C.Structure):
@@ -167,6 +188,7 @@ _SIGS = {
     "lisa_runner_forward_token_decode": (C.c_int, [_P, C.c_uint32, C.POINTER(C.c_uint32), _P]),
     "lisa_runner_forward_token_with_hidden": (C.c_int, [_P, C.c_uint32, C.POINTER(C.c_uint32), _P, _P]),
     "lisa_runner_decode_greedy": (C.c_int, [_P, C.c_uint32, C.c_int32, _P]),
+    "lisa_runner_forward_prefill": (C.c_int, [_P, _P, C.c_int32, C.c_int32, _P, _P]),
     "lisa_runner_profile_step": (C.c_int, [_P, C.c_uint32, C.c_int32, _P, _P]),
     "lisa_runner_verify_block3": (C.c_int, [_P, _P, _P, _P, _P]),
     "lisa_runner_commit_verified_prefix": (C.c_int, [_P, C.c_int32]),
@@ -381,6 +403,16 @@ class Runner:
         logits = np.empty(self.vocab, np.float32)
         _check(lib().lisa_runner_forward_token_with_hidden(self.h, token, C.byref(am), _ptr(hidden), _ptr(logits)))
         return int(am.value), hidden, logits
+
+    def forward_prefill(self, tokens, chunk: int = 0, want_hidden: bool = False):
+        """forward_prefill_with_progress (runner.rs:2129-2230): per-position
+        argmax (and hidden f32[n][5120]) of the prompt; position += n."""
+        t = np.ascontiguousarray(tokens, dtype=np.uint32)
+        am = np.zeros(t.size, np.uint32)
+        hidden = np.empty((t.size, HIDDEN), np.float32) if want_hidden else None
+        _check(lib().lisa_runner_forward_prefill(self.h, _ptr(t), t.size, chunk, _ptr(am),
+                                                 _ptr(hidden) if want_hidden else None))
+        return (am, hidden) if want_hidden else am
 
     def decode_greedy(self, token: int, steps: int) -> np.ndarray:
         out = np.zeros(steps, np.uint32)

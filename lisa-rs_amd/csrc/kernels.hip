@@ -11,6 +11,8 @@
 //   lisa_step_finalize    argmax finish + device-side token/position feedback [F5]
 //   lisa_synth_fill       seeded synthetic tensors
 //   lisa_copy_bytes       device-to-device copy
+//   lisa_q4_gemm, lisa_rows, lisa_gdn_conv_rows, lisa_gdn_recurrence_rows,
+//   lisa_attn_{store,partial,merge}_rows   batched prefill [F1 GEMM, F4-F14 rows forms]
 //
 // Numerics: every expression below is written in the evaluation order the CPU
 // oracle (oracle/oracle.cpp) restates, with the helpers of lisa_numerics.h;
@@ -678,8 +680,10 @@ QMV_KERNEL_EPI(5120, 3, LISA_PRO_RESNORM, resnorm, LISA_EPI_ARGMAX, argmax)
 // RMSNorm (gdn.metal:367-391). One workgroup per value head, 512 threads:
 // thread (v, q) = (tid/4, tid%4) owns state row v, columns [32q, 32q+32).
 // ===========================================================================
+// M = 0: the row count comes from p.m_rows (prefill).
 template <int M>
 DEV void gdn_body(const LisaGdnParams& p) {
+  const int rows = M ? M : (int)p.m_rows;
   const int h = blockIdx.x, kh = h / (LISA_GDN_VH / LISA_GDN_KH);
   const int tid = threadIdx.x, v = tid >> 2, q = tid & 3, lane = tid & 63, wave = tid >> 6;
   __shared__ float qn[128], kn[128], ybuf[128], sc[4];
@@ -690,7 +694,7 @@ DEV void gdn_body(const LisaGdnParams& p) {
     const float4 f = reinterpret_cast<const float4*>(srow)[i];
     S[4 * i] = f.x; S[4 * i + 1] = f.y; S[4 * i + 2] = f.z; S[4 * i + 3] = f.w;
   }
-  for (int t = 0; t < M; ++t) {
+  for (int t = 0; t < rows; ++t) {
     const float* co = p.conv_out + (size_t)t * LISA_GDN_CONV_DIM;
     if (wave < 2) {
       // q (wave 0) / k (wave 1) RMS with tree128, scaled 1/128 and 1/sqrt(128)
@@ -727,7 +731,7 @@ DEV void gdn_body(const LisaGdnParams& p) {
     py = py + xor_lane<1>(py);
     py = py + xor_lane<2>(py);
     if (q == 0) ybuf[v] = lisa_bf16r(py);
-    if (p.capture && p.slots && t + 1 < M) {
+    if (p.capture && p.slots && t + 1 < rows) {
       float4* dst = reinterpret_cast<float4*>(p.slots + (size_t)t * p.slot_stride + (size_t)h * 128 * 128 +
                                               (size_t)v * 128 + 32 * q);
 #pragma unroll
@@ -757,6 +761,7 @@ DEV void gdn_body(const LisaGdnParams& p) {
 
 extern "C" __global__ __launch_bounds__(512) void lisa_gdn_recurrence_m1(LisaGdnParams p) { gdn_body<1>(p); }
 extern "C" __global__ __launch_bounds__(512) void lisa_gdn_recurrence_m3(LisaGdnParams p) { gdn_body<3>(p); }
+extern "C" __global__ __launch_bounds__(512) void lisa_gdn_recurrence_rows(LisaGdnParams p) { gdn_body<0>(p); }
 
 // ===========================================================================
 // split-K decode attention
@@ -787,6 +792,52 @@ DEV void head_norm_rope_wave(const float* raw, const uint16_t* w, uint32_t pos, 
     out[0] = lisa_bf16r(n[0] * c + other * s);
 #pragma unroll
   for (int j = 1; j < 4; ++j) out[j] = lisa_bf16r(n[j]);
+}
+
+// Scores of one (row, head) over a slice of n cached tokens by one wave (lane =
+// token): q.k with four accumulators over d mod 8 pairs, /16, slice max,
+// p = exp2(log2e (score - max)), denominator tree64 (attention.metal:550-604).
+DEV void slice_scores(const float* qh, const uint16_t* Kt, int kp, int n, int lane, float* pbrow, float* ml) {
+  float score = -INFINITY;
+  if (lane < n) {
+    const uint16_t* kr = Kt + lane * kp;
+    float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
+#pragma unroll 4
+    for (int d = 0; d < LISA_ATT_HD; d += 8) {
+      const uint4 kk = *reinterpret_cast<const uint4*>(kr + d);
+      const float4 qa = *reinterpret_cast<const float4*>(qh + d);
+      const float4 qb = *reinterpret_cast<const float4*>(qh + d + 4);
+      a0 = lisa_fma(qa.x, lo_bf(kk.x), a0);
+      a1 = lisa_fma(qa.y, hi_bf(kk.x), a1);
+      a2 = lisa_fma(qa.z, lo_bf(kk.y), a2);
+      a3 = lisa_fma(qa.w, hi_bf(kk.y), a3);
+      a0 = lisa_fma(qb.x, lo_bf(kk.z), a0);
+      a1 = lisa_fma(qb.y, hi_bf(kk.z), a1);
+      a2 = lisa_fma(qb.z, lo_bf(kk.w), a2);
+      a3 = lisa_fma(qb.w, hi_bf(kk.w), a3);
+    }
+    score = ((a0 + a1) + (a2 + a3)) * 0.0625f;
+  }
+  const float mx = max64(score);
+  const float pv = (lane < n) ? lisa_exp2f(1.4426950408889634f * (score - mx)) : 0.0f;
+  const float den = tree64(pv);
+  pbrow[lane] = pv;
+  if (lane == 0) {
+    ml[0] = mx;
+    ml[1] = den;
+  }
+}
+
+// P.V of one row over the slice for the 6 heads of a KV head; thread = output
+// dimension, tokens in order.
+DEV void slice_pv(const float* pb6, const uint16_t* Vt, int n, int tid, float (&acc)[6]) {
+#pragma unroll
+  for (int i = 0; i < 6; ++i) acc[i] = 0.0f;
+  for (int tok = 0; tok < n; ++tok) {
+    const float vv = bf2f(Vt[tok * LISA_ATT_HD + tid]);
+#pragma unroll
+    for (int i = 0; i < 6; ++i) acc[i] = lisa_fma(pb6[i * LISA_ATT_SLICE + tok], vv, acc[i]);
+  }
 }
 
 template <int M>
@@ -845,36 +896,8 @@ DEV void attn_partial_body(const LisaAttnParams& p) {
     const uint32_t ctx = base + t + 1;
     if (ctx <= t0) continue;
     const int n = (int)min((uint32_t)T, ctx - t0);
-    float score = -INFINITY;
-    if (lane < n) {
-      const float* qh = qv + (t * 6 + i) * HD;
-      const uint16_t* kr = Kt + lane * KP;
-      float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
-#pragma unroll 4
-      for (int d = 0; d < HD; d += 8) {
-        const uint4 kk = *reinterpret_cast<const uint4*>(kr + d);
-        const float4 qa = *reinterpret_cast<const float4*>(qh + d);
-        const float4 qb = *reinterpret_cast<const float4*>(qh + d + 4);
-        a0 = lisa_fma(qa.x, lo_bf(kk.x), a0);
-        a1 = lisa_fma(qa.y, hi_bf(kk.x), a1);
-        a2 = lisa_fma(qa.z, lo_bf(kk.y), a2);
-        a3 = lisa_fma(qa.w, hi_bf(kk.y), a3);
-        a0 = lisa_fma(qb.x, lo_bf(kk.z), a0);
-        a1 = lisa_fma(qb.y, hi_bf(kk.z), a1);
-        a2 = lisa_fma(qb.z, lo_bf(kk.w), a2);
-        a3 = lisa_fma(qb.w, hi_bf(kk.w), a3);
-      }
-      score = ((a0 + a1) + (a2 + a3)) * 0.0625f;
-    }
-    const float mx = max64(score);
-    const float pv = (lane < n) ? lisa_exp2f(1.4426950408889634f * (score - mx)) : 0.0f;
-    const float den = tree64(pv);
-    pb[(t * 6 + i) * T + lane] = pv;
-    if (lane == 0) {
-      float* ml = p.part_ml + (((size_t)t * LISA_ATT_QH + h) * p.s_max + s) * 2;
-      ml[0] = mx;
-      ml[1] = den;
-    }
+    slice_scores(qv + (t * 6 + i) * HD, Kt, KP, n, lane, pb + (t * 6 + i) * T,
+                 p.part_ml + (((size_t)t * LISA_ATT_QH + h) * p.s_max + s) * 2);
   }
   __syncthreads();
   // 5. P.V: thread = output dimension
@@ -883,13 +906,7 @@ DEV void attn_partial_body(const LisaAttnParams& p) {
     if (ctx <= t0) continue;
     const int n = (int)min((uint32_t)T, ctx - t0);
     float acc[6];
-#pragma unroll
-    for (int i = 0; i < 6; ++i) acc[i] = 0.0f;
-    for (int tok = 0; tok < n; ++tok) {
-      const float vv = bf2f(Vt[tok * HD + tid]);
-#pragma unroll
-      for (int i = 0; i < 6; ++i) acc[i] = lisa_fma(pb[(t * 6 + i) * T + tok], vv, acc[i]);
-    }
+    slice_pv(pb + t * 6 * T, Vt, n, tid, acc);
 #pragma unroll
     for (int i = 0; i < 6; ++i) {
       const int h = kvh * 6 + i;
@@ -932,6 +949,321 @@ extern "C" __global__ __launch_bounds__(256) void lisa_attn_partial_m1(LisaAttnP
 extern "C" __global__ __launch_bounds__(256) void lisa_attn_partial_m3(LisaAttnParams p) { attn_partial_body<3>(p); }
 extern "C" __global__ __launch_bounds__(256) void lisa_attn_merge_m1(LisaAttnParams p) { attn_merge_body<1>(p); }
 extern "C" __global__ __launch_bounds__(256) void lisa_attn_merge_m3(LisaAttnParams p) { attn_merge_body<3>(p); }
+
+// ===========================================================================
+// batched prefill (runner.rs:2129-2230)
+// ===========================================================================
+// q4 GEMM (gemm.metal:152-341 semantics): C[m][n] = sum_k A[m][k] * Wd[n][k],
+// Wd = bf16(fma(scale, q, bias)), bf16 MFMA 32x32x16 with f32 accumulation.
+// 128x128 output tile per workgroup, 64-wide K step (one q4 group): the tile's
+// A rows and dequantized W rows are staged in LDS (rows padded to 72 bf16 so the
+// 32 rows a fragment read spans fall on distinct banks); each wave computes a
+// 64x64 quarter as 2x2 MFMA blocks. The next K step's global loads are issued
+// before the current step's MFMAs.
+typedef __bf16 lisa_bf16x8 __attribute__((ext_vector_type(8)));
+typedef float lisa_f32x16 __attribute__((ext_vector_type(16)));
+
+constexpr int GEMM_BM = 128, GEMM_BN = 128, GEMM_PAD = 72;
+
+extern "C" __global__ __launch_bounds__(256) void lisa_q4_gemm(LisaGemmParams p) {
+  __shared__ __attribute__((aligned(16))) uint16_t As[GEMM_BM * GEMM_PAD];
+  __shared__ __attribute__((aligned(16))) uint16_t Ws[GEMM_BN * GEMM_PAD];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  const uint32_t m0 = blockIdx.y * GEMM_BM, n0 = blockIdx.x * GEMM_BN;
+  const uint32_t K = p.k, nk = K / 64;
+
+  // loaders: A as 4 x 16 B per thread (row u/8, 8-element chunk u%8); W as
+  // 16 B (32 nibbles) of row tid/2, half tid%2, plus that row's scale/bias word
+  const uint4* asrc[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int u = tid + 256 * i;
+    const uint32_t row = min(m0 + (uint32_t)(u >> 3), p.m - 1);
+    asrc[i] = reinterpret_cast<const uint4*>(p.a + (size_t)row * K) + (u & 7);
+  }
+  const uint32_t wrow = min(n0 + (uint32_t)(tid >> 1), p.n - 1);
+  const uint4* wsrc = reinterpret_cast<const uint4*>(p.w + (size_t)wrow * (K / 8)) + (tid & 1);
+  const uint32_t* sbsrc = p.sb + (size_t)wrow * (K / 64);
+
+  uint4 ra[4], rw;
+  uint32_t rsb;
+  auto load = [&](uint32_t step) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) ra[i] = asrc[i][step * 8];
+    rw = wsrc[step * 2];
+    rsb = sbsrc[step];
+  };
+
+  lisa_f32x16 acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+  load(0);
+  for (uint32_t step = 0; step < nk; ++step) {
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int u = tid + 256 * i;
+      *reinterpret_cast<uint4*>(&As[(u >> 3) * GEMM_PAD + (u & 7) * 8]) = ra[i];
+    }
+    {
+      const float sc = lo_bf(rsb), bi = hi_bf(rsb);
+      const uint32_t wd[4] = {rw.x, rw.y, rw.z, rw.w};
+      uint16_t* dst = &Ws[(tid >> 1) * GEMM_PAD + (tid & 1) * 32];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        float v[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[e] = lisa_fma(sc, (float)((wd[j] >> (4 * e)) & 0xfu), bi);
+        *reinterpret_cast<uint4*>(dst + 8 * j) =
+            make_uint4(lisa_f32x2_to_bf16x2(v[0], v[1]), lisa_f32x2_to_bf16x2(v[2], v[3]),
+                       lisa_f32x2_to_bf16x2(v[4], v[5]), lisa_f32x2_to_bf16x2(v[6], v[7]));
+      }
+    }
+    __syncthreads();
+    load(min(step + 1, nk - 1));
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      lisa_bf16x8 af[2], bf[2];
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        af[i] = *reinterpret_cast<const lisa_bf16x8*>(
+            &As[(wm * 64 + i * 32 + (lane & 31)) * GEMM_PAD + ks * 16 + 8 * (lane >> 5)]);
+        bf[i] = *reinterpret_cast<const lisa_bf16x8*>(
+            &Ws[(wn * 64 + i * 32 + (lane & 31)) * GEMM_PAD + ks * 16 + 8 * (lane >> 5)]);
+      }
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bf[j], acc[i][j], 0, 0, 0);
+    }
+  }
+  // C layout of a 32x32 block: element r of lane l is row 8(r/4) + 4(l/32) + r%4, column l%32
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const uint32_t col = n0 + wn * 64 + j * 32 + (lane & 31);
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const uint32_t row = m0 + wm * 64 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+        if (row < p.m && col < p.n) p.c[(size_t)row * p.ldc + col] = acc[i][j][r];
+      }
+    }
+}
+
+// Per-row kernels. NORM/RESNORM follow the q4 prologue's arithmetic exactly
+// (chunks of 8 per thread, same statistic), so a prefill row normalizes as a
+// decode step does.
+extern "C" __global__ __launch_bounds__(256) void lisa_rows(LisaRowsParams p) {
+  __shared__ float red[64];
+  const int tid = threadIdx.x, t = blockIdx.y;
+  switch (p.mode) {
+    case LISA_ROWS_EMBED: {
+      const uint32_t tok = p.tokens[t];
+      for (int c = tid; c < kSegChunks; c += 256) {
+        const uint32_t word = p.emb_w[(size_t)tok * (LISA_HIDDEN / 8) + c];
+        const uint32_t sb = p.emb_sb[(size_t)tok * (LISA_HIDDEN / 64) + (c >> 3)];
+        float v[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[e] = lisa_bf16r((float)((word >> (4 * e)) & 0xfu) * lo_bf(sb) + hi_bf(sb));
+        reinterpret_cast<uint4*>(p.r_out + (size_t)t * LISA_HIDDEN)[c] = pack_bf8(v);
+      }
+      break;
+    }
+    case LISA_ROWS_NORM:
+    case LISA_ROWS_RESNORM: {
+      const uint4* hs = reinterpret_cast<const uint4*>(p.h_in + (size_t)t * LISA_HIDDEN);
+      const uint4* os = reinterpret_cast<const uint4*>(p.o_in + (size_t)t * LISA_HIDDEN);
+      const uint4* ws = reinterpret_cast<const uint4*>(p.norm_w);
+      float v[3][8];
+      float ss = 0.0f;
+#pragma unroll
+      for (int i = 0; i < 3; ++i) {
+        const int c = min(tid + 256 * i, kSegChunks - 1);
+        const bool valid = tid + 256 * i < kSegChunks;
+        float hv[8];
+        unpack_bf8(hs[c], hv);
+        if (p.mode == LISA_ROWS_RESNORM) {
+          const uint4 o0 = os[2 * c], o1 = os[2 * c + 1];
+          const float ov[8] = {__uint_as_float(o0.x), __uint_as_float(o0.y), __uint_as_float(o0.z),
+                               __uint_as_float(o0.w), __uint_as_float(o1.x), __uint_as_float(o1.y),
+                               __uint_as_float(o1.z), __uint_as_float(o1.w)};
+#pragma unroll
+          for (int e = 0; e < 8; ++e) v[i][e] = lisa_bf16r(hv[e] + lisa_bf16r(ov[e]));
+        } else {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) v[i][e] = hv[e];
+        }
+        if (valid)
+#pragma unroll
+          for (int e = 0; e < 8; ++e) ss = ss + v[i][e] * v[i][e];
+      }
+      const float inv = seg_rms_inv(ss, red, tid);
+#pragma unroll
+      for (int i = 0; i < 3; ++i) {
+        const int c = tid + 256 * i;
+        if (c >= kSegChunks) continue;
+        float wv[8], x[8];
+        unpack_bf8(ws[c], wv);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) x[e] = lisa_bf16r((v[i][e] * inv) * wv[e]);
+        reinterpret_cast<uint4*>(p.x_out + (size_t)t * LISA_HIDDEN)[c] = pack_bf8(x);
+        if (p.mode == LISA_ROWS_RESNORM)
+          reinterpret_cast<uint4*>(p.r_out + (size_t)t * LISA_HIDDEN)[c] = pack_bf8(v[i]);
+      }
+      break;
+    }
+    case LISA_ROWS_SILU: {
+      // mlp.metal:11-16; blockIdx.x walks the row in 2048-wide pieces
+      const uint32_t j = blockIdx.x * 2048u + (uint32_t)tid * 8u;
+      if (j >= p.width) break;
+      const float* g = p.g_in + (size_t)t * p.width + j;
+      const float* u = p.u_in + (size_t)t * p.width + j;
+      float a[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) a[e] = lisa_bf16r(lisa_silu_exp2(lisa_bf16r(g[e])) * lisa_bf16r(u[e]));
+      *reinterpret_cast<uint4*>(p.act_out + (size_t)t * p.width + j) = pack_bf8(a);
+      break;
+    }
+    default: { /* ARGMAX: embed.metal:78-118, ties to the lowest index */
+      const float* lg = p.logits + (size_t)t * p.width;
+      float bv = -INFINITY;
+      uint32_t bi = 0xffffffffu;
+      for (uint32_t j = tid; j < p.width; j += 256)
+        if (better(lg[j], j, bv, bi)) { bv = lg[j]; bi = j; }
+      for (int msk = 1; msk < 64; msk <<= 1) {
+        const float ov = __shfl_xor(bv, msk, 64);
+        const uint32_t oi = (uint32_t)__shfl_xor((int)bi, msk, 64);
+        if (better(ov, oi, bv, bi)) { bv = ov; bi = oi; }
+      }
+      uint32_t* ri = reinterpret_cast<uint32_t*>(red + 32);
+      if ((tid & 63) == 0) { red[tid >> 6] = bv; ri[tid >> 6] = bi; }
+      __syncthreads();
+      if (tid == 0) {
+        for (int q = 1; q < 4; ++q)
+          if (better(red[q], ri[q], red[0], ri[0])) { red[0] = red[q]; ri[0] = ri[q]; }
+        p.argmax_out[t] = ri[0] == 0xffffffffu ? 0u : ri[0];
+      }
+      break;
+    }
+  }
+}
+
+// GDN causal conv + SiLU over m rows (gdn.metal:125-170 prefill form, 212-240
+// history update): thread = channel, rows in order, the arithmetic of the
+// decode conv epilogue.
+extern "C" __global__ __launch_bounds__(256) void lisa_gdn_conv_rows(LisaConvRowsParams p) {
+  const int C = LISA_GDN_CONV_DIM;
+  const int c = blockIdx.x * 256 + threadIdx.x;
+  if (c >= C) return;
+  float h0 = bf2f(p.conv_state[c]), h1 = bf2f(p.conv_state[C + c]), h2 = bf2f(p.conv_state[2 * C + c]);
+  float w[4];
+#pragma unroll
+  for (int tap = 0; tap < 4; ++tap) w[tap] = bf2f(p.conv_w[(size_t)c * 4 + tap]);
+  for (uint32_t t = 0; t < p.m_rows; ++t) {
+    const float x = lisa_bf16r(p.qkv[(size_t)t * C + c]);
+    float acc = 0.0f;
+    acc = acc + h0 * w[0];
+    acc = acc + h1 * w[1];
+    acc = acc + h2 * w[2];
+    acc = acc + x * w[3];
+    p.conv_out[(size_t)t * C + c] = lisa_bf16r(lisa_silu_exp(lisa_bf16r(acc)));
+    h0 = h1;
+    h1 = h2;
+    h2 = x;
+  }
+  p.conv_state[c] = lisa_f32_to_bf16(h0);
+  p.conv_state[C + c] = lisa_f32_to_bf16(h1);
+  p.conv_state[2 * C + c] = lisa_f32_to_bf16(h2);
+}
+
+// Prefill attention (attention.metal:364-480 semantics) in the decode path's
+// split-K form, so every row equals what a decode step at its position gives.
+// 1. K/V rows appended and queries normalized + rotated: grid (m, 7); y = 0
+//    handles the 4 KV heads, y = 1..6 four query heads each, one wave per head.
+extern "C" __global__ __launch_bounds__(256) void lisa_attn_store_rows(LisaAttnParams p) {
+  const int t = blockIdx.x, grp = blockIdx.y, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const uint32_t pos = *p.pos + t;
+  constexpr int HD = LISA_ATT_HD;
+  float o[4];
+  if (grp == 0) {
+    const int kvh = wave;
+    head_norm_rope_wave(p.k_raw + (size_t)t * LISA_ATT_KV_OUT + kvh * HD, p.k_norm_w, pos, lane, o);
+    const size_t off = ((size_t)kvh * p.capacity + pos) * HD;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int d = lane + 64 * j;
+      p.key_cache[off + d] = lisa_f32_to_bf16(o[j]);
+      p.value_cache[off + d] = lisa_f32_to_bf16(p.v_raw[(size_t)t * LISA_ATT_KV_OUT + kvh * HD + d]);
+    }
+  } else {
+    const int h = (grp - 1) * 4 + wave;
+    head_norm_rope_wave(p.q_proj + (size_t)t * LISA_ATT_Q_OUT + h * 512, p.q_norm_w, pos, lane, o);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) p.query[((size_t)t * LISA_ATT_QH + h) * HD + lane + 64 * j] = lisa_f32_to_bf16(o[j]);
+  }
+}
+
+// 2. slice partials: grid (s_max, 4, ceil(m / ATT_RB)); a workgroup takes one
+//    64-token slice of one KV head for ATT_RB rows.
+constexpr int ATT_RB = 4;
+extern "C" __global__ __launch_bounds__(256) void lisa_attn_partial_rows(LisaAttnParams p) {
+  constexpr int T = LISA_ATT_SLICE, HD = LISA_ATT_HD, KP = HD + 8;
+  const uint32_t base = *p.pos;
+  const int s = blockIdx.x, kvh = blockIdx.y, r0 = blockIdx.z * ATT_RB;
+  const int nr = min(ATT_RB, (int)p.m_rows - r0);
+  const uint32_t t0 = (uint32_t)s * T;
+  if (nr <= 0 || t0 >= base + (uint32_t)(r0 + nr)) return;
+  __shared__ __attribute__((aligned(16))) uint16_t Kt[T * KP];
+  __shared__ __attribute__((aligned(16))) uint16_t Vt[T * HD];
+  __shared__ __attribute__((aligned(16))) float qv[ATT_RB * 6 * HD];
+  __shared__ float pb[ATT_RB * 6 * T];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const size_t cache_base = (size_t)kvh * p.capacity * HD;
+  const int nrows = (int)min((uint32_t)T, base + (uint32_t)(r0 + nr) - t0);
+  for (int c = tid; c < nrows * (HD / 8); c += 256) {
+    const int row = c / (HD / 8), col = (c % (HD / 8)) * 8;
+    const size_t off = cache_base + (size_t)(t0 + row) * HD + col;
+    *reinterpret_cast<uint4*>(&Kt[row * KP + col]) = *reinterpret_cast<const uint4*>(p.key_cache + off);
+    *reinterpret_cast<uint4*>(&Vt[row * HD + col]) = *reinterpret_cast<const uint4*>(p.value_cache + off);
+  }
+  for (int e = tid; e < nr * 6 * HD; e += 256) {
+    const int tt = e / (6 * HD), i = (e / HD) % 6, d = e % HD;
+    qv[e] = bf2f(p.query[((size_t)(r0 + tt) * LISA_ATT_QH + kvh * 6 + i) * HD + d]);
+  }
+  __syncthreads();
+  for (int pr = wave; pr < nr * 6; pr += 4) {
+    const int tt = pr / 6, i = pr % 6, h = kvh * 6 + i, t = r0 + tt;
+    const uint32_t ctx = base + t + 1;
+    if (ctx <= t0) continue;
+    const int n = (int)min((uint32_t)T, ctx - t0);
+    slice_scores(qv + (tt * 6 + i) * HD, Kt, KP, n, lane, pb + (tt * 6 + i) * T,
+                 p.part_ml + (((size_t)t * LISA_ATT_QH + h) * p.s_max + s) * 2);
+  }
+  __syncthreads();
+  for (int tt = 0; tt < nr; ++tt) {
+    const int t = r0 + tt;
+    const uint32_t ctx = base + t + 1;
+    if (ctx <= t0) continue;
+    const int n = (int)min((uint32_t)T, ctx - t0);
+    float acc[6];
+    slice_pv(pb + tt * 6 * T, Vt, n, tid, acc);
+#pragma unroll
+    for (int i = 0; i < 6; ++i) {
+      const int h = kvh * 6 + i;
+      p.part_o[(((size_t)t * LISA_ATT_QH + h) * p.s_max + s) * HD + tid] = acc[i];
+    }
+  }
+}
+
+// 3. merge + output gate per (head, row): the decode merge, grid (24, m).
+extern "C" __global__ __launch_bounds__(256) void lisa_attn_merge_rows(LisaAttnParams p) { attn_merge_body<0>(p); }
 
 // ===========================================================================
 // argmax finish (runner.rs:1077-1095 on the device) + step bookkeeping

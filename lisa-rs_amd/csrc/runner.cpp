@@ -96,6 +96,9 @@ struct LisaRunner {
   LisaFunction *qmv[2][5][6] = {};  // [m3][K index][prologue mode]
   LisaFunction *qmv_epi[2][6][4] = {};  // K = 5120 with a fixed epilogue: [m3][prologue][epilogue]
   LisaFunction *gdn[2] = {}, *attn_part[2] = {}, *attn_merge[2] = {}, *finalize = nullptr, *synth = nullptr;
+  // batched prefill
+  LisaFunction *gemm = nullptr, *rows = nullptr, *conv_rows = nullptr, *gdn_rows = nullptr, *attn_store_rows = nullptr,
+               *attn_partial_rows = nullptr, *attn_merge_rows = nullptr;
   // memory
   LisaBuffer *weights = nullptr, *state = nullptr, *scratch = nullptr;
   std::vector<LayerDev> layers;
@@ -111,6 +114,17 @@ struct LisaRunner {
   uint16_t *key_cache = nullptr, *value_cache = nullptr;
   uint16_t *mtp_key = nullptr, *mtp_value = nullptr;
   Ctx tgt{}, drf{};
+  // prefill scratch, allocated at the first prefill call (runner.rs:378 sizes it
+  // for PREFILL_BATCH rows)
+  struct Prefill {
+    LisaBuffer* buf = nullptr;
+    uint32_t att_rows = 0;  // rows per attention sub-block (bounds the slice partials)
+    uint32_t *tokens = nullptr, *argmax = nullptr, *pos = nullptr;
+    uint16_t *H = nullptr, *X = nullptr, *gated = nullptr, *act = nullptr, *query = nullptr;
+    float *B = nullptr, *qkv = nullptr, *conv_out = nullptr, *z = nullptr, *a = nullptr, *b = nullptr;
+    float *q_proj = nullptr, *k_raw = nullptr, *v_raw = nullptr, *G = nullptr, *U = nullptr, *logits = nullptr;
+    float *part_o = nullptr, *part_ml = nullptr;
+  } pf;
   // host mirrors
   uint32_t position = 0;
   int64_t verify_base = -1;
@@ -672,6 +686,13 @@ extern "C" int lisa_runner_create(const LisaRunnerConfig* cfg, LisaRunner** out)
   }
   LISA_TRY(lisa_function_get(r->mod, "lisa_step_finalize", &r->finalize));
   LISA_TRY(lisa_function_get(r->mod, "lisa_synth_fill", &r->synth));
+  LISA_TRY(lisa_function_get(r->mod, "lisa_q4_gemm", &r->gemm));
+  LISA_TRY(lisa_function_get(r->mod, "lisa_rows", &r->rows));
+  LISA_TRY(lisa_function_get(r->mod, "lisa_gdn_conv_rows", &r->conv_rows));
+  LISA_TRY(lisa_function_get(r->mod, "lisa_gdn_recurrence_rows", &r->gdn_rows));
+  LISA_TRY(lisa_function_get(r->mod, "lisa_attn_store_rows", &r->attn_store_rows));
+  LISA_TRY(lisa_function_get(r->mod, "lisa_attn_partial_rows", &r->attn_partial_rows));
+  LISA_TRY(lisa_function_get(r->mod, "lisa_attn_merge_rows", &r->attn_merge_rows));
   r->s_max = ((uint32_t)cfg->capacity + LISA_ATT_SLICE - 1) / LISA_ATT_SLICE;
 
   Arena wa;
@@ -714,8 +735,10 @@ extern "C" void lisa_runner_free(LisaRunner* r) {
     for (auto& b : a)
       for (LisaFunction* f : b) delete f;
   for (LisaFunction* f : {r->gdn[0], r->gdn[1], r->attn_part[0], r->attn_part[1], r->attn_merge[0], r->attn_merge[1],
-                          r->finalize, r->synth})
+                          r->finalize, r->synth, r->gemm, r->rows, r->conv_rows, r->gdn_rows, r->attn_store_rows,
+                          r->attn_partial_rows, r->attn_merge_rows})
     delete f;
+  lisa_buffer_free(r->pf.buf);
   lisa_buffer_free(r->scratch);
   lisa_buffer_free(r->state);
   lisa_buffer_free(r->weights);
@@ -1015,5 +1038,228 @@ extern "C" int lisa_mtp_trim_state(LisaRunner* r, int32_t count) {
     return lisa_fail(LISA_E_ARG, "cannot trim %d MTP positions from %u", count, r->mtp_position);
   r->mtp_position -= (uint32_t)count;
   LISA_TRY(write_pos(r, r->drf, r->mtp_position));
+  return sync(r);
+}
+
+// =============================================================================
+// batched prefill: forward_prefill_with_progress (runner.rs:2129-2230)
+// =============================================================================
+namespace {
+
+constexpr uint32_t kPrefillRows = 512;  // PREFILL_BATCH (runner.rs:51)
+
+void plan_prefill(LisaRunner* r, Arena& A) {
+  auto& P = r->pf;
+  const size_t c = kPrefillRows;
+  P.tokens = A.take<uint32_t>(c);
+  P.argmax = A.take<uint32_t>(c);
+  P.pos = A.take<uint32_t>(c + 1);
+  P.H = A.take<uint16_t>(c * LISA_HIDDEN);
+  P.X = A.take<uint16_t>(c * LISA_HIDDEN);
+  P.B = A.take<float>(c * LISA_HIDDEN);
+  P.qkv = A.take<float>(c * LISA_GDN_CONV_DIM);
+  P.conv_out = A.take<float>(c * LISA_GDN_CONV_DIM);
+  P.z = A.take<float>(c * LISA_GDN_VALUE_DIM);
+  P.a = A.take<float>(c * LISA_GDN_VH);
+  P.b = A.take<float>(c * LISA_GDN_VH);
+  P.gated = A.take<uint16_t>(c * LISA_ATT_OUT);
+  P.q_proj = A.take<float>(c * LISA_ATT_Q_OUT);
+  P.k_raw = A.take<float>(c * LISA_ATT_KV_OUT);
+  P.v_raw = A.take<float>(c * LISA_ATT_KV_OUT);
+  P.query = A.take<uint16_t>(c * LISA_ATT_OUT);
+  P.G = A.take<float>(c * LISA_INTER);
+  P.U = A.take<float>(c * LISA_INTER);
+  P.act = A.take<uint16_t>(c * LISA_INTER);
+  P.logits = A.take<float>(c * (size_t)r->cfg.vocab);
+  // slice partials of one attention sub-block: at most ~1 GiB
+  const size_t per_row = (size_t)LISA_ATT_QH * r->s_max * (LISA_ATT_HD + 2) * sizeof(float);
+  uint32_t ar = (uint32_t)std::min<size_t>(kPrefillRows, std::max<size_t>(4, (size_t(1) << 30) / per_row));
+  P.att_rows = ar & ~3u;
+  P.part_o = A.take<float>((size_t)P.att_rows * LISA_ATT_QH * r->s_max * LISA_ATT_HD);
+  P.part_ml = A.take<float>((size_t)P.att_rows * LISA_ATT_QH * r->s_max * 2);
+}
+
+int ensure_prefill(LisaRunner* r) {
+  if (r->pf.buf) return LISA_OK;
+  Arena a;
+  plan_prefill(r, a);
+  LisaBuffer* buf = nullptr;
+  LISA_TRY(lisa_buffer_alloc(r->dev, a.used, &buf));
+  r->pf.buf = buf;
+  a.base = (char*)buf->ptr;
+  a.used = 0;
+  plan_prefill(r, a);
+  return LISA_OK;
+}
+
+// C[m][w.n] = A[m][w.k] . deq(w)^T
+int launch_gemm(LisaRunner* r, const uint16_t* a, uint32_t m, const Q4Dev& w, float* c) {
+  LisaGemmParams g{};
+  g.a = a;
+  g.w = w.w;
+  g.sb = w.sb;
+  g.c = c;
+  g.m = m;
+  g.n = w.n;
+  g.k = w.k;
+  g.ldc = w.n;
+  return lisa_launch(r->dev, r->gemm, &g, sizeof g, (w.n + 127) / 128, (m + 127) / 128, 1, 256, 1, 1);
+}
+
+int launch_rows(LisaRunner* r, LisaRowsParams& p, uint32_t gx, uint32_t m) {
+  return lisa_launch(r->dev, r->rows, &p, sizeof p, gx, m, 1, 256, 1, 1);
+}
+
+int rows_norm(LisaRunner* r, uint32_t m, const uint16_t* h, const float* o, const uint16_t* w, uint16_t* r_out,
+              uint16_t* x_out) {
+  LisaRowsParams p{};
+  p.mode = o ? LISA_ROWS_RESNORM : LISA_ROWS_NORM;
+  p.h_in = h;
+  p.o_in = o;
+  p.norm_w = w;
+  p.r_out = r_out;
+  p.x_out = x_out;
+  return launch_rows(r, p, 1, m);
+}
+
+// One prefill chunk of m rows at positions [r->position, r->position + m).
+int prefill_chunk(LisaRunner* r, uint32_t m) {
+  auto& P = r->pf;
+  const float inv = 1.0f / lisa_sqrt((float)LISA_GDN_HD);  // runner.rs:1316-1317
+  {
+    LisaRowsParams e{};
+    e.mode = LISA_ROWS_EMBED;
+    e.tokens = P.tokens;
+    e.emb_w = r->embed.w;
+    e.emb_sb = r->embed.sb;
+    e.r_out = P.H;
+    LISA_TRY(launch_rows(r, e, 1, m));
+  }
+  for (int i = 0; i < r->cfg.layers; ++i) {
+    const LayerDev& l = r->layers[i];
+    LISA_TRY(rows_norm(r, m, P.H, i == 0 ? nullptr : P.B, l.input_norm, P.H, P.X));
+    if (!l.attention) {
+      const int si = l.state_index;
+      LISA_TRY(launch_gemm(r, P.X, m, l.qkv, P.qkv));
+      LISA_TRY(launch_gemm(r, P.X, m, l.z, P.z));
+      LISA_TRY(launch_gemm(r, P.X, m, l.a, P.a));
+      LISA_TRY(launch_gemm(r, P.X, m, l.b, P.b));
+      LisaConvRowsParams cv{};
+      cv.qkv = P.qkv;
+      cv.conv_w = l.conv_w;
+      cv.conv_state = r->conv_state + (size_t)si * 3 * LISA_GDN_CONV_DIM;
+      cv.conv_out = P.conv_out;
+      cv.m_rows = m;
+      LISA_TRY(lisa_launch(r->dev, r->conv_rows, &cv, sizeof cv, (LISA_GDN_CONV_DIM + 255) / 256, 1, 1, 256, 1, 1));
+      LisaGdnParams g{};
+      g.conv_out = P.conv_out;
+      g.z = P.z;
+      g.a = P.a;
+      g.b = P.b;
+      g.a_log = l.a_log;
+      g.dt_bias = l.dt_bias;
+      g.norm_w = l.gnorm;
+      g.state = r->gdn_state + (size_t)si * LISA_GDN_STATE;
+      g.gated = P.gated;
+      g.q_scale = inv * inv;
+      g.k_scale = inv;
+      g.m_rows = m;
+      LISA_TRY(lisa_launch(r->dev, r->gdn_rows, &g, sizeof g, LISA_GDN_VH, 1, 1, 512, 1, 1));
+      LISA_TRY(launch_gemm(r, P.gated, m, l.out, P.B));
+    } else {
+      LISA_TRY(launch_gemm(r, P.X, m, l.q, P.q_proj));
+      LISA_TRY(launch_gemm(r, P.X, m, l.k, P.k_raw));
+      LISA_TRY(launch_gemm(r, P.X, m, l.v, P.v_raw));
+      const size_t off = (size_t)l.cache_index * LISA_ATT_KVH * r->cfg.capacity * LISA_ATT_HD;
+      LisaAttnParams a{};
+      a.q_proj = P.q_proj;
+      a.k_raw = P.k_raw;
+      a.v_raw = P.v_raw;
+      a.q_norm_w = l.q_norm;
+      a.k_norm_w = l.k_norm;
+      a.key_cache = r->key_cache + off;
+      a.value_cache = r->value_cache + off;
+      a.part_o = P.part_o;
+      a.part_ml = P.part_ml;
+      a.pos = P.pos;
+      a.gated = P.gated;
+      a.capacity = (uint32_t)r->cfg.capacity;
+      a.s_max = r->s_max;
+      a.query = P.query;
+      a.m_rows = m;
+      LISA_TRY(lisa_launch(r->dev, r->attn_store_rows, &a, sizeof a, m, 7, 1, 256, 1, 1));
+      for (uint32_t r0 = 0; r0 < m; r0 += P.att_rows) {
+        const uint32_t ms = std::min(P.att_rows, m - r0);
+        LisaAttnParams b = a;
+        b.q_proj = P.q_proj + (size_t)r0 * LISA_ATT_Q_OUT;
+        b.query = P.query + (size_t)r0 * LISA_ATT_OUT;
+        b.gated = P.gated + (size_t)r0 * LISA_ATT_OUT;
+        b.pos = P.pos + 1 + r0 / P.att_rows;
+        b.m_rows = ms;
+        const uint32_t slices = (r->position + r0 + ms + LISA_ATT_SLICE - 1) / LISA_ATT_SLICE;
+        LISA_TRY(lisa_launch(r->dev, r->attn_partial_rows, &b, sizeof b, slices, LISA_ATT_KVH, (ms + 3) / 4, 256, 1,
+                             1));
+        LISA_TRY(lisa_launch(r->dev, r->attn_merge_rows, &b, sizeof b, LISA_ATT_QH, ms, 1, 256, 1, 1));
+      }
+      LISA_TRY(launch_gemm(r, P.gated, m, l.o, P.B));
+    }
+    LISA_TRY(rows_norm(r, m, P.H, P.B, l.post_norm, P.H, P.X));
+    LISA_TRY(launch_gemm(r, P.X, m, l.gate, P.G));
+    LISA_TRY(launch_gemm(r, P.X, m, l.up, P.U));
+    LisaRowsParams sw{};
+    sw.mode = LISA_ROWS_SILU;
+    sw.g_in = P.G;
+    sw.u_in = P.U;
+    sw.act_out = P.act;
+    sw.width = LISA_INTER;
+    LISA_TRY(launch_rows(r, sw, (LISA_INTER + 2047) / 2048, m));
+    LISA_TRY(launch_gemm(r, P.act, m, l.down, P.B));
+  }
+  LISA_TRY(rows_norm(r, m, P.H, P.B, r->final_norm, P.H, P.X));
+  LISA_TRY(launch_gemm(r, P.X, m, r->head, P.logits));
+  LisaRowsParams am{};
+  am.mode = LISA_ROWS_ARGMAX;
+  am.logits = P.logits;
+  am.width = (uint32_t)r->cfg.vocab;
+  am.argmax_out = P.argmax;
+  return launch_rows(r, am, 1, m);
+}
+
+}  // namespace
+
+extern "C" int lisa_runner_forward_prefill(LisaRunner* r, const uint32_t* tokens, int32_t n, int32_t chunk,
+                                           uint32_t* argmax_out, float* hidden_out) {
+  if (!r || n < 0 || (n && !tokens)) return lisa_fail(LISA_E_ARG, "lisa_runner_forward_prefill: bad argument");
+  for (int32_t i = 0; i < n; ++i) LISA_TRY(check_token(r, tokens[i]));
+  if (!n) return LISA_OK;
+  if (r->position + (uint32_t)n > (uint32_t)r->cfg.capacity)
+    return lisa_fail(LISA_E_CAPACITY, "KV capacity %d exhausted by prefill of %d tokens", r->cfg.capacity, n);
+  const uint32_t rows = (chunk <= 0 || (uint32_t)chunk > kPrefillRows) ? kPrefillRows : (uint32_t)chunk;
+  LISA_TRY(ensure_prefill(r));
+  auto& P = r->pf;
+  std::vector<uint16_t> h;
+  for (uint32_t b = 0; b < (uint32_t)n; b += rows) {
+    const uint32_t m = std::min(rows, (uint32_t)n - b);
+    LISA_TRY(upload_u32(r, P.tokens, tokens + b, m));
+    std::vector<uint32_t> pos(1 + (m + P.att_rows - 1) / P.att_rows);
+    pos[0] = r->position;
+    for (size_t j = 1; j < pos.size(); ++j) pos[j] = r->position + (uint32_t)(j - 1) * P.att_rows;
+    LISA_TRY(upload_u32(r, P.pos, pos.data(), pos.size()));
+    LISA_TRY(prefill_chunk(r, m));
+    if (argmax_out)
+      LISA_TRY(lisa_hip_check(hipMemcpyAsync(argmax_out + b, P.argmax, (size_t)m * 4, hipMemcpyDeviceToHost,
+                                             r->dev->stream), "D2H argmax"));
+    if (hidden_out) {
+      h.resize((size_t)m * LISA_HIDDEN);
+      LISA_TRY(lisa_hip_check(hipMemcpyAsync(h.data(), P.H, h.size() * 2, hipMemcpyDeviceToHost, r->dev->stream),
+                              "D2H hidden"));
+    }
+    LISA_TRY(sync(r));  // the host staging above is reused by the next chunk
+    if (hidden_out)
+      for (size_t i = 0; i < h.size(); ++i) hidden_out[(size_t)b * LISA_HIDDEN + i] = lisa_bf16_to_f32(h[i]);
+    r->position += m;
+  }
+  r->verify_base = -1;
+  LISA_TRY(write_pos(r, r->tgt, r->position));
   return sync(r);
 }

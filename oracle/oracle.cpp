@@ -318,6 +318,39 @@ void orc_q4_linear(const uint16_t* x, const uint32_t* w, const uint16_t* scales,
   q4_linear_prepped(xp.data(), m_rows, w, scales, biases, n_rows, k, ksplit, out);
 }
 
+// Prefill q4 GEMM (gemm.metal:238-266): each weight dequantized to
+// bf16(fma(scale, q, bias)); C[m][n] = sum_k A[m][k] Wd[n][k] accumulated in
+// double and rounded once to f32 (the MFMA accumulation order of the HIP path
+// is the hardware's, so its results are compared with a tolerance).
+void orc_q4_gemm(const uint16_t* a, const uint32_t* w, const uint16_t* scales, const uint16_t* biases, int n_rows,
+                 int k, int m_rows, float* out) {
+  const int wpr = k / 8, groups = k / 64;
+  std::vector<float> af((size_t)m_rows * k);
+  for (size_t i = 0; i < af.size(); ++i) af[i] = bf(a[i]);
+#pragma omp parallel
+  {
+    std::vector<float> wd(k);
+#pragma omp for schedule(static)
+    for (int n = 0; n < n_rows; ++n) {
+      for (int g = 0; g < groups; ++g) {
+        const float sc = bf(scales[(size_t)n * groups + g]), bi = bf(biases[(size_t)n * groups + g]);
+        for (int e = 0; e < 64; ++e) {
+          const int kk = 64 * g + e;
+          const uint32_t q = (w[(size_t)n * wpr + kk / 8] >> (4 * (kk % 8))) & 0xfu;
+          wd[kk] = bfr(lisa_fma(sc, (float)q, bi));
+        }
+      }
+      for (int m = 0; m < m_rows; ++m) {
+        const float* ar = &af[(size_t)m * k];
+        double acc[4] = {0.0, 0.0, 0.0, 0.0};
+        for (int kk = 0; kk < k; kk += 4)
+          for (int j = 0; j < 4; ++j) acc[j] += (double)ar[kk + j] * (double)wd[kk + j];
+        out[(size_t)m * n_rows + n] = (float)((acc[0] + acc[1]) + (acc[2] + acc[3]));
+      }
+    }
+  }
+}
+
 void orc_rms_norm(const uint16_t* x, const uint16_t* w, int cols, uint16_t* out) {
   std::vector<float> xf(cols);
   for (int j = 0; j < cols; ++j) xf[j] = bf(x[j]);
@@ -349,9 +382,10 @@ void orc_silu_mul(const float* g, const float* u, int n, uint16_t* act) {
 void orc_gdn_conv(const float* qkv, const uint16_t* conv_w, uint16_t* conv_state, int m_rows,
                   float* conv_out, uint16_t* slots) {
   const int C = LISA_GDN_CONV_DIM;
-  if (m_rows < 1 || m_rows > 16) return;
+  if (m_rows < 1) return;
+#pragma omp parallel for schedule(static)
   for (int c = 0; c < C; ++c) {
-    float hist[3 + 16];
+    std::vector<float> hist(3 + m_rows);
     for (int i = 0; i < 3; ++i) hist[i] = bf(conv_state[(size_t)i * C + c]);
     for (int t = 0; t < m_rows; ++t) hist[3 + t] = bfr(qkv[(size_t)t * C + c]);
     for (int t = 0; t < m_rows; ++t) {
@@ -899,6 +933,85 @@ int orc_model_forward(OrcModel* M, const uint32_t* tokens, int m, int capture, u
   if (logits_out) std::memcpy(logits_out, logits.data(), sizeof(float) * logits.size());
   M->position += m;
   M->verify_base = capture ? (int64_t)base : -1;
+  return 0;
+}
+
+static void gemm_q4(const std::vector<uint16_t>& a, int m, const Q4& w, std::vector<float>& c) {
+  c.resize((size_t)m * w.n);
+  orc_q4_gemm(a.data(), w.w.data(), w.s.data(), w.b.data(), w.n, w.k, m, c.data());
+}
+
+static void norm_rows_bf16(const std::vector<float>& h, int m, const std::vector<uint16_t>& w,
+                           std::vector<uint16_t>& x) {
+  x.resize((size_t)m * LISA_HIDDEN);
+  for (int t = 0; t < m; ++t) rms_norm_f(&h[(size_t)t * LISA_HIDDEN], w.data(), LISA_HIDDEN, &x[(size_t)t * LISA_HIDDEN]);
+}
+
+// forward_prefill_with_progress (runner.rs:2129-2230): chunks of `chunk` rows;
+// GEMM projections, conv/recurrence over the chunk's rows, attention rows as in
+// decode, residual + norms per row.
+int orc_model_prefill(OrcModel* M, const uint32_t* tokens, int n, int chunk, uint32_t* argmax_out,
+                      float* hidden_out) {
+  if (n < 0) return -1;
+  for (int t = 0; t < n; ++t)
+    if ((int)tokens[t] >= M->vocab) return -2;
+  if (M->position + n > M->capacity) return -3;
+  if (chunk <= 0 || chunk > 512) chunk = 512;
+  for (int b0 = 0; b0 < n; b0 += chunk) {
+    const int m = std::min(chunk, n - b0);
+    const uint32_t base = M->position;
+    std::vector<float> H, B;
+    std::vector<uint16_t> X;
+    embed_rows(M, tokens + b0, m, H);
+    for (int i = 0; i < M->layers; ++i) {
+      OrcLayer& l = M->L[i];
+      if (i > 0) residual_rows(H, B, m, H);
+      norm_rows_bf16(H, m, l.input_norm, X);
+      if (!l.attention) {
+        const int si = l.state_index;
+        std::vector<float> qkv, z, a, b;
+        gemm_q4(X, m, l.qkv, qkv);
+        gemm_q4(X, m, l.z, z);
+        gemm_q4(X, m, l.a, a);
+        gemm_q4(X, m, l.b, b);
+        std::vector<float> conv_out((size_t)m * LISA_GDN_CONV_DIM);
+        orc_gdn_conv(qkv.data(), l.conv_w.data(), &M->conv_state[(size_t)si * 3 * LISA_GDN_CONV_DIM], m,
+                     conv_out.data(), nullptr);
+        std::vector<uint16_t> gated((size_t)m * LISA_GDN_VALUE_DIM);
+        orc_gdn_recurrence(conv_out.data(), z.data(), a.data(), b.data(), l.a_log.data(), l.dt_bias.data(),
+                           l.gnorm.data(), &M->gdn_state[(size_t)si * LISA_GDN_STATE], m, gated.data(), nullptr,
+                           nullptr);
+        gemm_q4(gated, m, l.out, B);
+      } else {
+        std::vector<float> qp, kr, vr;
+        gemm_q4(X, m, l.q, qp);
+        gemm_q4(X, m, l.k, kr);
+        gemm_q4(X, m, l.v, vr);
+        const size_t off = (size_t)l.cache_index * LISA_ATT_KVH * M->capacity * LISA_ATT_HD;
+        std::vector<uint16_t> gated((size_t)m * LISA_ATT_OUT);
+        orc_attention(qp.data(), kr.data(), vr.data(), l.q_norm.data(), l.k_norm.data(), &M->key_cache[off],
+                      &M->value_cache[off], M->capacity, base, m, gated.data());
+        gemm_q4(gated, m, l.o, B);
+      }
+      residual_rows(H, B, m, H);
+      norm_rows_bf16(H, m, l.post_norm, X);
+      std::vector<float> g, u;
+      gemm_q4(X, m, l.gate, g);
+      gemm_q4(X, m, l.up, u);
+      std::vector<uint16_t> act((size_t)m * LISA_INTER);
+      orc_silu_mul(g.data(), u.data(), m * LISA_INTER, act.data());
+      gemm_q4(act, m, l.down, B);
+    }
+    residual_rows(H, B, m, H);
+    norm_rows_bf16(H, m, M->final_norm, X);
+    std::vector<float> logits;
+    gemm_q4(X, m, M->head, logits);
+    for (int t = 0; t < m; ++t)
+      if (argmax_out) argmax_out[b0 + t] = orc_argmax(&logits[(size_t)t * M->vocab], M->vocab);
+    if (hidden_out) std::memcpy(hidden_out + (size_t)b0 * LISA_HIDDEN, H.data(), sizeof(float) * H.size());
+    M->position += m;
+  }
+  M->verify_base = -1;
   return 0;
 }
 

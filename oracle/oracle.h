@@ -77,6 +77,10 @@ void orc_attention(const float* q_proj, const float* k_raw, const float* v_raw,
 void orc_sdpa(const uint16_t* query, const uint16_t* key_cache, const uint16_t* value_cache, uint32_t capacity,
               uint32_t base, int m_rows, float* out);
 
+/* K20 prefill q4 GEMM: bf16(fma(s, q, b)) dequant, double accumulation, f32 out [m][n]. */
+void orc_q4_gemm(const uint16_t* a, const uint32_t* w, const uint16_t* scales, const uint16_t* biases, int n_rows,
+                 int k, int m_rows, float* out);
+
 /* Shared numerics element-wise (see oracle.cpp orc_math for fn codes). */
 void orc_math(int fn, const float* x, size_t n, float* out);
 
@@ -111,6 +115,8 @@ void orc_model_reset(OrcModel* m);
 int orc_model_forward(OrcModel* m, const uint32_t* tokens, int m_rows, int capture,
                       uint32_t* argmax, float* hidden, float* logits);
 /* commit_verified_prefix (runner.rs:911-944). Returns 0 or -1 on error. */
+/* H11 forward_prefill_with_progress over `n` tokens in chunks (<= 512). */
+int orc_model_prefill(OrcModel* m, const uint32_t* tokens, int n, int chunk, uint32_t* argmax_out, float* hidden_out);
 int orc_model_commit(OrcModel* m, int rows);
 
 /* MTP drafter step (runner.rs:2711-2765): cond is the bf16 conditioning

@@ -17,6 +17,8 @@ _P = C.c_void_p
 _SIGS = {
     "orc_q4_linear": (None, [_P, _P, _P, _P, C.c_int, C.c_int, C.c_int, C.c_int, _P]),
     "orc_rms_norm": (None, [_P, _P, C.c_int, _P]),
+    "orc_q4_gemm": (None, [_P, _P, _P, _P, C.c_int, C.c_int, C.c_int, _P]),
+    "orc_model_prefill": (C.c_int, [_P, _P, C.c_int, C.c_int, _P, _P]),
     "orc_residual": (None, [_P, _P, C.c_int, _P]),
     "orc_embed": (None, [_P, _P, _P, C.c_uint32, C.c_int, _P]),
     "orc_silu_mul": (None, [_P, _P, C.c_int, _P]),
@@ -77,6 +79,14 @@ def q4_linear(x_bf16, w, scales, biases, n, k, m=1, ksplit=1):
     w, s, b = _c(w, np.uint32), _c(scales, np.uint16), _c(biases, np.uint16)
     out = np.empty(m * n, np.float32)
     lib().orc_q4_linear(p(x), p(w), p(s), p(b), n, k, m, ksplit, p(out))
+    return out.reshape(m, n)
+
+
+def q4_gemm(a_bf16, w, scales, biases, n, k, m):
+    """Prefill GEMM: f32 [m][n] of bf16 rows a[m][k] against bf16(fma(s, q, b)) weights."""
+    out = np.empty(m * n, np.float32)
+    lib().orc_q4_gemm(p(_c(a_bf16, np.uint16)), p(_c(w, np.uint32)), p(_c(scales, np.uint16)),
+                      p(_c(biases, np.uint16)), n, k, m, p(out))
     return out.reshape(m, n)
 
 
@@ -229,6 +239,15 @@ class Model:
         if want_logits:
             return am, hidden.reshape(m, 5120), logits.reshape(m, self.vocab)
         return am, hidden.reshape(m, 5120)
+
+    def prefill(self, tokens, chunk=0, want_hidden=False):
+        t = _c(tokens, np.uint32)
+        am = np.zeros(t.size, np.uint32)
+        hidden = np.empty((t.size, 5120), np.float32) if want_hidden else None
+        rc = lib().orc_model_prefill(self.h, p(t), t.size, chunk, p(am), p(hidden))
+        if rc:
+            raise RuntimeError(f"oracle prefill failed ({rc})")
+        return (am, hidden) if want_hidden else am
 
     def commit(self, rows):
         rc = lib().orc_model_commit(self.h, rows)
