@@ -36,6 +36,7 @@ import numpy as np
 ROOT = Path(__file__).resolve().parent
 SEED = 0x15A2026
 CTX_SEED = 0x4C1A
+PROMPT_SEED = 0x2048
 FIRST_TOKEN = 2005  # the reference CLI's default prompt token (src/cli/run.rs:177)
 CTX = 4096
 HBM_PEAK_GBS = 8000.0
@@ -71,6 +72,14 @@ def bytes_per_token(ctx):
     kv = 16 * 4 * 256 * 2 * 2 * ctx + 16 * 4 * 256 * 2 * 2
     embed = HIDDEN // 2 + (HIDDEN // 64) * 4
     return weights + small + state + kv + embed
+
+
+def q4_params():
+    """q4 weights of all projections and the lm_head (the prefill GEMM work per row)."""
+    mlp = 3 * INTER * HIDDEN
+    gdn = (10240 + 6144 + 48 + 48) * HIDDEN + HIDDEN * 6144
+    attn = (12288 + 2048) * HIDDEN + HIDDEN * 6144
+    return LAYERS * mlp + 48 * gdn + 16 * attn + VOCAB * HIDDEN
 
 
 def gate_up_bytes():
@@ -115,6 +124,8 @@ def main():
                     help="decode steps of the CPU oracle baseline (about 11 s on 16 host cores)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--profile-steps", type=int, default=4)
+    ap.add_argument("--prefill-tokens", type=int, default=2048,
+                    help="config 3 prompt length for the prefill phase (0 skips it)")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="only run the plain copy kernel over MIB MiB (counter calibration)")
     args = ap.parse_args()
@@ -130,7 +141,7 @@ def main():
 
     pkg = load("lisa_rs_amd", ROOT / "lisa-rs_amd" / "__init__.py", ROOT / "lisa-rs_amd")
     K, W = args.steps, args.warmup
-    capacity = CTX + max(K, args.profile_steps, args.cpu_steps) + W + 16
+    capacity = max(CTX + max(K, args.profile_steps, args.cpu_steps) + W + 16, args.prefill_tokens + 16)
     t0 = time.time()
     runner = pkg.Runner(layers=LAYERS, vocab=VOCAB, capacity=capacity, seed=SEED, use_graph=True)
     dev = pkg.lib().lisa_runner_device(runner.h)
@@ -173,6 +184,29 @@ def main():
     gu_gbs = gate_up_bytes() / gu_avg_s / 1e9
     print(f"[bench] profile per token (us): {kernels_us}", file=sys.stderr, flush=True)
     traffic = traffic_per_launch()
+
+    # config 3 prompt phase: batched prefill of PREFILL_TOKENS uniform random ids
+    # from an empty state (runner.rs:2129-2230, 512-row chunks)
+    prefill = None
+    if args.prefill_tokens > 0:
+        rng = np.random.default_rng(PROMPT_SEED)
+        prompt = rng.integers(0, VOCAB, args.prefill_tokens).astype(np.uint32)
+        runner.reset_state()
+        runner.forward_prefill(prompt[:512])  # allocates the prefill scratch
+        runner.reset_state()
+        pkg._check(L.lisa_device_synchronize(dev))
+        pkg._check(L.lisa_event_record(ev0, dev))
+        runner.forward_prefill(prompt)
+        pkg._check(L.lisa_event_record(ev1, dev))
+        pkg._check(L.lisa_event_elapsed_ms(ev0, ev1, pkg.C.byref(ms)))
+        pf_s = ms.value / 1e3
+        flops = 2.0 * q4_params() * args.prefill_tokens
+        prefill = {"tokens": args.prefill_tokens, "chunk_rows": 512, "ms": round(ms.value, 2),
+                   "tok_s": round(args.prefill_tokens / pf_s, 1),
+                   "gemm_tflops_effective": round(flops / pf_s / 1e12, 1),
+                   "note": "q4 GEMM FLOPs / whole prefill time (includes GDN, attention, norms)"}
+        print(f"[bench] prefill {args.prefill_tokens} tokens: {ms.value:.1f} ms, {prefill['tok_s']} tok/s, "
+              f"{prefill['gemm_tflops_effective']} TFLOP/s effective", file=sys.stderr, flush=True)
     runner.close()
 
     result = {
@@ -201,6 +235,9 @@ def main():
                      "bytes_per_launch": gate_up_bytes(), "avg_launch_us": round(gu_avg_s * 1e6, 2)},
         "kernels_us_per_token": kernels_us,
     }
+    if prefill:
+        result["target_prefill_tok_s"] = prefill["tok_s"]
+        result["prefill"] = prefill
 
     if not args.no_cpu and args.cpu_steps > 0:
         orc = load("lisa_oracle", ROOT / "oracle" / "oracle.py")
