@@ -31,14 +31,19 @@ enum {
   LISA_PRO_EMBED = 2,   /* r = q4 embedding row of tokens[m]; x = RMSNorm(r) */
   LISA_PRO_CAST = 3,    /* r = bf16(o_in); x = RMSNorm(r) */
   LISA_PRO_NORM = 4,    /* r = h_in; x = RMSNorm(r) */
-  LISA_PRO_MTPFC = 5    /* x = [RMSNorm(embed(tok), norm_w) | RMSNorm(x_in, norm_w2)] */
+  LISA_PRO_MTPFC = 5,   /* x = [RMSNorm(embed(tok), norm_w) | RMSNorm(x_in, norm_w2)] */
+  LISA_PRO_PRENORM = 6  /* x = RMSNorm(h_in) with the statistic from the producer's tile
+                           partials ss_part[M][640] (residual already added, EPI_RESID) */
 };
 
 enum {
   LISA_EPI_STORE = 0,  /* out f32[M][rows] */
   LISA_EPI_GATEUP = 1, /* rows j of (w, w2) -> out bf16[M][rows] = bf16(silu(g)*u) */
   LISA_EPI_CONV = 2,   /* GDN qkv: causal conv + SiLU -> out f32[M][rows], conv state update */
-  LISA_EPI_ARGMAX = 3  /* out f32 logits[M][rows] + per-workgroup (max, idx) partials */
+  LISA_EPI_ARGMAX = 3, /* out f32 logits[M][rows] + per-workgroup (max, idx) partials */
+  LISA_EPI_RESID = 4   /* rows of the 5120-wide residual: h_in[m][j] <- bf16(h_in[m][j] +
+                          bf16(y)) in place, plus one sum of squares per 8-row tile in
+                          ss_part[m][tile] (for a PRENORM consumer) */
 };
 
 typedef struct LisaQ4Mat {
@@ -54,7 +59,7 @@ typedef struct LisaQ4Mat {
 typedef struct LisaQmvParams {
   /* prologue */
   const uint16_t* x_in;
-  const uint16_t* h_in;
+  const uint16_t* h_in; /* residual rows bf16 [M][5120]; EPI_RESID updates them in place */
   const float* o_in;
   const uint32_t* tokens;
   const uint32_t* emb_w;
@@ -78,6 +83,7 @@ typedef struct LisaQmvParams {
   uint32_t pro_mode;
   uint32_t capture;
   uint32_t ksplit; /* 1 or 4: waves of a workgroup split K of one tile */
+  float* ss_part;  /* EPI_RESID writes / PRENORM reads: [M][640] tile sums of squares */
 } LisaQmvParams;
 
 /* ---- GDN recurrence + gated RMSNorm --------------------------------------

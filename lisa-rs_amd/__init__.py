@@ -44,8 +44,8 @@ KINDS = ["gdn_in_proj", "gdn_recurrence", "gdn_out_proj", "attn_in_proj", "attn_
          "attn_o_proj", "mlp_gate_up", "mlp_down", "lm_head", "finalize"]
 
 # lisa_kernels.h enums
-PRO_LOADX, PRO_RESNORM, PRO_EMBED, PRO_CAST, PRO_NORM, PRO_MTPFC = range(6)
-EPI_STORE, EPI_GATEUP, EPI_CONV, EPI_ARGMAX = range(4)
+PRO_LOADX, PRO_RESNORM, PRO_EMBED, PRO_CAST, PRO_NORM, PRO_MTPFC, PRO_PRENORM = range(7)
+EPI_STORE, EPI_GATEUP, EPI_CONV, EPI_ARGMAX, EPI_RESID = range(5)
 
 
 class LisaError(RuntimeError):
@@ -70,7 +70,8 @@ class QmvParams(C.Structure):
                 ("conv_slot_stride", C.c_uint64),
                 ("am_val", C.c_uint64), ("am_idx", C.c_uint64),
                 ("mats", Q4Mat * 4), ("tile_start", C.c_uint32 * 5),
-                ("n_mats", C.c_uint32), ("pro_mode", C.c_uint32), ("capture", C.c_uint32), ("ksplit", C.c_uint32)]
+                ("n_mats", C.c_uint32), ("pro_mode", C.c_uint32), ("capture", C.c_uint32), ("ksplit", C.c_uint32),
+                ("ss_part", C.c_uint64)]
 
 
 class GdnParams(C.Structure):

@@ -196,7 +196,7 @@ DEV float seg_rms_inv(float s, float* red, int tid) {
 }
 
 // Sources of a normalized segment (pro_mode, or the two halves of MTPFC).
-enum SegSrc { SEG_RESNORM, SEG_EMBED, SEG_CAST, SEG_NORM };
+enum SegSrc { SEG_RESNORM, SEG_EMBED, SEG_CAST, SEG_NORM, SEG_PRENORM };
 
 template <int MODE>
 DEV constexpr int seg_source(int seg) {
@@ -204,6 +204,7 @@ DEV constexpr int seg_source(int seg) {
          : MODE == LISA_PRO_EMBED ? SEG_EMBED
          : MODE == LISA_PRO_CAST  ? SEG_CAST
          : MODE == LISA_PRO_NORM  ? SEG_NORM
+         : MODE == LISA_PRO_PRENORM ? SEG_PRENORM
          : (seg == 0 ? SEG_EMBED : SEG_NORM); /* MTPFC */
 }
 
@@ -221,7 +222,10 @@ DEV void seg_load(const LisaQmvParams& p, int m, ProRaw<R>& raw) {
   for (int i = 0; i < 3; ++i) {
     const int c = min(tid + 256 * i, kSegChunks - 1);
     raw.w[i] = reinterpret_cast<const uint4*>(nw)[c];
-    if constexpr (src == SEG_RESNORM || src == SEG_NORM) raw.a[i] = reinterpret_cast<const uint4*>(hsrc)[c];
+    if constexpr (src == SEG_RESNORM || src == SEG_NORM || src == SEG_PRENORM)
+      raw.a[i] = reinterpret_cast<const uint4*>(hsrc)[c];
+    if constexpr (src == SEG_PRENORM)  // this thread's tile partials t, t+256, t+512
+      raw.b[i].x = __float_as_uint(p.ss_part[(size_t)m * kSegChunks + c]);
     if constexpr (src == SEG_RESNORM || src == SEG_CAST) {
       raw.b[i] = reinterpret_cast<const uint4*>(osrc)[2 * c];
       raw.c[i] = reinterpret_cast<const uint4*>(osrc)[2 * c + 1];
@@ -248,7 +252,7 @@ DEV void seg_process(const LisaQmvParams& p, unsigned char* lds, int m, const Pr
   for (int i = 0; i < 3; ++i) {
     const bool valid = tid + 256 * i < kSegChunks;
     float hv[8] = {}, ov[8] = {};
-    if constexpr (src == SEG_RESNORM || src == SEG_NORM) unpack_bf8(raw.a[i], hv);
+    if constexpr (src == SEG_RESNORM || src == SEG_NORM || src == SEG_PRENORM) unpack_bf8(raw.a[i], hv);
     if constexpr (src == SEG_RESNORM || src == SEG_CAST) {
       ov[0] = __uint_as_float(raw.b[i].x); ov[1] = __uint_as_float(raw.b[i].y);
       ov[2] = __uint_as_float(raw.b[i].z); ov[3] = __uint_as_float(raw.b[i].w);
@@ -260,11 +264,14 @@ DEV void seg_process(const LisaQmvParams& p, unsigned char* lds, int m, const Pr
       float r;
       if constexpr (src == SEG_RESNORM) r = lisa_bf16r(hv[e] + lisa_bf16r(ov[e]));
       else if constexpr (src == SEG_CAST) r = lisa_bf16r(ov[e]);
-      else if constexpr (src == SEG_NORM) r = hv[e];
+      else if constexpr (src == SEG_NORM || src == SEG_PRENORM) r = hv[e];
       else r = lisa_bf16r((float)((raw.a[i].x >> (4 * e)) & 0xfu) * lo_bf(raw.a[i].y) + hi_bf(raw.a[i].y));
       v[i][e] = r;
-      if (valid) ss = ss + r * r;
+      if constexpr (src != SEG_PRENORM)
+        if (valid) ss = ss + r * r;
     }
+    if constexpr (src == SEG_PRENORM)
+      if (valid) ss = ss + __uint_as_float(raw.b[i].x);
   }
   const float inv = seg_rms_inv(ss, red, tid);
   const bool writer = blockIdx.x == 0;
@@ -592,6 +599,26 @@ DEV void qmv_body(const LisaQmvParams& p, unsigned char* lds) {
         if (li == 1 && v1) conv_epilogue<M>(p, static_cast<float*>(mt.out), (int)r1, T1);
         break;
       }
+      case LISA_EPI_RESID: {
+        // r = bf16(h + bf16(y)) in place; tile partial ((s0 + s1) + (s2 + s3)),
+        // s_rp = r_{2rp}^2 + r_{2rp+1}^2 over the four row-groups (lanes 0, 16, 32, 48)
+        uint16_t* hres = const_cast<uint16_t*>(p.h_in);  // read-write for this epilogue
+#pragma unroll
+        for (int m = 0; m < M; ++m) {
+          float ra = 0.0f, rb = 0.0f;
+          if (li == 0 && v0 && v1) {
+            ra = lisa_bf16r(bf2f(hres[(size_t)m * LISA_HIDDEN + r0]) + lisa_bf16r(T0[m]));
+            rb = lisa_bf16r(bf2f(hres[(size_t)m * LISA_HIDDEN + r1]) + lisa_bf16r(T1[m]));
+            hres[(size_t)m * LISA_HIDDEN + r0] = lisa_f32_to_bf16(ra);
+            hres[(size_t)m * LISA_HIDDEN + r1] = lisa_f32_to_bf16(rb);
+          }
+          float sq = ra * ra + rb * rb;
+          sq = sq + xor_lane<16>(sq);
+          sq = sq + xor_lane<32>(sq);
+          if (lane == 0) p.ss_part[(size_t)m * (LISA_HIDDEN / 8) + tr.r0 / 8] = sq;
+        }
+        break;
+      }
       default: { /* ARGMAX */
         float* out = static_cast<float*>(mt.out);
 #pragma unroll
@@ -638,9 +665,9 @@ DEV void qmv_body(const LisaQmvParams& p, unsigned char* lds) {
   }
 }
 
-// One kernel per (K, M, prologue): lisa_qmv_k<K>_m<M>_<x|resnorm|embed|cast|norm|mtpfc>,
+// One kernel per (K, M, prologue): lisa_qmv_k<K>_m<M>_<x|resnorm|embed|cast|norm|mtpfc|prenorm>,
 // plus variants whose epilogue is fixed at compile time:
-// lisa_qmv_k5120_m<M>_resnorm_<gateup|argmax> (MLP gate/up, lm_head).
+// lisa_qmv_k5120_m<M>_<resnorm|prenorm>_<gateup|argmax> (MLP gate/up, lm_head).
 #define QMV_KERNEL(K, M, MODE, NAME)                                                             \
   extern "C" __global__ __launch_bounds__(256) void lisa_qmv_k##K##_m##M##_##NAME(LisaQmvParams p) { \
     __shared__ __attribute__((aligned(16))) unsigned char lds[QmvCfg<K, M>::BYTES];                \
@@ -662,6 +689,8 @@ QMV_KERNEL(5120, 3, LISA_PRO_LOADX, x)
 QMV_KERNEL(5120, 3, LISA_PRO_RESNORM, resnorm)
 QMV_KERNEL(5120, 3, LISA_PRO_EMBED, embed)
 QMV_KERNEL(5120, 3, LISA_PRO_NORM, norm)
+QMV_KERNEL(5120, 1, LISA_PRO_PRENORM, prenorm)
+QMV_KERNEL(5120, 3, LISA_PRO_PRENORM, prenorm)
 QMV_KERNEL(6144, 1, LISA_PRO_LOADX, x)
 QMV_KERNEL(6144, 3, LISA_PRO_LOADX, x)
 QMV_KERNEL(10240, 1, LISA_PRO_LOADX, x)
@@ -674,6 +703,10 @@ QMV_KERNEL_EPI(5120, 1, LISA_PRO_RESNORM, resnorm, LISA_EPI_GATEUP, gateup)
 QMV_KERNEL_EPI(5120, 3, LISA_PRO_RESNORM, resnorm, LISA_EPI_GATEUP, gateup)
 QMV_KERNEL_EPI(5120, 1, LISA_PRO_RESNORM, resnorm, LISA_EPI_ARGMAX, argmax)
 QMV_KERNEL_EPI(5120, 3, LISA_PRO_RESNORM, resnorm, LISA_EPI_ARGMAX, argmax)
+QMV_KERNEL_EPI(5120, 1, LISA_PRO_PRENORM, prenorm, LISA_EPI_GATEUP, gateup)
+QMV_KERNEL_EPI(5120, 3, LISA_PRO_PRENORM, prenorm, LISA_EPI_GATEUP, gateup)
+QMV_KERNEL_EPI(5120, 1, LISA_PRO_PRENORM, prenorm, LISA_EPI_ARGMAX, argmax)
+QMV_KERNEL_EPI(5120, 3, LISA_PRO_PRENORM, prenorm, LISA_EPI_ARGMAX, argmax)
 
 // ===========================================================================
 // GDN recurrence (gdn.metal:245-328) + gates (gdn.metal:170-205) + gated

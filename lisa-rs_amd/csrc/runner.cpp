@@ -4,12 +4,14 @@
 // gfx950 kernels through the bridge of device.cpp.
 //
 // Per-token dispatch recipe (one hipGraph for M=1):
-//   layer i, GDN      : qmv[in_proj: embed|residual + input RMSNorm -> qkv(conv)|z|a|b]
-//                       gdn_recurrence -> gated;  qmv[out_proj] -> branch
+//   layer i, GDN      : qmv[in_proj: embed | input RMSNorm -> qkv(conv)|z|a|b]
+//                       gdn_recurrence -> gated;  qmv[out_proj + residual add]
 //   layer i, attention: qmv[in_proj -> q|k|v];  attn_partial;  attn_merge -> gated;
-//                       qmv[o_proj] -> branch
-//   every layer       : qmv[residual + post RMSNorm -> gate/up -> SwiGLU];  qmv[down] -> branch
-//   final             : qmv[residual + final RMSNorm -> lm_head -> argmax partials];  step_finalize
+//                       qmv[o_proj + residual add]
+//   every layer       : qmv[post RMSNorm -> gate/up -> SwiGLU];  qmv[down + residual add]
+//   final             : qmv[final RMSNorm -> lm_head -> argmax partials];  step_finalize
+// A residual-add epilogue updates the residual rows in place and leaves one
+// sum of squares per 8-row tile; the next launch's RMSNorm prologue sums those.
 // 5 launches per GDN layer, 6 per attention layer, 2 final (338 for 64 layers)
 // against the reference's 852 dispatches (runner.rs:568-582, 1248-1592).
 #include <hip/hip_runtime.h>
@@ -59,7 +61,8 @@ struct MtpDev {
 // Scratch of one forward context (target: rows <= 3; drafter: 1 row).
 struct Ctx {
   int rows = 1;
-  uint16_t *H, *R, *gated, *act, *xnorm, *cond;
+  uint16_t *H, *gated, *act, *xnorm, *cond;  // H: residual rows, updated in place
+  float* ss;  // tile sums of squares of the residual rows [rows][640]
   float *B, *conv_out, *z, *a, *b, *q_proj, *k_raw, *v_raw, *part_o, *part_ml, *logits, *am_val;
   uint32_t *am_idx, *tokens, *argmax, *pos, *step, *history;
 };
@@ -93,8 +96,8 @@ struct LisaRunner {
   LisaDevice* dev = nullptr;
   LisaModule* mod = nullptr;
   // kernels
-  LisaFunction *qmv[2][5][6] = {};  // [m3][K index][prologue mode]
-  LisaFunction *qmv_epi[2][6][4] = {};  // K = 5120 with a fixed epilogue: [m3][prologue][epilogue]
+  LisaFunction *qmv[2][5][7] = {};  // [m3][K index][prologue mode]
+  LisaFunction *qmv_epi[2][7][5] = {};  // K = 5120 with a fixed epilogue: [m3][prologue][epilogue]
   LisaFunction *gdn[2] = {}, *attn_part[2] = {}, *attn_merge[2] = {}, *finalize = nullptr, *synth = nullptr;
   // batched prefill
   LisaFunction *gemm = nullptr, *rows = nullptr, *conv_rows = nullptr, *gdn_rows = nullptr, *attn_store_rows = nullptr,
@@ -332,7 +335,7 @@ void plan_state(LisaRunner* r, Arena& A) {
 void plan_ctx(LisaRunner* r, Arena& A, Ctx& c, int rows) {
   c.rows = rows;
   c.H = A.take<uint16_t>((size_t)3 * LISA_HIDDEN);
-  c.R = A.take<uint16_t>((size_t)rows * LISA_HIDDEN);
+  c.ss = A.take<float>((size_t)rows * (LISA_HIDDEN / 8));
   c.B = A.take<float>((size_t)rows * LISA_HIDDEN);
   c.conv_out = A.take<float>((size_t)rows * LISA_GDN_CONV_DIM);
   c.z = A.take<float>((size_t)rows * LISA_GDN_VALUE_DIM);
@@ -369,12 +372,12 @@ struct MatSpec {
 int launch_qmv(LisaRunner* r, int m_rows, uint32_t K, LisaQmvParams& p, const std::vector<MatSpec>& mats) {
   const int ki = k_index(K);
   if (ki < 0) return lisa_fail(LISA_E_ARG, "no q4 kernel for K=%u", K);
-  if (p.pro_mode > LISA_PRO_MTPFC) return lisa_fail(LISA_E_ARG, "bad q4 prologue mode %u", p.pro_mode);
+  if (p.pro_mode > LISA_PRO_PRENORM) return lisa_fail(LISA_E_ARG, "bad q4 prologue mode %u", p.pro_mode);
   LisaFunction* fn = r->qmv[m_rows == 3 ? 1 : 0][ki][p.pro_mode];
   // a launch whose matrices all share one epilogue uses the specialized kernel when there is one
   bool same_kind = !mats.empty();
   for (const MatSpec& s : mats) same_kind = same_kind && s.kind == mats[0].kind;
-  if (K == LISA_HIDDEN && same_kind && mats[0].kind < 4) {
+  if (K == LISA_HIDDEN && same_kind && mats[0].kind < 5) {
     if (LisaFunction* f = r->qmv_epi[m_rows == 3 ? 1 : 0][p.pro_mode][mats[0].kind]) fn = f;
   }
   if (!fn) return lisa_fail(LISA_E_ARG, "no q4 kernel for K=%u M=%d prologue %u", K, m_rows, p.pro_mode);
@@ -403,21 +406,26 @@ int launch_qmv(LisaRunner* r, int m_rows, uint32_t K, LisaQmvParams& p, const st
   return lisa_launch(r->dev, fn, &p, sizeof p, grid, 1, 1, 256, 1, 1);
 }
 
-LisaQmvParams pro_resnorm(const uint16_t* h, const float* o, const uint16_t* w, uint16_t* r_out) {
+// Consumer of the residual rows: x = RMSNorm(c.H) from the tile partials the
+// producing launch left in c.ss.
+LisaQmvParams pro_prenorm(Ctx& c, const uint16_t* w) {
   LisaQmvParams p{};
-  p.pro_mode = LISA_PRO_RESNORM;
-  p.h_in = h;
-  p.o_in = o;
+  p.pro_mode = LISA_PRO_PRENORM;
+  p.h_in = c.H;
+  p.ss_part = c.ss;
   p.norm_w = w;
-  p.r_out = r_out;
   return p;
 }
 
-LisaQmvParams pro_loadx(const uint16_t* x) {
+// Producer of the residual rows: c.H += y (bf16 residual add, runner.rs
+// encode_residual), tile partials into c.ss.
+int launch_resid(LisaRunner* r, Ctx& c, int m, uint32_t K, const uint16_t* x, const Q4Dev& w) {
   LisaQmvParams p{};
   p.pro_mode = LISA_PRO_LOADX;
   p.x_in = x;
-  return p;
+  p.h_in = c.H;
+  p.ss_part = c.ss;
+  return launch_qmv(r, m, K, p, {{&w, nullptr, nullptr, LISA_EPI_RESID}});
 }
 
 int launch_attention(LisaRunner* r, Ctx& c, int m, const uint16_t* qn, const uint16_t* kn, uint16_t* kc,
@@ -445,16 +453,17 @@ int launch_attention(LisaRunner* r, Ctx& c, int m, const uint16_t* qn, const uin
 
 int launch_mlp(LisaRunner* r, Ctx& c, int m, const uint16_t* post_norm, const Q4Dev& gate, const Q4Dev& up,
                const Q4Dev& down) {
-  LisaQmvParams p = pro_resnorm(c.H, c.B, post_norm, c.R);
+  LisaQmvParams p = pro_prenorm(c, post_norm);
   LISA_TRY(prof_mark(r, LISA_KIND_MLP_GATE_UP));
   LISA_TRY(launch_qmv(r, m, LISA_HIDDEN, p, {{&gate, &up, c.act, LISA_EPI_GATEUP}}));
-  LisaQmvParams d = pro_loadx(c.act);
   LISA_TRY(prof_mark(r, LISA_KIND_MLP_DOWN));
-  return launch_qmv(r, m, LISA_INTER, d, {{&down, nullptr, c.B, LISA_EPI_STORE}});
+  return launch_resid(r, c, m, LISA_INTER, c.act, down);
 }
 
-int launch_lm_head(LisaRunner* r, Ctx& c, int m, const uint16_t* norm, uint16_t* x_out, uint16_t* h_out) {
-  LisaQmvParams p = pro_resnorm(c.R, c.B, norm, h_out);
+// Final norm + lm_head; x_out (nullable) receives the normalized rows. The
+// hidden rows (before the final norm) are c.H.
+int launch_lm_head(LisaRunner* r, Ctx& c, int m, const uint16_t* norm, uint16_t* x_out) {
+  LisaQmvParams p = pro_prenorm(c, norm);
   p.x_out = x_out;
   p.am_val = c.am_val;
   p.am_idx = c.am_idx;
@@ -494,7 +503,7 @@ int encode_target(LisaRunner* r, int m, bool capture, bool feedback) {
       p.norm_w = l.input_norm;
       p.r_out = c.H;
     } else {
-      p = pro_resnorm(c.R, c.B, l.input_norm, c.H);
+      p = pro_prenorm(c, l.input_norm);
     }
     if (!l.attention) {
       const int si = l.state_index;
@@ -526,9 +535,8 @@ int encode_target(LisaRunner* r, int m, bool capture, bool feedback) {
       g.capture = capture ? 1 : 0;
       LISA_TRY(prof_mark(r, LISA_KIND_GDN_RECURRENCE));
       LISA_TRY(lisa_launch(r->dev, r->gdn[m == 3 ? 1 : 0], &g, sizeof g, LISA_GDN_VH, 1, 1, 512, 1, 1));
-      LisaQmvParams o = pro_loadx(c.gated);
       LISA_TRY(prof_mark(r, LISA_KIND_GDN_OUT));
-      LISA_TRY(launch_qmv(r, m, LISA_GDN_VALUE_DIM, o, {{&l.out, nullptr, c.B, LISA_EPI_STORE}}));
+      LISA_TRY(launch_resid(r, c, m, LISA_GDN_VALUE_DIM, c.gated, l.out));
     } else {
       LISA_TRY(prof_mark(r, LISA_KIND_ATTN_IN));
       LISA_TRY(launch_qmv(r, m, LISA_HIDDEN, p,
@@ -537,14 +545,13 @@ int encode_target(LisaRunner* r, int m, bool capture, bool feedback) {
                            {&l.v, nullptr, c.v_raw, LISA_EPI_STORE}}));
       const size_t off = (size_t)l.cache_index * LISA_ATT_KVH * r->cfg.capacity * LISA_ATT_HD;
       LISA_TRY(launch_attention(r, c, m, l.q_norm, l.k_norm, r->key_cache + off, r->value_cache + off));
-      LisaQmvParams o = pro_loadx(c.gated);
       LISA_TRY(prof_mark(r, LISA_KIND_ATTN_OUT));
-      LISA_TRY(launch_qmv(r, m, LISA_ATT_OUT, o, {{&l.o, nullptr, c.B, LISA_EPI_STORE}}));
+      LISA_TRY(launch_resid(r, c, m, LISA_ATT_OUT, c.gated, l.o));
     }
     LISA_TRY(launch_mlp(r, c, m, l.post_norm, l.gate, l.up, l.down));
   }
   LISA_TRY(prof_mark(r, LISA_KIND_LM_HEAD));
-  LISA_TRY(launch_lm_head(r, c, m, r->final_norm, nullptr, c.H));
+  LISA_TRY(launch_lm_head(r, c, m, r->final_norm, nullptr));
   LISA_TRY(prof_mark(r, LISA_KIND_FINALIZE));
   LISA_TRY(launch_finalize(r, c, m, feedback, (uint32_t)m));
   return prof_mark(r, -1);
@@ -573,10 +580,9 @@ int encode_mtp(LisaRunner* r, const uint16_t* cond) {
                        {&t.k, nullptr, c.k_raw, LISA_EPI_STORE},
                        {&t.v, nullptr, c.v_raw, LISA_EPI_STORE}}));
   LISA_TRY(launch_attention(r, c, 1, t.q_norm, t.k_norm, r->mtp_key, r->mtp_value));
-  LisaQmvParams o = pro_loadx(c.gated);
-  LISA_TRY(launch_qmv(r, 1, LISA_ATT_OUT, o, {{&t.o, nullptr, c.B, LISA_EPI_STORE}}));
+  LISA_TRY(launch_resid(r, c, 1, LISA_ATT_OUT, c.gated, t.o));
   LISA_TRY(launch_mlp(r, c, 1, t.post_norm, t.gate, t.up, t.down));
-  LISA_TRY(launch_lm_head(r, c, 1, t.final_norm, c.xnorm, nullptr));
+  LISA_TRY(launch_lm_head(r, c, 1, t.final_norm, c.xnorm));
   return launch_finalize(r, c, 1, false, 1);
 }
 
@@ -662,16 +668,16 @@ extern "C" int lisa_runner_create(const LisaRunnerConfig* cfg, LisaRunner** out)
   LISA_TRY(lisa_module_load_default(r->dev, &r->mod));
   // lisa_qmv_k<K>_m<M>_<prologue>; combinations the module does not hold stay null
   static const char* knames[5] = {"5120", "6144", "10240", "17408", "1024"};
-  static const char* pnames[6] = {"x", "resnorm", "embed", "cast", "norm", "mtpfc"};
+  static const char* pnames[7] = {"x", "resnorm", "embed", "cast", "norm", "mtpfc", "prenorm"};
   for (int mi = 0; mi < 2; ++mi)
     for (int ki = 0; ki < 5; ++ki)
-      for (int pi = 0; pi < 6; ++pi) {
+      for (int pi = 0; pi < 7; ++pi) {
         const std::string name = std::string("lisa_qmv_k") + knames[ki] + (mi ? "_m3_" : "_m1_") + pnames[pi];
         hipFunction_t hf;
         if (hipModuleGetFunction(&hf, r->mod->mod, name.c_str()) == hipSuccess)
           r->qmv[mi][ki][pi] = new LisaFunction{hf, name};
-        static const char* enames[4] = {"store", "gateup", "conv", "argmax"};
-        for (int ei = 0; ki == 0 && ei < 4; ++ei) {
+        static const char* enames[5] = {"store", "gateup", "conv", "argmax", "resid"};
+        for (int ei = 0; ki == 0 && ei < 5; ++ei) {
           const std::string en = name + "_" + enames[ei];
           if (hipModuleGetFunction(&hf, r->mod->mod, en.c_str()) == hipSuccess)
             r->qmv_epi[mi][pi][ei] = new LisaFunction{hf, en};

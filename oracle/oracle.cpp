@@ -74,6 +74,31 @@ float sumsq_chunks8(const float* x, int cols) {
   return (w[0] + w[1]) + (w[2] + w[3]);
 }
 
+// Sum of squares of a 5120-wide residual row as the decode path computes it
+// across two launches: the launch that adds the residual writes one partial per
+// 8-row tile, ((r0^2 + r1^2) + (r2^2 + r3^2)) + ((r4^2 + r5^2) + (r6^2 + r7^2)),
+// and the consuming launch's thread t of 256 sums partials t, t+256, t+512 in
+// order, tree64 per wave, (W0 + W1) + (W2 + W3).
+float sumsq_tiles8(const float* x, int cols) {
+  const int tiles = cols / 8;
+  std::vector<float> part(tiles);
+  for (int b = 0; b < tiles; ++b) {
+    const float* r = x + 8 * b;
+    float s[4];
+    for (int q = 0; q < 4; ++q) s[q] = r[2 * q] * r[2 * q] + r[2 * q + 1] * r[2 * q + 1];
+    part[b] = (s[0] + s[1]) + (s[2] + s[3]);
+  }
+  float lanes[256];
+  for (int t = 0; t < 256; ++t) {
+    float acc = 0.0f;
+    for (int b = t; b < tiles; b += 256) acc = acc + part[b];
+    lanes[t] = acc;
+  }
+  float w[4];
+  for (int q = 0; q < 4; ++q) w[q] = tree_xor(lanes + 64 * q, 64);
+  return (w[0] + w[1]) + (w[2] + w[3]);
+}
+
 // Sum of squares of `cols` values (multiple of 256) with the rows-of-256 tree.
 float sumsq_rows256(const float* x, int cols) {
   float lanes[256];
@@ -96,8 +121,8 @@ float sumsq_tree128(const float* v) {
 
 // RMSNorm of a row of f32 (bf16-valued) inputs; norm.metal:10-47:
 // inv = rsqrt(sum/cols + eps), y = bf16(x * inv * w).
-void rms_norm_f(const float* x, const uint16_t* w, int cols, uint16_t* out) {
-  const float ss = sumsq_chunks8(x, cols);
+void rms_norm_f(const float* x, const uint16_t* w, int cols, uint16_t* out, bool tiles = false) {
+  const float ss = tiles ? sumsq_tiles8(x, cols) : sumsq_chunks8(x, cols);
   const float inv = lisa_rsqrt(ss / (float)cols + LISA_EPS);
   for (int j = 0; j < cols; ++j) out[j] = tobf((x[j] * inv) * bf(w[j]));
 }
@@ -355,6 +380,13 @@ void orc_rms_norm(const uint16_t* x, const uint16_t* w, int cols, uint16_t* out)
   std::vector<float> xf(cols);
   for (int j = 0; j < cols; ++j) xf[j] = bf(x[j]);
   rms_norm_f(xf.data(), w, cols, out);
+}
+
+// RMSNorm with the tile-partial statistic (residual-add launch + consumer).
+void orc_rms_norm_tiles(const uint16_t* x, const uint16_t* w, int cols, uint16_t* out) {
+  std::vector<float> xf(cols);
+  for (int j = 0; j < cols; ++j) xf[j] = bf(x[j]);
+  rms_norm_f(xf.data(), w, cols, out, true);
 }
 
 void orc_residual(const uint16_t* x, const float* o, int n, uint16_t* y) {
@@ -679,13 +711,15 @@ static void embed_rows(const OrcModel* M, const uint32_t* tokens, int m, std::ve
   }
 }
 
+// tiles: the statistic comes from the residual-add launch's tile partials
+// (every decode-path norm except the one after the embedding).
 static void norm_rows(const std::vector<float>& h, int m, const std::vector<uint16_t>& w,
-                      std::vector<XPrep>& xp, std::vector<uint16_t>* keep = nullptr) {
+                      std::vector<XPrep>& xp, std::vector<uint16_t>* keep = nullptr, bool tiles = false) {
   xp.resize(m);
   std::vector<uint16_t> x(LISA_HIDDEN);
   if (keep) keep->resize((size_t)m * LISA_HIDDEN);
   for (int t = 0; t < m; ++t) {
-    rms_norm_f(&h[(size_t)t * LISA_HIDDEN], w.data(), LISA_HIDDEN, x.data());
+    rms_norm_f(&h[(size_t)t * LISA_HIDDEN], w.data(), LISA_HIDDEN, x.data(), tiles);
     prep_x(x.data(), LISA_HIDDEN, xp[t]);
     if (keep) std::memcpy(keep->data() + (size_t)t * LISA_HIDDEN, x.data(), LISA_HIDDEN * 2);
   }
@@ -880,7 +914,7 @@ int orc_model_forward(OrcModel* M, const uint32_t* tokens, int m, int capture, u
   std::vector<XPrep> xp;
   for (int i = 0; i < M->layers; ++i) {
     OrcLayer& l = M->L[i];
-    norm_rows(H, m, l.input_norm, xp);
+    norm_rows(H, m, l.input_norm, xp, nullptr, i > 0);
     if (!l.attention) {
       const int si = l.state_index;
       std::vector<float> qkv((size_t)m * LISA_GDN_CONV_DIM), z((size_t)m * LISA_GDN_VALUE_DIM),
@@ -919,11 +953,11 @@ int orc_model_forward(OrcModel* M, const uint32_t* tokens, int m, int capture, u
                       &M->value_cache[off], M->capacity, base, xp, m, B);
     }
     residual_rows(H, B, m, R);
-    norm_rows(R, m, l.post_norm, xp);
+    norm_rows(R, m, l.post_norm, xp, nullptr, true);
     mlp_block(l.gate, l.up, l.down, xp, m, B);
     residual_rows(R, B, m, H);
   }
-  norm_rows(H, m, M->final_norm, xp);
+  norm_rows(H, m, M->final_norm, xp, nullptr, true);
   std::vector<float> logits((size_t)m * M->vocab);
   q4_apply(M->head, xp, m, logits.data());
   for (int t = 0; t < m; ++t) {
@@ -1050,11 +1084,11 @@ int orc_mtp_forward(OrcModel* M, uint32_t token, const uint16_t* cond, uint32_t*
   attention_block(t.q, t.k, t.v, t.o, t.q_norm, t.k_norm, t.key_cache.data(), t.value_cache.data(),
                   M->capacity, t.position, xp, 1, B);
   residual_rows(H, B, 1, R);
-  norm_rows(R, 1, t.post_norm, xp);
+  norm_rows(R, 1, t.post_norm, xp, nullptr, true);
   mlp_block(t.gate, t.up, t.down, xp, 1, B);
   residual_rows(R, B, 1, H);
   std::vector<uint16_t> xn;
-  norm_rows(H, 1, t.final_norm, xp, &xn);
+  norm_rows(H, 1, t.final_norm, xp, &xn, true);
   std::vector<float> logits(M->vocab);
   q4_apply(M->head, xp, 1, logits.data());
   if (argmax_out) *argmax_out = orc_argmax(logits.data(), M->vocab);

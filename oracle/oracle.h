@@ -77,6 +77,10 @@ void orc_attention(const float* q_proj, const float* k_raw, const float* v_raw,
 void orc_sdpa(const uint16_t* query, const uint16_t* key_cache, const uint16_t* value_cache, uint32_t capacity,
               uint32_t base, int m_rows, float* out);
 
+/* RMSNorm whose statistic is summed from per-8-row tile partials (the decode
+ * path's norms after a residual-add launch). */
+void orc_rms_norm_tiles(const uint16_t* x, const uint16_t* w, int cols, uint16_t* out);
+
 /* K20 prefill q4 GEMM: bf16(fma(s, q, b)) dequant, double accumulation, f32 out [m][n]. */
 void orc_q4_gemm(const uint16_t* a, const uint32_t* w, const uint16_t* scales, const uint16_t* biases, int n_rows,
                  int k, int m_rows, float* out);

@@ -17,6 +17,7 @@ _P = C.c_void_p
 _SIGS = {
     "orc_q4_linear": (None, [_P, _P, _P, _P, C.c_int, C.c_int, C.c_int, C.c_int, _P]),
     "orc_rms_norm": (None, [_P, _P, C.c_int, _P]),
+    "orc_rms_norm_tiles": (None, [_P, _P, C.c_int, _P]),
     "orc_q4_gemm": (None, [_P, _P, _P, _P, C.c_int, C.c_int, C.c_int, _P]),
     "orc_model_prefill": (C.c_int, [_P, _P, C.c_int, C.c_int, _P, _P]),
     "orc_residual": (None, [_P, _P, C.c_int, _P]),
@@ -114,6 +115,14 @@ def rms_norm(x_bf16, w_bf16):
     x = _c(x_bf16, np.uint16)
     out = np.empty_like(x)
     lib().orc_rms_norm(p(x), p(_c(w_bf16, np.uint16)), x.size, p(out))
+    return out
+
+
+def rms_norm_tiles(x_bf16, w_bf16):
+    """RMSNorm with the statistic from 8-row tile partials (decode norms after a residual add)."""
+    x = _c(x_bf16, np.uint16)
+    out = np.empty_like(x)
+    lib().orc_rms_norm_tiles(p(x), p(_c(w_bf16, np.uint16)), x.size, p(out))
     return out
 
 

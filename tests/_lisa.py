@@ -62,7 +62,7 @@ class DevQ4:
         self.w, self.s, self.b = w, s, b
 
 
-PROLOGUE_NAMES = ["x", "resnorm", "embed", "cast", "norm", "mtpfc"]
+PROLOGUE_NAMES = ["x", "resnorm", "embed", "cast", "norm", "mtpfc", "prenorm"]
 
 
 def launch_qmv(pkg, dev, K, M, params, mats):
@@ -88,7 +88,8 @@ def launch_qmv(pkg, dev, K, M, params, mats):
     grid = max(1, tiles if params.ksplit == 4 else (tiles + 3) // 4)
     name = f"lisa_qmv_k{K}_m{M}_{PROLOGUE_NAMES[params.pro_mode]}"
     kinds = {kind for _, _, _, kind in mats}
-    if K == 5120 and params.pro_mode == pkg.PRO_RESNORM and kinds in ({pkg.EPI_GATEUP}, {pkg.EPI_ARGMAX}):
+    if K == 5120 and params.pro_mode in (pkg.PRO_RESNORM, pkg.PRO_PRENORM) and kinds in ({pkg.EPI_GATEUP},
+                                                                                    {pkg.EPI_ARGMAX}):
         name += "_gateup" if kinds == {pkg.EPI_GATEUP} else "_argmax"  # the runner's specialized kernels
     dev.dispatch(name, params, (grid,), (256,))
     return params.ksplit, grid

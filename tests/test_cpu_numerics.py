@@ -86,3 +86,18 @@ def test_rms_norm_matches_double():
     xf, wf = orc.bf16_bits_to_f32(x).astype(np.float64), orc.bf16_bits_to_f32(w).astype(np.float64)
     ref = xf / np.sqrt(np.mean(xf**2) + 1e-6) * wf
     assert np.all(np.abs(got - ref) <= np.abs(ref) * 2.0**-8 + 1e-30)
+
+
+def test_rms_norm_tiles_matches_double():
+    """The decode path's RMSNorm whose statistic is summed from per-8-row tile
+    partials: the same closed form as norm.metal:10-47."""
+    rng = np.random.default_rng(4)
+    x = orc.f32_to_bf16_bits((rng.standard_normal(5120) * 3).astype(np.float32))
+    w = orc.f32_to_bf16_bits(rng.uniform(0.9, 1.1, 5120).astype(np.float32))
+    got = orc.bf16_bits_to_f32(orc.rms_norm_tiles(x, w))
+    xf, wf = orc.bf16_bits_to_f32(x).astype(np.float64), orc.bf16_bits_to_f32(w).astype(np.float64)
+    ref = xf / np.sqrt(np.mean(xf**2) + 1e-6) * wf
+    assert np.all(np.abs(got - ref) <= np.abs(ref) * 2.0**-8 + 1e-30)
+    # a different summation order than the single-launch statistic, same value to rounding
+    other = orc.bf16_bits_to_f32(orc.rms_norm(x, w))
+    assert np.max(np.abs(got - other) / np.maximum(np.abs(other), 1e-30)) <= 2.0**-7

@@ -157,6 +157,41 @@ def test_qmv_resnorm_gateup(pkg, orc, dev, M):
     assert np.array_equal(act.read(np.uint16, M * N), want)
 
 
+@pytest.mark.parametrize("M", [1, 3])
+def test_qmv_resid_then_prenorm_gateup(pkg, orc, dev, M):
+    """The decode path's split residual: an out_proj-shaped launch (K=6144)
+    adds its rows into the residual in place and leaves per-tile sums of
+    squares; the gate/up launch normalizes from those partials
+    (norm.metal:10-57 statistic, mlp.metal:6-17)."""
+    rng = np.random.default_rng(70 + M)
+    K, H, N = 6144, 5120, 17408
+    ow, osc, ob = rand_q4(rng, H, K)
+    gw, gs, gb = rand_q4(rng, N, H)
+    uw, us, ub = rand_q4(rng, N, H)
+    x = bf16(rng.standard_normal((M, K)).astype(np.float32))
+    h = bf16((rng.standard_normal((M, H)) * 4).astype(np.float32))
+    nw = bf16(rng.uniform(0.9, 1.1, H).astype(np.float32))
+    xb, hb, nb = dev.upload(x), dev.upload(h), dev.upload(nw)
+    ss = dev.buffer(M * (H // 8) * 4)
+    p = pkg.QmvParams()
+    p.pro_mode = pkg.PRO_LOADX
+    p.x_in, p.h_in, p.ss_part = xb.ptr, hb.ptr, ss.ptr
+    ks, _ = launch_qmv(pkg, dev, K, M, p, [(DevQ4(dev, ow, osc, ob), None, 0, pkg.EPI_RESID)])
+    y = orc.q4_linear(x, ow, osc, ob, H, K, M, ks)
+    r = np.stack([orc.residual(h[m], y[m]) for m in range(M)])
+    assert np.array_equal(hb.read(np.uint16, M * H).reshape(M, H), r)
+    act, xo = dev.buffer(M * N * 2), dev.buffer(M * H * 2)
+    q = pkg.QmvParams()
+    q.pro_mode = pkg.PRO_PRENORM
+    q.h_in, q.ss_part, q.norm_w, q.x_out = hb.ptr, ss.ptr, nb.ptr, xo.ptr
+    ks2, _ = launch_qmv(pkg, dev, H, M, q, [(DevQ4(dev, gw, gs, gb), DevQ4(dev, uw, us, ub), act.ptr, pkg.EPI_GATEUP)])
+    xn = np.stack([orc.rms_norm_tiles(r[m], nw) for m in range(M)])
+    assert np.array_equal(xo.read(np.uint16, M * H).reshape(M, H), xn)
+    g = orc.q4_linear(xn, gw, gs, gb, N, H, M, ks2)
+    u = orc.q4_linear(xn, uw, us, ub, N, H, M, ks2)
+    assert np.array_equal(act.read(np.uint16, M * N), orc.silu_mul(g, u))
+
+
 # ---------------------------------------------------------------- config 1
 @pytest.mark.parametrize("M", [1, 3])
 def test_gdn_layer_config1(pkg, orc, dev, M):
