@@ -100,9 +100,11 @@ DEV float hi_bf(uint32_t u) { return __uint_as_float(u & 0xffff0000u); }
 // iterations [ITER*w/4, ITER*(w+1)/4), and the results are combined as
 // (W0 + W1) + (W2 + W3).
 //
-// One tile per wave, no persistent loop: every wave issues the whole of its
-// weight stream at once (after the few prologue loads, so the prologue never
-// waits for weights), and the dispatcher balances the tail.
+// One tile per wave, no persistent loop: every wave issues its weight stream
+// right behind the prologue loads (so the prologue never waits for weights;
+// under a normalizing prologue only the first iteration goes ahead of it, to
+// keep the register count low enough for the whole grid to be resident), and
+// the dispatcher balances the tail.
 //
 // x lives in LDS (f32, or bf16 for K = 17408), one copy per input row, in
 // 64-element groups padded to 272 (f32) or 144 (bf16) bytes: the 16 lanes of a
@@ -186,13 +188,27 @@ DEV void put_gsum(float* gsum, int m, int k0, bool valid, const float (&x)[8]) {
 
 // RMSNorm statistic of one 5120-wide segment from each thread's partial sum of
 // squares: tree64 per wave, then (W0 + W1) + (W2 + W3).
+// One lane forms the factor and the workgroup reads it back, so the IEEE
+// divide and square root run once per workgroup rather than once per lane.
 DEV float seg_rms_inv(float s, float* red, int tid) {
   s = tree64(s);
   __syncthreads();
   if ((tid & 63) == 0) red[tid >> 6] = s;
   __syncthreads();
-  const float tot = (red[0] + red[1]) + (red[2] + red[3]);
-  return lisa_rsqrt(tot / (float)LISA_HIDDEN + LISA_EPS);
+  if (tid == 0) {
+    const float tot = (red[0] + red[1]) + (red[2] + red[3]);
+    red[4] = lisa_rsqrt(tot / (float)LISA_HIDDEN + LISA_EPS);
+  }
+  __syncthreads();
+  return red[4];
+}
+
+// Eight values rounded to bf16 (returned as floats) and the packed bf16 pairs.
+DEV void round_bf8(const float (&f)[8], float (&x)[8], uint4& packed) {
+  const uint32_t u0 = lisa_f32x2_to_bf16x2(f[0], f[1]), u1 = lisa_f32x2_to_bf16x2(f[2], f[3]);
+  const uint32_t u2 = lisa_f32x2_to_bf16x2(f[4], f[5]), u3 = lisa_f32x2_to_bf16x2(f[6], f[7]);
+  packed = make_uint4(u0, u1, u2, u3);
+  unpack_bf8(packed, x);
 }
 
 // Sources of a normalized segment (pro_mode, or the two halves of MTPFC).
@@ -246,10 +262,13 @@ DEV void seg_process(const LisaQmvParams& p, unsigned char* lds, int m, const Pr
   float* gsum = reinterpret_cast<float*>(lds + C::XBYTES);
   float* red = gsum + M * C::G;
   constexpr int src = seg_source<MODE>(SEG);
+  // chunk 2 (c = tid + 512 < 640) exists on waves 0 and 1 only: a wave-uniform skip
+  const bool has2 = __builtin_amdgcn_readfirstlane(tid >> 6) < 2;
   float v[3][8];
   float ss = 0.0f;
 #pragma unroll
   for (int i = 0; i < 3; ++i) {
+    if (i == 2 && !has2) break;
     const bool valid = tid + 256 * i < kSegChunks;
     float hv[8] = {}, ov[8] = {};
     if constexpr (src == SEG_RESNORM || src == SEG_NORM || src == SEG_PRENORM) unpack_bf8(raw.a[i], hv);
@@ -277,12 +296,15 @@ DEV void seg_process(const LisaQmvParams& p, unsigned char* lds, int m, const Pr
   const bool writer = blockIdx.x == 0;
 #pragma unroll
   for (int i = 0; i < 3; ++i) {
+    if (i == 2 && !has2) break;
     const int c = tid + 256 * i;
     const bool valid = c < kSegChunks;
-    float wv[8], x[8];
+    float wv[8], f[8], x[8];
+    uint4 xb;
     unpack_bf8(raw.w[i], wv);
 #pragma unroll
-    for (int e = 0; e < 8; ++e) x[e] = lisa_bf16r((v[i][e] * inv) * wv[e]);
+    for (int e = 0; e < 8; ++e) f[e] = (v[i][e] * inv) * wv[e];
+    round_bf8(f, x, xb);
     const int k0 = SEG * LISA_HIDDEN + 8 * c;
     if (valid) put_chunk<K, M>(lds, m, k0, x);
     put_gsum<K, M>(gsum, m, k0, valid, x);
@@ -290,9 +312,7 @@ DEV void seg_process(const LisaQmvParams& p, unsigned char* lds, int m, const Pr
       if (MODE != LISA_PRO_MTPFC && p.r_out) {
         reinterpret_cast<uint4*>(p.r_out + (size_t)m * LISA_HIDDEN)[c] = pack_bf8(v[i]);
       }
-      if (p.x_out) {
-        reinterpret_cast<uint4*>(p.x_out + (size_t)m * K + SEG * LISA_HIDDEN)[c] = pack_bf8(x);
-      }
+      if (p.x_out) reinterpret_cast<uint4*>(p.x_out + (size_t)m * K + SEG * LISA_HIDDEN)[c] = xb;
     }
   }
 }
@@ -430,9 +450,9 @@ DEV TileRef tile_ref(const LisaQmvParams& p, uint32_t tile, int rp) {
 // Every load is unconditional (iterations past the wave's range re-read its
 // last one) so the loads of a wave form one straight run.
 template <int K, int IMAX>
-DEV void load_unit(Unit<IMAX>& u, const TileRef& t, int it0, int it1, int li) {
+DEV void load_unit(Unit<IMAX>& u, const TileRef& t, int it0, int it1, int li, int i0, int i1) {
 #pragma unroll
-  for (int i = 0; i < IMAX; ++i) {
+  for (int i = i0; i < i1; ++i) {
     const int ii = max(min(it0 + i, it1 - 1), 0);
     const int g = 16 * ii + li;
     u.a0[i] = t.wp0[2 * g];
@@ -522,13 +542,20 @@ DEV void qmv_body(const LisaQmvParams& p, unsigned char* lds) {
 
   ProRaw<C::RR> raw;
   // issue order: prologue loads, then the weight stream (the fences keep the
-  // scheduler from interleaving them, so the prologue waits only for its own)
+  // scheduler from interleaving them, so the prologue waits only for its own).
+  // A normalizing prologue holds many registers while it works, so only the
+  // first iteration's weights are in flight across it: the rest are issued
+  // after it, which roughly halves the register count and doubles the waves
+  // resident per SIMD (every workgroup of the launch then runs in one round).
   pro_load<K, M, MODE, C::RR>(p, 0, raw);
   __builtin_amdgcn_sched_barrier(0);
   Unit<C::IMAX> u;
-  load_unit<K, C::IMAX>(u, tr, it0, it1, li);
+  constexpr int EARLY = MODE == LISA_PRO_LOADX ? C::IMAX : 1;
+  load_unit<K, C::IMAX>(u, tr, it0, it1, li, 0, EARLY);
   __builtin_amdgcn_sched_barrier(0);
   qmv_prologue<K, M, MODE, C::RR>(p, lds, raw);
+  __builtin_amdgcn_sched_barrier(0);
+  load_unit<K, C::IMAX>(u, tr, it0, it1, li, EARLY, C::IMAX);
 
   float T0[M], T1[M];
 #pragma unroll
@@ -729,10 +756,16 @@ DEV void gdn_body(const LisaGdnParams& p) {
   }
   for (int t = 0; t < rows; ++t) {
     const float* co = p.conv_out + (size_t)t * LISA_GDN_CONV_DIM;
+    // every global read of this row is issued here, ahead of the dependent chain
+    const float* src = co + (wave == 0 ? 0 : LISA_GDN_KEY_DIM) + kh * 128;
+    float c0 = 0.0f, c1 = 0.0f;
+    if (wave < 2) { c0 = src[lane]; c1 = src[lane + 64]; }
+    const float vval = co[2 * LISA_GDN_KEY_DIM + h * 128 + v];
+    const size_t o = (size_t)t * LISA_GDN_VALUE_DIM + h * 128 + tid;
+    float zraw = 0.0f, nwt = 0.0f;
+    if (tid < 128) { zraw = p.z[o]; nwt = bf2f(p.norm_w[tid]); }
     if (wave < 2) {
       // q (wave 0) / k (wave 1) RMS with tree128, scaled 1/128 and 1/sqrt(128)
-      const float* src = co + (wave == 0 ? 0 : LISA_GDN_KEY_DIM) + kh * 128;
-      const float c0 = src[lane], c1 = src[lane + 64];
       const float tot = tree64(c0 * c0 + c1 * c1);
       const float inv = lisa_rsqrt(tot / 128.0f + 1.0e-6f) * (wave == 0 ? p.q_scale : p.k_scale);
       float* dst = wave == 0 ? qn : kn;
@@ -754,7 +787,6 @@ DEV void gdn_body(const LisaGdnParams& p) {
     for (int k = 1; k < 32; ++k) pk = lisa_fma(S[k], kn[32 * q + k], pk);
     pk = pk + xor_lane<1>(pk);
     pk = pk + xor_lane<2>(pk);
-    const float vval = co[2 * LISA_GDN_KEY_DIM + h * 128 + v];
     const float delta = (vval - pk) * beta;
 #pragma unroll
     for (int k = 0; k < 32; ++k) S[k] = lisa_fma(delta, kn[32 * q + k], S[k]);
@@ -779,9 +811,8 @@ DEV void gdn_body(const LisaGdnParams& p) {
     __syncthreads();
     if (tid < 128) {
       const float y = ybuf[tid];
-      const float n = lisa_bf16r((y * sc[2]) * bf2f(p.norm_w[tid]));
-      const size_t o = (size_t)t * LISA_GDN_VALUE_DIM + h * 128 + tid;
-      const float z = lisa_bf16r(p.z[o]);
+      const float n = lisa_bf16r((y * sc[2]) * nwt);
+      const float z = lisa_bf16r(zraw);
       p.gated[o] = lisa_f32_to_bf16(n * lisa_silu_exp(z));
       if (p.y_out) p.y_out[o] = y;
     }
@@ -887,13 +918,32 @@ DEV void attn_partial_body(const LisaAttnParams& p) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const size_t cache_base = (size_t)kvh * p.capacity * HD;
 
-  // 1. rows of the slice already in the cache (positions < base)
+  // 1. rows of the slice already in the cache (positions < base); a full slice
+  // issues all of its loads before the first LDS store
   const int nold = (base > t0) ? (int)min((uint32_t)T, base - t0) : 0;
-  for (int c = tid; c < nold * (HD / 8); c += 256) {
-    const int row = c / (HD / 8), col = (c % (HD / 8)) * 8;
-    const size_t off = cache_base + (size_t)(t0 + row) * HD + col;
-    *reinterpret_cast<uint4*>(&Kt[row * KP + col]) = *reinterpret_cast<const uint4*>(p.key_cache + off);
-    *reinterpret_cast<uint4*>(&Vt[row * HD + col]) = *reinterpret_cast<const uint4*>(p.value_cache + off);
+  if (nold == T) {
+    constexpr int R = T * (HD / 8) / 256;
+    uint4 kr[R], vr[R];
+#pragma unroll
+    for (int i = 0; i < R; ++i) {
+      const int c = tid + 256 * i, row = c / (HD / 8), col = (c % (HD / 8)) * 8;
+      const size_t off = cache_base + (size_t)(t0 + row) * HD + col;
+      kr[i] = *reinterpret_cast<const uint4*>(p.key_cache + off);
+      vr[i] = *reinterpret_cast<const uint4*>(p.value_cache + off);
+    }
+#pragma unroll
+    for (int i = 0; i < R; ++i) {
+      const int c = tid + 256 * i, row = c / (HD / 8), col = (c % (HD / 8)) * 8;
+      *reinterpret_cast<uint4*>(&Kt[row * KP + col]) = kr[i];
+      *reinterpret_cast<uint4*>(&Vt[row * HD + col]) = vr[i];
+    }
+  } else {
+    for (int c = tid; c < nold * (HD / 8); c += 256) {
+      const int row = c / (HD / 8), col = (c % (HD / 8)) * 8;
+      const size_t off = cache_base + (size_t)(t0 + row) * HD + col;
+      *reinterpret_cast<uint4*>(&Kt[row * KP + col]) = *reinterpret_cast<const uint4*>(p.key_cache + off);
+      *reinterpret_cast<uint4*>(&Vt[row * HD + col]) = *reinterpret_cast<const uint4*>(p.value_cache + off);
+    }
   }
   // 2. rows appended by this step that fall into the slice (kv_cache_store_decode)
   if (wave < M) {
@@ -969,6 +1019,7 @@ DEV void attn_merge_body(const LisaAttnParams& p) {
   __syncthreads();
   const float* po = p.part_o + ((size_t)t * LISA_ATT_QH + h) * p.s_max * LISA_ATT_HD + tid;
   float res = 0.0f, tot = 0.0f;
+#pragma unroll 16
   for (int s = 0; s < used; ++s) {
     res = lisa_fma(ws[s], po[(size_t)s * LISA_ATT_HD], res);
     tot = lisa_fma(ws[s], dn[s], tot);
