@@ -373,16 +373,15 @@ DEV void qmv_prologue(const LisaQmvParams& p, unsigned char* lds, ProRaw<R>& raw
 }
 
 template <int M>
-DEV void conv_epilogue(const LisaQmvParams& p, float* out, int c, const float* pr) {
+DEV void conv_epilogue(const LisaQmvParams& p, float* out, int c, const float* pr, const uint32_t (&cs)[3],
+                       uint2 cw) {
   const int C = LISA_GDN_CONV_DIM;
   float hist[3 + M];
 #pragma unroll
-  for (int i = 0; i < 3; ++i) hist[i] = bf2f(p.conv_state[(size_t)i * C + c]);
+  for (int i = 0; i < 3; ++i) hist[i] = lo_bf(cs[i]);
 #pragma unroll
   for (int t = 0; t < M; ++t) hist[3 + t] = lisa_bf16r(pr[t]);
-  float w[4];
-#pragma unroll
-  for (int tap = 0; tap < 4; ++tap) w[tap] = bf2f(p.conv_w[(size_t)c * 4 + tap]);
+  const float w[4] = {lo_bf(cw.x), hi_bf(cw.x), lo_bf(cw.y), hi_bf(cw.y)};
 #pragma unroll
   for (int t = 0; t < M; ++t) {
     // gdn.metal:163-170: acc += x * w over the 4 taps, conv = bf16(acc), out = bf16(silu(conv))
@@ -522,6 +521,31 @@ DEV void group_dot2(const unsigned char* lds, int g, const uint4& a0, const uint
   }
 }
 
+// Global inputs of a tile's epilogue, read at the start of the launch so the
+// epilogue does not begin with a memory round trip: the residual pair h[r0],
+// h[r1] (RESID) or the channel's three conv-state values and four taps (CONV).
+template <int M>
+struct EpiPre {
+  uint32_t h[M];
+  uint32_t cs[3];
+  uint2 cw;
+};
+
+template <int M, int EPI>
+DEV void epi_preload(const LisaQmvParams& p, const TileRef& tr, int li, EpiPre<M>& e) {
+  const uint32_t kind = EPI >= 0 ? (uint32_t)EPI : p.mats[tr.e].kind;
+  if (kind == LISA_EPI_RESID) {
+    const uint32_t r = tr.v1 ? tr.r0 : 0;
+#pragma unroll
+    for (int m = 0; m < M; ++m) e.h[m] = *reinterpret_cast<const uint32_t*>(p.h_in + (size_t)m * LISA_HIDDEN + r);
+  } else if (kind == LISA_EPI_CONV) {
+    const uint32_t c = (li & 1) ? (tr.v1 ? tr.r1 : 0) : (tr.v0 ? tr.r0 : 0);
+#pragma unroll
+    for (int i = 0; i < 3; ++i) e.cs[i] = p.conv_state[(size_t)i * LISA_GDN_CONV_DIM + c];
+    e.cw = *reinterpret_cast<const uint2*>(p.conv_w + (size_t)c * 4);
+  }
+}
+
 // EPI: the epilogue of every matrix of the launch, or -1 to read it per tile.
 template <int K, int M, int MODE, int EPI>
 DEV void qmv_body(const LisaQmvParams& p, unsigned char* lds) {
@@ -556,6 +580,12 @@ DEV void qmv_body(const LisaQmvParams& p, unsigned char* lds) {
   qmv_prologue<K, M, MODE, C::RR>(p, lds, raw);
   __builtin_amdgcn_sched_barrier(0);
   load_unit<K, C::IMAX>(u, tr, it0, it1, li, EARLY, C::IMAX);
+  // epilogue inputs: read here behind the weights for plain-x launches; under a
+  // normalizing prologue registers are too scarce, and they are read at the end
+  constexpr bool PRE = MODE == LISA_PRO_LOADX;
+  EpiPre<M> pre;
+  if constexpr (PRE)
+    if (!C::SPLIT || wv == 0) epi_preload<M, EPI>(p, tr, li, pre);
 
   float T0[M], T1[M];
 #pragma unroll
@@ -596,6 +626,8 @@ DEV void qmv_body(const LisaQmvParams& p, unsigned char* lds) {
 #pragma unroll
   for (int m = 0; m < M; ++m) { best_v[m] = -INFINITY; best_i[m] = 0xffffffffu; }
 
+  if constexpr (!PRE)
+    if (active) epi_preload<M, EPI>(p, tr, li, pre);
   if (active) {
     const LisaQ4Mat& mt = p.mats[tr.e];
     const uint32_t r0 = tr.r0, r1 = tr.r1;
@@ -622,8 +654,8 @@ DEV void qmv_body(const LisaQmvParams& p, unsigned char* lds) {
         break;
       }
       case LISA_EPI_CONV: {
-        if (li == 0 && v0) conv_epilogue<M>(p, static_cast<float*>(mt.out), (int)r0, T0);
-        if (li == 1 && v1) conv_epilogue<M>(p, static_cast<float*>(mt.out), (int)r1, T1);
+        if (li == 0 && v0) conv_epilogue<M>(p, static_cast<float*>(mt.out), (int)r0, T0, pre.cs, pre.cw);
+        if (li == 1 && v1) conv_epilogue<M>(p, static_cast<float*>(mt.out), (int)r1, T1, pre.cs, pre.cw);
         break;
       }
       case LISA_EPI_RESID: {
@@ -634,8 +666,8 @@ DEV void qmv_body(const LisaQmvParams& p, unsigned char* lds) {
         for (int m = 0; m < M; ++m) {
           float ra = 0.0f, rb = 0.0f;
           if (li == 0 && v0 && v1) {
-            ra = lisa_bf16r(bf2f(hres[(size_t)m * LISA_HIDDEN + r0]) + lisa_bf16r(T0[m]));
-            rb = lisa_bf16r(bf2f(hres[(size_t)m * LISA_HIDDEN + r1]) + lisa_bf16r(T1[m]));
+            ra = lisa_bf16r(lo_bf(pre.h[m]) + lisa_bf16r(T0[m]));
+            rb = lisa_bf16r(hi_bf(pre.h[m]) + lisa_bf16r(T1[m]));
             hres[(size_t)m * LISA_HIDDEN + r0] = lisa_f32_to_bf16(ra);
             hres[(size_t)m * LISA_HIDDEN + r1] = lisa_f32_to_bf16(rb);
           }
