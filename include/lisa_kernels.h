@@ -171,7 +171,11 @@ typedef struct LisaSynthParams {
 /* ---- batched prefill ------------------------------------------------------
  * lisa_q4_gemm: C[m][n] (f32, row stride ldc) = A[m][k] (bf16) . deq(W)[n][k]
  * with deq = bf16(fma(scale, q, bias)) (gemm.metal:238-266), bf16 MFMA with f32
- * accumulation. Grid (ceil(n/128), ceil(m/128)) x 256; k multiple of 64. */
+ * accumulation. Grid (ceil(n / LISA_GEMM_TILE_N), ceil(m / LISA_GEMM_TILE_M)) x 256;
+ * k multiple of 64. */
+#define LISA_GEMM_TILE_M 256
+#define LISA_GEMM_TILE_N 128
+
 typedef struct LisaGemmParams {
   const uint16_t* a;
   const uint32_t* w;

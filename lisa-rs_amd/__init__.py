@@ -96,6 +96,7 @@ class GemmParams(C.Structure):
 
 
 ROWS_EMBED, ROWS_NORM, ROWS_RESNORM, ROWS_SILU, ROWS_ARGMAX = range(5)
+GEMM_TILE_M, GEMM_TILE_N = 256, 128  # lisa_q4_gemm output tile (LISA_GEMM_TILE_M/N)
 
 
 class RowsParams(C.Structure):

@@ -1109,7 +1109,8 @@ int launch_gemm(LisaRunner* r, const uint16_t* a, uint32_t m, const Q4Dev& w, fl
   g.n = w.n;
   g.k = w.k;
   g.ldc = w.n;
-  return lisa_launch(r->dev, r->gemm, &g, sizeof g, (w.n + 127) / 128, (m + 127) / 128, 1, 256, 1, 1);
+  return lisa_launch(r->dev, r->gemm, &g, sizeof g, (w.n + LISA_GEMM_TILE_N - 1) / LISA_GEMM_TILE_N,
+                     (m + LISA_GEMM_TILE_M - 1) / LISA_GEMM_TILE_M, 1, 256, 1, 1);
 }
 
 int launch_rows(LisaRunner* r, LisaRowsParams& p, uint32_t gx, uint32_t m) {

@@ -34,7 +34,8 @@ def gemm(pkg, dev, a_bf16, q, m):
     out = dev.buffer(m * q.n * 4)
     ab = dev.upload(a_bf16)
     p = pkg.GemmParams(ab.ptr, q.wbuf.ptr, q.sbbuf.ptr, out.ptr, m, q.n, q.k, q.n)
-    dev.dispatch("lisa_q4_gemm", p, ((q.n + 127) // 128, (m + 127) // 128), (256,))
+    tm, tn = pkg.GEMM_TILE_M, pkg.GEMM_TILE_N
+    dev.dispatch("lisa_q4_gemm", p, ((q.n + tn - 1) // tn, (m + tm - 1) // tm), (256,))
     return out.read(np.float32, m * q.n).reshape(m, q.n)
 
 
