@@ -87,7 +87,10 @@ typedef struct LisaQmvParams {
 } LisaQmvParams;
 
 /* ---- GDN recurrence + gated RMSNorm --------------------------------------
- * Kernels: lisa_gdn_recurrence_m{1,3}; grid 48 workgroups x 512 threads. */
+ * Kernels: lisa_gdn_recurrence_m{1,3}; grid 48 workgroups x 512 threads.
+ * Prefill over m rows: lisa_gdn_prep_rows grid (m, 9) x 256, then
+ * lisa_gdn_scan_rows grid 48 x 512 (y_out required), then lisa_gdn_out_rows
+ * grid (m, 48) x 128; together they equal the decode kernel applied row by row. */
 typedef struct LisaGdnParams {
   const float* conv_out; /* [M][10240] */
   const float* z;        /* [M][6144] raw */
@@ -103,7 +106,9 @@ typedef struct LisaGdnParams {
   float* y_out;    /* nullable: pre-norm readout [M][6144] */
   float q_scale, k_scale;
   uint32_t capture;
-  uint32_t m_rows; /* lisa_gdn_recurrence_rows: number of rows (time steps) */
+  uint32_t m_rows; /* prefill kernels: number of rows (time steps) */
+  float* qk;       /* prefill: normalized q, k per row [m][2][2048] */
+  float* gates;    /* prefill: (beta, decay) per row and value head [m][48][2] */
 } LisaGdnParams;
 
 /* ---- split-K decode attention --------------------------------------------

@@ -79,7 +79,7 @@ class GdnParams(C.Structure):
                 ("a_log", C.c_uint64), ("dt_bias", C.c_uint64), ("norm_w", C.c_uint64),
                 ("state", C.c_uint64), ("slots", C.c_uint64), ("slot_stride", C.c_uint64),
                 ("gated", C.c_uint64), ("y_out", C.c_uint64), ("q_scale", C.c_float), ("k_scale", C.c_float),
-                ("capture", C.c_uint32), ("m_rows", C.c_uint32)]
+                ("capture", C.c_uint32), ("m_rows", C.c_uint32), ("qk", C.c_uint64), ("gates", C.c_uint64)]
 
 
 class AttnParams(C.Structure):

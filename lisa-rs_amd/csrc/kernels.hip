@@ -11,7 +11,7 @@
 //   lisa_step_finalize    argmax finish + device-side token/position feedback [F5]
 //   lisa_synth_fill       seeded synthetic tensors
 //   lisa_copy_bytes       device-to-device copy
-//   lisa_q4_gemm, lisa_rows, lisa_gdn_conv_rows, lisa_gdn_recurrence_rows,
+//   lisa_q4_gemm, lisa_rows, lisa_gdn_conv_rows, lisa_gdn_{prep,scan,out}_rows,
 //   lisa_attn_{store,partial,merge}_rows   batched prefill [F1 GEMM, F4-F14 rows forms]
 //
 // Numerics: every expression below is written in the evaluation order the CPU
@@ -773,9 +773,55 @@ QMV_KERNEL_EPI(5120, 3, LISA_PRO_PRENORM, prenorm, LISA_EPI_ARGMAX, argmax)
 // thread (v, q) = (tid/4, tid%4) owns state row v, columns [32q, 32q+32).
 // ===========================================================================
 // M = 0: the row count comes from p.m_rows (prefill).
+// q or k of one key head (gdn.metal q/k norm): RMS over 128 values as tree64 of
+// c0^2 + c1^2 (lane l holds c[l], c[l+64]), scaled, rounded to bf16.
+DEV void gdn_qk_norm(float c0, float c1, float scale, float& n0, float& n1) {
+  const float tot = tree64(c0 * c0 + c1 * c1);
+  const float inv = lisa_rsqrt(tot / 128.0f + 1.0e-6f) * scale;
+  n0 = lisa_bf16r(c0 * inv);
+  n1 = lisa_bf16r(c1 * inv);
+}
+
+// beta = sigmoid(b), decay = exp(-exp(a_log) softplus(a + dt_bias)) of one value head.
+DEV void gdn_gates(float braw, float araw, uint16_t dt_bias, uint16_t a_log, float& beta, float& decay) {
+  beta = lisa_bf16r(lisa_sigmoid_exp(lisa_bf16r(braw)));
+  const float dt_arg = lisa_bf16r(lisa_bf16r(araw) + bf2f(dt_bias));
+  const float dt = lisa_bf16r(lisa_softplus(dt_arg));
+  decay = lisa_expf(-lisa_expf(bf2f(a_log)) * dt);
+}
+
+// One time step of state row v, quarter q (S = the row's 32 elements 32q..32q+31;
+// kq, qq = the matching 32 elements of k and q): decay, delta rule, readout.
+// Returns the row's readout (the four quarters combined by xor 1, 2).
+DEV float gdn_row_step(float (&S)[32], const float* kq, const float* qq, float vval, float beta, float decay) {
+#pragma unroll
+  for (int k = 0; k < 32; ++k) S[k] = S[k] * decay;
+  float pk = S[0] * kq[0];
+#pragma unroll
+  for (int k = 1; k < 32; ++k) pk = lisa_fma(S[k], kq[k], pk);
+  pk = pk + xor_lane<1>(pk);
+  pk = pk + xor_lane<2>(pk);
+  const float delta = (vval - pk) * beta;
+#pragma unroll
+  for (int k = 0; k < 32; ++k) S[k] = lisa_fma(delta, kq[k], S[k]);
+  float py = S[0] * qq[0];
+#pragma unroll
+  for (int k = 1; k < 32; ++k) py = lisa_fma(S[k], qq[k], py);
+  py = py + xor_lane<1>(py);
+  py = py + xor_lane<2>(py);
+  return py;
+}
+
+// Gated RMSNorm output of one element: bf16(bf16(y rinv w) silu(bf16 z)).
+DEV uint16_t gdn_gated(float y, float rinv, float nw, float zraw) {
+  const float n = lisa_bf16r((y * rinv) * nw);
+  const float z = lisa_bf16r(zraw);
+  return lisa_f32_to_bf16(n * lisa_silu_exp(z));
+}
+
 template <int M>
 DEV void gdn_body(const LisaGdnParams& p) {
-  const int rows = M ? M : (int)p.m_rows;
+  const int rows = M;
   const int h = blockIdx.x, kh = h / (LISA_GDN_VH / LISA_GDN_KH);
   const int tid = threadIdx.x, v = tid >> 2, q = tid & 3, lane = tid & 63, wave = tid >> 6;
   __shared__ float qn[128], kn[128], ybuf[128], sc[4];
@@ -798,35 +844,17 @@ DEV void gdn_body(const LisaGdnParams& p) {
     if (tid < 128) { zraw = p.z[o]; nwt = bf2f(p.norm_w[tid]); }
     if (wave < 2) {
       // q (wave 0) / k (wave 1) RMS with tree128, scaled 1/128 and 1/sqrt(128)
-      const float tot = tree64(c0 * c0 + c1 * c1);
-      const float inv = lisa_rsqrt(tot / 128.0f + 1.0e-6f) * (wave == 0 ? p.q_scale : p.k_scale);
+      float n0, n1;
+      gdn_qk_norm(c0, c1, wave == 0 ? p.q_scale : p.k_scale, n0, n1);
       float* dst = wave == 0 ? qn : kn;
-      dst[lane] = lisa_bf16r(c0 * inv);
-      dst[lane + 64] = lisa_bf16r(c1 * inv);
+      dst[lane] = n0;
+      dst[lane + 64] = n1;
     } else if (tid == 128) {
-      const float beta = lisa_bf16r(lisa_sigmoid_exp(lisa_bf16r(p.b[(size_t)t * LISA_GDN_VH + h])));
-      const float dt_arg = lisa_bf16r(lisa_bf16r(p.a[(size_t)t * LISA_GDN_VH + h]) + bf2f(p.dt_bias[h]));
-      const float dt = lisa_bf16r(lisa_softplus(dt_arg));
-      sc[0] = beta;
-      sc[1] = lisa_expf(-lisa_expf(bf2f(p.a_log[h])) * dt);
+      gdn_gates(p.b[(size_t)t * LISA_GDN_VH + h], p.a[(size_t)t * LISA_GDN_VH + h], p.dt_bias[h], p.a_log[h], sc[0],
+                sc[1]);
     }
     __syncthreads();
-    const float beta = sc[0], decay = sc[1];
-#pragma unroll
-    for (int k = 0; k < 32; ++k) S[k] = S[k] * decay;
-    float pk = S[0] * kn[32 * q];
-#pragma unroll
-    for (int k = 1; k < 32; ++k) pk = lisa_fma(S[k], kn[32 * q + k], pk);
-    pk = pk + xor_lane<1>(pk);
-    pk = pk + xor_lane<2>(pk);
-    const float delta = (vval - pk) * beta;
-#pragma unroll
-    for (int k = 0; k < 32; ++k) S[k] = lisa_fma(delta, kn[32 * q + k], S[k]);
-    float py = S[0] * qn[32 * q];
-#pragma unroll
-    for (int k = 1; k < 32; ++k) py = lisa_fma(S[k], qn[32 * q + k], py);
-    py = py + xor_lane<1>(py);
-    py = py + xor_lane<2>(py);
+    const float py = gdn_row_step(S, kn + 32 * q, qn + 32 * q, vval, sc[0], sc[1]);
     if (q == 0) ybuf[v] = lisa_bf16r(py);
     if (p.capture && p.slots && t + 1 < rows) {
       float4* dst = reinterpret_cast<float4*>(p.slots + (size_t)t * p.slot_stride + (size_t)h * 128 * 128 +
@@ -843,9 +871,7 @@ DEV void gdn_body(const LisaGdnParams& p) {
     __syncthreads();
     if (tid < 128) {
       const float y = ybuf[tid];
-      const float n = lisa_bf16r((y * sc[2]) * nwt);
-      const float z = lisa_bf16r(zraw);
-      p.gated[o] = lisa_f32_to_bf16(n * lisa_silu_exp(z));
+      p.gated[o] = gdn_gated(y, sc[2], nwt, zraw);
       if (p.y_out) p.y_out[o] = y;
     }
     __syncthreads();
@@ -855,9 +881,107 @@ DEV void gdn_body(const LisaGdnParams& p) {
     reinterpret_cast<float4*>(srow)[i] = make_float4(S[4 * i], S[4 * i + 1], S[4 * i + 2], S[4 * i + 3]);
 }
 
+// Prefill over rows, in three launches with the arithmetic of gdn_body:
+// lisa_gdn_prep_rows (grid (m, 9) x 256): normalized q and k of every row and
+//   key head into qk [m][2][2048], beta and decay into gates [m][48][2];
+// lisa_gdn_scan_rows (grid 48 x 512): the sequential delta-rule scan, with no
+//   barrier in the time loop (each state row only needs the precomputed
+//   inputs), the next row's inputs loaded while the current one is reduced;
+//   readout y (bf16 values) into y_out [m][6144];
+// lisa_gdn_out_rows (grid (m, 48) x 128): gated RMSNorm of y into gated.
+extern "C" __global__ __launch_bounds__(256) void lisa_gdn_prep_rows(LisaGdnParams p) {
+  const int t = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const float* co = p.conv_out + (size_t)t * LISA_GDN_CONV_DIM;
+  if (blockIdx.y < 8) {
+    const int pi = blockIdx.y * 4 + wave, which = pi / LISA_GDN_KH, kh = pi % LISA_GDN_KH;
+    const float* src = co + which * LISA_GDN_KEY_DIM + kh * 128;
+    float n0, n1;
+    gdn_qk_norm(src[lane], src[lane + 64], which == 0 ? p.q_scale : p.k_scale, n0, n1);
+    float* dst = p.qk + ((size_t)t * 2 + which) * LISA_GDN_KEY_DIM + kh * 128;
+    dst[lane] = n0;
+    dst[lane + 64] = n1;
+  } else if (tid < LISA_GDN_VH) {
+    float beta, decay;
+    gdn_gates(p.b[(size_t)t * LISA_GDN_VH + tid], p.a[(size_t)t * LISA_GDN_VH + tid], p.dt_bias[tid], p.a_log[tid],
+              beta, decay);
+    reinterpret_cast<float2*>(p.gates)[(size_t)t * LISA_GDN_VH + tid] = make_float2(beta, decay);
+  }
+}
+
+// Per-row inputs of the scan as one lane sees them: its 16 B of the row's k
+// (lanes 0-31) or q (lanes 32-63) of the key head, the head's (beta, decay) and
+// the state row's v value.
+struct GdnRowIn {
+  float4 kq;
+  float2 g;
+  float v;
+};
+
+DEV void gdn_row_load(const LisaGdnParams& p, int t, int h, int kh, int v, int lane, GdnRowIn& in) {
+  const int which = lane < 32 ? 1 : 0;  // k, then q
+  in.kq = reinterpret_cast<const float4*>(p.qk + ((size_t)t * 2 + which) * LISA_GDN_KEY_DIM + kh * 128)[lane & 31];
+  in.g = reinterpret_cast<const float2*>(p.gates)[(size_t)t * LISA_GDN_VH + h];
+  in.v = p.conv_out[(size_t)t * LISA_GDN_CONV_DIM + 2 * LISA_GDN_KEY_DIM + h * 128 + v];
+}
+
+extern "C" __global__ __launch_bounds__(512) void lisa_gdn_scan_rows(LisaGdnParams p) {
+  const int rows = (int)p.m_rows;
+  const int h = blockIdx.x, kh = h / (LISA_GDN_VH / LISA_GDN_KH);
+  const int tid = threadIdx.x, v = tid >> 2, q = tid & 3, lane = tid & 63, wave = tid >> 6;
+  // each wave stages the row's k and q in its own LDS slot (a wave reads only
+  // what it wrote, so no workgroup barrier is needed)
+  __shared__ float4 kqs[8][64];
+  float* srow = p.state + (size_t)h * 128 * 128 + (size_t)v * 128 + 32 * q;
+  float S[32];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const float4 f = reinterpret_cast<const float4*>(srow)[i];
+    S[4 * i] = f.x; S[4 * i + 1] = f.y; S[4 * i + 2] = f.z; S[4 * i + 3] = f.w;
+  }
+  auto step = [&](const GdnRowIn& in, int t) {
+    kqs[wave][lane] = in.kq;
+    float kv[32], qv[32];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const float4 k4 = kqs[wave][8 * q + i], q4 = kqs[wave][32 + 8 * q + i];
+      kv[4 * i] = k4.x; kv[4 * i + 1] = k4.y; kv[4 * i + 2] = k4.z; kv[4 * i + 3] = k4.w;
+      qv[4 * i] = q4.x; qv[4 * i + 1] = q4.y; qv[4 * i + 2] = q4.z; qv[4 * i + 3] = q4.w;
+    }
+    const float py = gdn_row_step(S, kv, qv, in.v, in.g.x, in.g.y);
+    if (q == 0) p.y_out[(size_t)t * LISA_GDN_VALUE_DIM + h * 128 + v] = lisa_bf16r(py);
+  };
+  // two input sets in turn: the next row's loads are in flight during a step
+  GdnRowIn ia, ib;
+  gdn_row_load(p, 0, h, kh, v, lane, ia);
+  for (int t = 0; t < rows; t += 2) {
+    gdn_row_load(p, min(t + 1, rows - 1), h, kh, v, lane, ib);
+    step(ia, t);
+    if (t + 1 >= rows) break;
+    gdn_row_load(p, min(t + 2, rows - 1), h, kh, v, lane, ia);
+    step(ib, t + 1);
+  }
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+    reinterpret_cast<float4*>(srow)[i] = make_float4(S[4 * i], S[4 * i + 1], S[4 * i + 2], S[4 * i + 3]);
+}
+
+extern "C" __global__ __launch_bounds__(128) void lisa_gdn_out_rows(LisaGdnParams p) {
+  const int t = blockIdx.x, h = blockIdx.y, tid = threadIdx.x, lane = tid & 63;
+  __shared__ float rinv;
+  const size_t o = (size_t)t * LISA_GDN_VALUE_DIM + h * 128;
+  const float y = p.y_out[o + tid];
+  const float zraw = p.z[o + tid], nwt = bf2f(p.norm_w[tid]);
+  if (tid < 64) {
+    const float y0 = y, y1 = p.y_out[o + lane + 64];
+    const float tot = tree64(y0 * y0 + y1 * y1);
+    if (lane == 0) rinv = lisa_rsqrt(tot / 128.0f + LISA_EPS);
+  }
+  __syncthreads();
+  p.gated[o + tid] = gdn_gated(y, rinv, nwt, zraw);
+}
+
 extern "C" __global__ __launch_bounds__(512) void lisa_gdn_recurrence_m1(LisaGdnParams p) { gdn_body<1>(p); }
 extern "C" __global__ __launch_bounds__(512) void lisa_gdn_recurrence_m3(LisaGdnParams p) { gdn_body<3>(p); }
-extern "C" __global__ __launch_bounds__(512) void lisa_gdn_recurrence_rows(LisaGdnParams p) { gdn_body<0>(p); }
 
 // ===========================================================================
 // split-K decode attention

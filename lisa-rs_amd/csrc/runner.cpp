@@ -100,7 +100,8 @@ struct LisaRunner {
   LisaFunction *qmv_epi[2][7][5] = {};  // K = 5120 with a fixed epilogue: [m3][prologue][epilogue]
   LisaFunction *gdn[2] = {}, *attn_part[2] = {}, *attn_merge[2] = {}, *finalize = nullptr, *synth = nullptr;
   // batched prefill
-  LisaFunction *gemm = nullptr, *rows = nullptr, *conv_rows = nullptr, *gdn_rows = nullptr, *attn_store_rows = nullptr,
+  LisaFunction *gemm = nullptr, *rows = nullptr, *conv_rows = nullptr, *gdn_prep_rows = nullptr, *gdn_scan_rows = nullptr,
+               *gdn_out_rows = nullptr, *attn_store_rows = nullptr,
                *attn_partial_rows = nullptr, *attn_merge_rows = nullptr;
   // memory
   LisaBuffer *weights = nullptr, *state = nullptr, *scratch = nullptr;
@@ -127,6 +128,7 @@ struct LisaRunner {
     float *B = nullptr, *qkv = nullptr, *conv_out = nullptr, *z = nullptr, *a = nullptr, *b = nullptr;
     float *q_proj = nullptr, *k_raw = nullptr, *v_raw = nullptr, *G = nullptr, *U = nullptr, *logits = nullptr;
     float *part_o = nullptr, *part_ml = nullptr;
+    float *gdn_qk = nullptr, *gdn_gates = nullptr, *gdn_y = nullptr;
   } pf;
   // host mirrors
   uint32_t position = 0;
@@ -695,7 +697,9 @@ extern "C" int lisa_runner_create(const LisaRunnerConfig* cfg, LisaRunner** out)
   LISA_TRY(lisa_function_get(r->mod, "lisa_q4_gemm", &r->gemm));
   LISA_TRY(lisa_function_get(r->mod, "lisa_rows", &r->rows));
   LISA_TRY(lisa_function_get(r->mod, "lisa_gdn_conv_rows", &r->conv_rows));
-  LISA_TRY(lisa_function_get(r->mod, "lisa_gdn_recurrence_rows", &r->gdn_rows));
+  LISA_TRY(lisa_function_get(r->mod, "lisa_gdn_prep_rows", &r->gdn_prep_rows));
+  LISA_TRY(lisa_function_get(r->mod, "lisa_gdn_scan_rows", &r->gdn_scan_rows));
+  LISA_TRY(lisa_function_get(r->mod, "lisa_gdn_out_rows", &r->gdn_out_rows));
   LISA_TRY(lisa_function_get(r->mod, "lisa_attn_store_rows", &r->attn_store_rows));
   LISA_TRY(lisa_function_get(r->mod, "lisa_attn_partial_rows", &r->attn_partial_rows));
   LISA_TRY(lisa_function_get(r->mod, "lisa_attn_merge_rows", &r->attn_merge_rows));
@@ -741,7 +745,7 @@ extern "C" void lisa_runner_free(LisaRunner* r) {
     for (auto& b : a)
       for (LisaFunction* f : b) delete f;
   for (LisaFunction* f : {r->gdn[0], r->gdn[1], r->attn_part[0], r->attn_part[1], r->attn_merge[0], r->attn_merge[1],
-                          r->finalize, r->synth, r->gemm, r->rows, r->conv_rows, r->gdn_rows, r->attn_store_rows,
+                          r->finalize, r->synth, r->gemm, r->rows, r->conv_rows, r->gdn_prep_rows, r->gdn_scan_rows, r->gdn_out_rows, r->attn_store_rows,
                           r->attn_partial_rows, r->attn_merge_rows})
     delete f;
   lisa_buffer_free(r->pf.buf);
@@ -1077,6 +1081,9 @@ void plan_prefill(LisaRunner* r, Arena& A) {
   P.U = A.take<float>(c * LISA_INTER);
   P.act = A.take<uint16_t>(c * LISA_INTER);
   P.logits = A.take<float>(c * (size_t)r->cfg.vocab);
+  P.gdn_qk = A.take<float>(c * 2 * LISA_GDN_KEY_DIM);
+  P.gdn_gates = A.take<float>(c * 2 * LISA_GDN_VH);
+  P.gdn_y = A.take<float>(c * LISA_GDN_VALUE_DIM);
   // slice partials of one attention sub-block: at most ~1 GiB
   const size_t per_row = (size_t)LISA_ATT_QH * r->s_max * (LISA_ATT_HD + 2) * sizeof(float);
   uint32_t ar = (uint32_t)std::min<size_t>(kPrefillRows, std::max<size_t>(4, (size_t(1) << 30) / per_row));
@@ -1171,7 +1178,12 @@ int prefill_chunk(LisaRunner* r, uint32_t m) {
       g.q_scale = inv * inv;
       g.k_scale = inv;
       g.m_rows = m;
-      LISA_TRY(lisa_launch(r->dev, r->gdn_rows, &g, sizeof g, LISA_GDN_VH, 1, 1, 512, 1, 1));
+      g.qk = P.gdn_qk;
+      g.gates = P.gdn_gates;
+      g.y_out = P.gdn_y;
+      LISA_TRY(lisa_launch(r->dev, r->gdn_prep_rows, &g, sizeof g, m, 9, 1, 256, 1, 1));
+      LISA_TRY(lisa_launch(r->dev, r->gdn_scan_rows, &g, sizeof g, LISA_GDN_VH, 1, 1, 512, 1, 1));
+      LISA_TRY(lisa_launch(r->dev, r->gdn_out_rows, &g, sizeof g, m, LISA_GDN_VH, 1, 128, 1, 1));
       LISA_TRY(launch_gemm(r, P.gated, m, l.out, P.B));
     } else {
       LISA_TRY(launch_gemm(r, P.X, m, l.q, P.q_proj));

@@ -127,14 +127,18 @@ def test_gdn_rows_bit_exact(pkg, orc, dev):
     s0 = (rng.standard_normal(VH * HD * HD) * 0.01).astype(np.float32)
     zb, ab_, bb, alb, dtb, nwb, stb = (dev.upload(x) for x in (z, a, b, a_log, dt_bias, nw, s0))
     gb = dev.buffer(m * VH * HD * 2)
+    qkb, gtb, yb = dev.buffer(m * 2 * 2048 * 4), dev.buffer(m * VH * 2 * 4), dev.buffer(m * VH * HD * 4)
     inv = 1.0 / np.sqrt(np.float32(128))
     p = pkg.GdnParams(conv_out=cob.ptr, z=zb.ptr, a=ab_.ptr, b=bb.ptr, a_log=alb.ptr, dt_bias=dtb.ptr, norm_w=nwb.ptr,
-                      state=stb.ptr, gated=gb.ptr, q_scale=float(np.float32(inv * inv)), k_scale=float(np.float32(inv)),
-                      m_rows=m)
-    dev.dispatch("lisa_gdn_recurrence_rows", p, (VH,), (512,))
-    gated, st, _, _ = orc.gdn_recurrence(co, z, a, b, a_log, dt_bias, nw, s0, m)
+                      state=stb.ptr, gated=gb.ptr, y_out=yb.ptr, q_scale=float(np.float32(inv * inv)),
+                      k_scale=float(np.float32(inv)), m_rows=m, qk=qkb.ptr, gates=gtb.ptr)
+    dev.dispatch("lisa_gdn_prep_rows", p, (m, 9), (256,))
+    dev.dispatch("lisa_gdn_scan_rows", p, (VH,), (512,))
+    dev.dispatch("lisa_gdn_out_rows", p, (m, VH), (128,))
+    gated, st, y, _ = orc.gdn_recurrence(co, z, a, b, a_log, dt_bias, nw, s0, m)
     assert np.array_equal(gb.read(np.uint16, m * VH * HD).reshape(m, -1), gated)
     assert np.array_equal(stb.read(np.float32, VH * HD * HD).view(np.uint32), st.view(np.uint32))
+    assert np.array_equal(yb.read(np.float32, m * VH * HD).reshape(m, -1).view(np.uint32), y.view(np.uint32))
 
 
 def test_attention_rows_bit_exact(pkg, orc, dev):
