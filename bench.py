@@ -186,7 +186,7 @@ def main():
     traffic = traffic_per_launch()
 
     # config 3 prompt phase: batched prefill of PREFILL_TOKENS uniform random ids
-    # from an empty state (runner.rs:2129-2230, 512-row chunks)
+    # from an empty state (runner.rs:2129-2230; 2048-row chunks, the default)
     prefill = None
     if args.prefill_tokens > 0:
         rng = np.random.default_rng(PROMPT_SEED)
@@ -201,7 +201,7 @@ def main():
         pkg._check(L.lisa_event_elapsed_ms(ev0, ev1, pkg.C.byref(ms)))
         pf_s = ms.value / 1e3
         flops = 2.0 * q4_params() * args.prefill_tokens
-        prefill = {"tokens": args.prefill_tokens, "chunk_rows": 512, "ms": round(ms.value, 2),
+        prefill = {"tokens": args.prefill_tokens, "chunk_rows": min(args.prefill_tokens, 2048), "ms": round(ms.value, 2),
                    "tok_s": round(args.prefill_tokens / pf_s, 1),
                    "gemm_tflops_effective": round(flops / pf_s / 1e12, 1),
                    "note": "q4 GEMM FLOPs / whole prefill time (includes GDN, attention, norms)"}

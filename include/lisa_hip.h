@@ -166,7 +166,8 @@ enum {
 int lisa_runner_profile_step(LisaRunner* r, uint32_t token, int32_t steps, float* kind_ms, int32_t* kind_count);
 
 /* forward_prefill_with_progress (runner.rs:2129-2230): the `n` prompt tokens
- * in chunks of `chunk` rows (<= 512, the reference's PREFILL_BATCH; 0 = 512)
+ * in chunks of `chunk` rows (<= 2048; 0 = 2048; the reference's PREFILL_BATCH
+ * is 512, and the result is the same for every chunk size)
  * with q4 GEMMs (bf16 MFMA), batched GDN and attention; GDN/conv state and KV
  * carry across chunks. argmax_out[n] (nullable) gets each position's greedy
  * token, hidden_out (nullable) f32[n][5120] the hidden before the final norm.

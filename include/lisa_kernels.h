@@ -215,6 +215,10 @@ typedef struct LisaRowsParams {
   uint32_t mode;
 } LisaRowsParams;
 
+/* lisa_attn_partial_rows takes LISA_ATT_ROWS_PER_WG rows per workgroup:
+ * grid (s_max, 4, ceil(m / LISA_ATT_ROWS_PER_WG)) x 256. */
+#define LISA_ATT_ROWS_PER_WG 8
+
 /* lisa_gdn_conv_rows: causal conv + SiLU over m rows per channel with the
  * carried history, grid ceil(10240/256) x 256. */
 typedef struct LisaConvRowsParams {

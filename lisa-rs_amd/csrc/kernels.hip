@@ -1473,17 +1473,27 @@ extern "C" __global__ __launch_bounds__(256) void lisa_gdn_conv_rows(LisaConvRow
   float w[4];
 #pragma unroll
   for (int tap = 0; tap < 4; ++tap) w[tap] = bf2f(p.conv_w[(size_t)c * 4 + tap]);
-  for (uint32_t t = 0; t < p.m_rows; ++t) {
-    const float x = lisa_bf16r(p.qkv[(size_t)t * C + c]);
-    float acc = 0.0f;
-    acc = acc + h0 * w[0];
-    acc = acc + h1 * w[1];
-    acc = acc + h2 * w[2];
-    acc = acc + x * w[3];
-    p.conv_out[(size_t)t * C + c] = lisa_bf16r(lisa_silu_exp(lisa_bf16r(acc)));
-    h0 = h1;
-    h1 = h2;
-    h2 = x;
+  // rows in batches of 16: the batch's loads are all in flight before its
+  // (sequential) history update
+  constexpr int RB = 16;
+  for (uint32_t t0 = 0; t0 < p.m_rows; t0 += RB) {
+    float xs[RB];
+#pragma unroll
+    for (int j = 0; j < RB; ++j) xs[j] = p.qkv[(size_t)min(t0 + j, p.m_rows - 1) * C + c];
+#pragma unroll
+    for (int j = 0; j < RB; ++j) {
+      if (t0 + j >= p.m_rows) break;
+      const float x = lisa_bf16r(xs[j]);
+      float acc = 0.0f;
+      acc = acc + h0 * w[0];
+      acc = acc + h1 * w[1];
+      acc = acc + h2 * w[2];
+      acc = acc + x * w[3];
+      p.conv_out[(size_t)(t0 + j) * C + c] = lisa_bf16r(lisa_silu_exp(lisa_bf16r(acc)));
+      h0 = h1;
+      h1 = h2;
+      h2 = x;
+    }
   }
   p.conv_state[c] = lisa_f32_to_bf16(h0);
   p.conv_state[C + c] = lisa_f32_to_bf16(h1);
@@ -1519,7 +1529,7 @@ extern "C" __global__ __launch_bounds__(256) void lisa_attn_store_rows(LisaAttnP
 
 // 2. slice partials: grid (s_max, 4, ceil(m / ATT_RB)); a workgroup takes one
 //    64-token slice of one KV head for ATT_RB rows.
-constexpr int ATT_RB = 4;
+constexpr int ATT_RB = LISA_ATT_ROWS_PER_WG;
 extern "C" __global__ __launch_bounds__(256) void lisa_attn_partial_rows(LisaAttnParams p) {
   constexpr int T = LISA_ATT_SLICE, HD = LISA_ATT_HD, KP = HD + 8;
   const uint32_t base = *p.pos;

@@ -1056,7 +1056,10 @@ extern "C" int lisa_mtp_trim_state(LisaRunner* r, int32_t count) {
 // =============================================================================
 namespace {
 
-constexpr uint32_t kPrefillRows = 512;  // PREFILL_BATCH (runner.rs:51)
+// Rows per prefill chunk. The reference uses 512 (PREFILL_BATCH, runner.rs:51);
+// the result does not depend on the chunk (the recurrent state and the KV cache
+// carry across chunks), and 2048-row GEMMs keep the matrix cores far busier.
+constexpr uint32_t kPrefillRows = 2048;
 
 void plan_prefill(LisaRunner* r, Arena& A) {
   auto& P = r->pf;
@@ -1086,8 +1089,9 @@ void plan_prefill(LisaRunner* r, Arena& A) {
   P.gdn_y = A.take<float>(c * LISA_GDN_VALUE_DIM);
   // slice partials of one attention sub-block: at most ~1 GiB
   const size_t per_row = (size_t)LISA_ATT_QH * r->s_max * (LISA_ATT_HD + 2) * sizeof(float);
-  uint32_t ar = (uint32_t)std::min<size_t>(kPrefillRows, std::max<size_t>(4, (size_t(1) << 30) / per_row));
-  P.att_rows = ar & ~3u;
+  const uint32_t rb = LISA_ATT_ROWS_PER_WG;
+  uint32_t ar = (uint32_t)std::min<size_t>(kPrefillRows, std::max<size_t>(rb, (size_t(1) << 30) / per_row));
+  P.att_rows = ar / rb * rb;
   P.part_o = A.take<float>((size_t)P.att_rows * LISA_ATT_QH * r->s_max * LISA_ATT_HD);
   P.part_ml = A.take<float>((size_t)P.att_rows * LISA_ATT_QH * r->s_max * 2);
 }
@@ -1216,7 +1220,8 @@ int prefill_chunk(LisaRunner* r, uint32_t m) {
         b.pos = P.pos + 1 + r0 / P.att_rows;
         b.m_rows = ms;
         const uint32_t slices = (r->position + r0 + ms + LISA_ATT_SLICE - 1) / LISA_ATT_SLICE;
-        LISA_TRY(lisa_launch(r->dev, r->attn_partial_rows, &b, sizeof b, slices, LISA_ATT_KVH, (ms + 3) / 4, 256, 1,
+        LISA_TRY(lisa_launch(r->dev, r->attn_partial_rows, &b, sizeof b, slices, LISA_ATT_KVH,
+                             (ms + LISA_ATT_ROWS_PER_WG - 1) / LISA_ATT_ROWS_PER_WG, 256, 1,
                              1));
         LISA_TRY(lisa_launch(r->dev, r->attn_merge_rows, &b, sizeof b, LISA_ATT_QH, ms, 1, 256, 1, 1));
       }
