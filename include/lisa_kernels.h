@@ -89,7 +89,7 @@ typedef struct LisaQmvParams {
 /* ---- GDN recurrence + gated RMSNorm --------------------------------------
  * Kernels: lisa_gdn_recurrence_m{1,3}; grid 48 workgroups x 512 threads.
  * Prefill over m rows: lisa_gdn_prep_rows grid (m, 9) x 256, then
- * lisa_gdn_scan_rows grid 48 x 512 (y_out required), then lisa_gdn_out_rows
+ * lisa_gdn_scan_rows grid (48, 2) x 256 (y_out required), then lisa_gdn_out_rows
  * grid (m, 48) x 128; together they equal the decode kernel applied row by row. */
 typedef struct LisaGdnParams {
   const float* conv_out; /* [M][10240] */
@@ -220,7 +220,7 @@ typedef struct LisaRowsParams {
 #define LISA_ATT_ROWS_PER_WG 8
 
 /* lisa_gdn_conv_rows: causal conv + SiLU over m rows per channel with the
- * carried history, grid ceil(10240/256) x 256. */
+ * carried history, grid (ceil(10240/256), ceil(m/64)) x 256. */
 typedef struct LisaConvRowsParams {
   const float* qkv;        /* f32 [m][10240] */
   const uint16_t* conv_w;  /* bf16 [10240][4] */

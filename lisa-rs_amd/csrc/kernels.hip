@@ -884,9 +884,10 @@ DEV void gdn_body(const LisaGdnParams& p) {
 // Prefill over rows, in three launches with the arithmetic of gdn_body:
 // lisa_gdn_prep_rows (grid (m, 9) x 256): normalized q and k of every row and
 //   key head into qk [m][2][2048], beta and decay into gates [m][48][2];
-// lisa_gdn_scan_rows (grid 48 x 512): the sequential delta-rule scan, with no
-//   barrier in the time loop (each state row only needs the precomputed
-//   inputs), the next row's inputs loaded while the current one is reduced;
+// lisa_gdn_scan_rows (grid (48, 2) x 256, 64 state rows per workgroup): the
+//   sequential delta-rule scan, with no barrier in the time loop (each state
+//   row only needs the precomputed inputs), one wave per SIMD, the next row's
+//   inputs loaded while the current one is reduced;
 //   readout y (bf16 values) into y_out [m][6144];
 // lisa_gdn_out_rows (grid (m, 48) x 128): gated RMSNorm of y into gated.
 extern "C" __global__ __launch_bounds__(256) void lisa_gdn_prep_rows(LisaGdnParams p) {
@@ -924,13 +925,13 @@ DEV void gdn_row_load(const LisaGdnParams& p, int t, int h, int kh, int v, int l
   in.v = p.conv_out[(size_t)t * LISA_GDN_CONV_DIM + 2 * LISA_GDN_KEY_DIM + h * 128 + v];
 }
 
-extern "C" __global__ __launch_bounds__(512) void lisa_gdn_scan_rows(LisaGdnParams p) {
+extern "C" __global__ __launch_bounds__(256) void lisa_gdn_scan_rows(LisaGdnParams p) {
   const int rows = (int)p.m_rows;
   const int h = blockIdx.x, kh = h / (LISA_GDN_VH / LISA_GDN_KH);
-  const int tid = threadIdx.x, v = tid >> 2, q = tid & 3, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, v = blockIdx.y * 64 + (tid >> 2), q = tid & 3, lane = tid & 63, wave = tid >> 6;
   // each wave stages the row's k and q in its own LDS slot (a wave reads only
   // what it wrote, so no workgroup barrier is needed)
-  __shared__ float4 kqs[8][64];
+  __shared__ float4 kqs[4][64];
   float* srow = p.state + (size_t)h * 128 * 128 + (size_t)v * 128 + 32 * q;
   float S[32];
 #pragma unroll
@@ -1465,39 +1466,52 @@ extern "C" __global__ __launch_bounds__(256) void lisa_rows(LisaRowsParams p) {
 // GDN causal conv + SiLU over m rows (gdn.metal:125-170 prefill form, 212-240
 // history update): thread = channel, rows in order, the arithmetic of the
 // decode conv epilogue.
+// Causal conv over rows, parallel in time: grid (40, ceil(m / 64)) x 256; thread
+// (channel c, row block b) forms rows 64b .. 64b+63 from x[64b-3 .. 64b+63]
+// (rows before 0 come from the carried conv state). Block 0 is the only reader
+// of the old state and, after reading it, the only writer of the new one.
 extern "C" __global__ __launch_bounds__(256) void lisa_gdn_conv_rows(LisaConvRowsParams p) {
   const int C = LISA_GDN_CONV_DIM;
   const int c = blockIdx.x * 256 + threadIdx.x;
   if (c >= C) return;
-  float h0 = bf2f(p.conv_state[c]), h1 = bf2f(p.conv_state[C + c]), h2 = bf2f(p.conv_state[2 * C + c]);
+  const int m = (int)p.m_rows, t0 = blockIdx.y * 64;
+  if (t0 >= m) return;
   float w[4];
 #pragma unroll
   for (int tap = 0; tap < 4; ++tap) w[tap] = bf2f(p.conv_w[(size_t)c * 4 + tap]);
-  // rows in batches of 16: the batch's loads are all in flight before its
-  // (sequential) history update
-  constexpr int RB = 16;
-  for (uint32_t t0 = 0; t0 < p.m_rows; t0 += RB) {
-    float xs[RB];
+  // history h(t) for t in [t0-3, t0+63]: x rows, or the old state before row 0
+  float x[67];
 #pragma unroll
-    for (int j = 0; j < RB; ++j) xs[j] = p.qkv[(size_t)min(t0 + j, p.m_rows - 1) * C + c];
+  for (int j = 0; j < 67; ++j) {
+    const int t = t0 - 3 + j;
+    const int tc = min(max(t, 0), m - 1);
+    const float raw = p.qkv[(size_t)tc * C + c];
+    x[j] = lisa_bf16r(raw);
+  }
+  if (t0 == 0) {
+    float s[3];
 #pragma unroll
-    for (int j = 0; j < RB; ++j) {
-      if (t0 + j >= p.m_rows) break;
-      const float x = lisa_bf16r(xs[j]);
-      float acc = 0.0f;
-      acc = acc + h0 * w[0];
-      acc = acc + h1 * w[1];
-      acc = acc + h2 * w[2];
-      acc = acc + x * w[3];
-      p.conv_out[(size_t)(t0 + j) * C + c] = lisa_bf16r(lisa_silu_exp(lisa_bf16r(acc)));
-      h0 = h1;
-      h1 = h2;
-      h2 = x;
+    for (int i = 0; i < 3; ++i) s[i] = bf2f(p.conv_state[(size_t)i * C + c]);
+#pragma unroll
+    for (int i = 0; i < 3; ++i) x[i] = s[i];
+    // new state: h(m-3), h(m-2), h(m-1) of the sequence [old state, x rows]
+#pragma unroll
+    for (int i = 0; i < 3; ++i) {
+      const int t = m - 3 + i;
+      const float hv = t >= 0 ? lisa_bf16r(p.qkv[(size_t)t * C + c]) : s[3 + t];
+      p.conv_state[(size_t)i * C + c] = lisa_f32_to_bf16(hv);
     }
   }
-  p.conv_state[c] = lisa_f32_to_bf16(h0);
-  p.conv_state[C + c] = lisa_f32_to_bf16(h1);
-  p.conv_state[2 * C + c] = lisa_f32_to_bf16(h2);
+#pragma unroll
+  for (int j = 0; j < 64; ++j) {
+    if (t0 + j >= m) break;
+    float acc = 0.0f;
+    acc = acc + x[j] * w[0];
+    acc = acc + x[j + 1] * w[1];
+    acc = acc + x[j + 2] * w[2];
+    acc = acc + x[j + 3] * w[3];
+    p.conv_out[(size_t)(t0 + j) * C + c] = lisa_bf16r(lisa_silu_exp(lisa_bf16r(acc)));
+  }
 }
 
 // Prefill attention (attention.metal:364-480 semantics) in the decode path's

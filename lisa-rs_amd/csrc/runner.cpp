@@ -1168,7 +1168,8 @@ int prefill_chunk(LisaRunner* r, uint32_t m) {
       cv.conv_state = r->conv_state + (size_t)si * 3 * LISA_GDN_CONV_DIM;
       cv.conv_out = P.conv_out;
       cv.m_rows = m;
-      LISA_TRY(lisa_launch(r->dev, r->conv_rows, &cv, sizeof cv, (LISA_GDN_CONV_DIM + 255) / 256, 1, 1, 256, 1, 1));
+      LISA_TRY(lisa_launch(r->dev, r->conv_rows, &cv, sizeof cv, (LISA_GDN_CONV_DIM + 255) / 256, (m + 63) / 64, 1, 256, 1,
+                              1));
       LisaGdnParams g{};
       g.conv_out = P.conv_out;
       g.z = P.z;
@@ -1186,7 +1187,7 @@ int prefill_chunk(LisaRunner* r, uint32_t m) {
       g.gates = P.gdn_gates;
       g.y_out = P.gdn_y;
       LISA_TRY(lisa_launch(r->dev, r->gdn_prep_rows, &g, sizeof g, m, 9, 1, 256, 1, 1));
-      LISA_TRY(lisa_launch(r->dev, r->gdn_scan_rows, &g, sizeof g, LISA_GDN_VH, 1, 1, 512, 1, 1));
+      LISA_TRY(lisa_launch(r->dev, r->gdn_scan_rows, &g, sizeof g, LISA_GDN_VH, 2, 1, 256, 1, 1));
       LISA_TRY(lisa_launch(r->dev, r->gdn_out_rows, &g, sizeof g, m, LISA_GDN_VH, 1, 128, 1, 1));
       LISA_TRY(launch_gemm(r, P.gated, m, l.out, P.B));
     } else {

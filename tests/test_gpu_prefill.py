@@ -107,6 +107,23 @@ def test_rows_kernels_bit_exact(pkg, orc, dev):
     assert np.array_equal(rb.read(np.uint16, m * H).reshape(m, H), np.stack([orc.embed(ew, es, eb, t) for t in toks]))
 
 
+@pytest.mark.parametrize("m", [1, 2, 3, 64, 65, 150])
+def test_gdn_conv_rows_bit_exact(pkg, orc, dev, m):
+    """Row blocks of 64 in parallel; rows before 0 and the new state come from the
+    carried conv state (m < 3 keeps part of the old state)."""
+    rng = np.random.default_rng(60 + m)
+    CV = 10240
+    qkv = rng.standard_normal((m, CV)).astype(np.float32)
+    conv_w = bf16(rng.uniform(-0.5, 0.5, CV * 4).astype(np.float32))
+    state = bf16(rng.standard_normal(3 * CV).astype(np.float32))
+    qb, cwb, sb, cob = dev.upload(qkv), dev.upload(conv_w), dev.upload(state), dev.buffer(m * CV * 4)
+    dev.dispatch("lisa_gdn_conv_rows", pkg.ConvRowsParams(qb.ptr, cwb.ptr, sb.ptr, cob.ptr, m, 0), (40, (m + 63) // 64),
+                 (256,))
+    want_co, want_state, _ = orc.gdn_conv(qkv, conv_w, state, m)
+    assert np.array_equal(cob.read(np.float32, m * CV).reshape(m, CV).view(np.uint32), want_co.view(np.uint32))
+    assert np.array_equal(sb.read(np.uint16, 3 * CV), want_state)
+
+
 def test_gdn_rows_bit_exact(pkg, orc, dev):
     rng = np.random.default_rng(6)
     m, CV, VH, HD = 40, 10240, 48, 128
@@ -114,7 +131,7 @@ def test_gdn_rows_bit_exact(pkg, orc, dev):
     conv_w = bf16(rng.uniform(-0.5, 0.5, CV * 4).astype(np.float32))
     state = bf16(rng.standard_normal(3 * CV).astype(np.float32))
     qb, cwb, sb, cob = dev.upload(qkv), dev.upload(conv_w), dev.upload(state), dev.buffer(m * CV * 4)
-    dev.dispatch("lisa_gdn_conv_rows", pkg.ConvRowsParams(qb.ptr, cwb.ptr, sb.ptr, cob.ptr, m, 0), (40,), (256,))
+    dev.dispatch("lisa_gdn_conv_rows", pkg.ConvRowsParams(qb.ptr, cwb.ptr, sb.ptr, cob.ptr, m, 0), (40, (m + 63) // 64), (256,))
     want_co, want_state, _ = orc.gdn_conv(qkv, conv_w, state, m)
     co = cob.read(np.float32, m * CV).reshape(m, CV)
     assert np.array_equal(co.view(np.uint32), want_co.view(np.uint32))
@@ -133,7 +150,7 @@ def test_gdn_rows_bit_exact(pkg, orc, dev):
                       state=stb.ptr, gated=gb.ptr, y_out=yb.ptr, q_scale=float(np.float32(inv * inv)),
                       k_scale=float(np.float32(inv)), m_rows=m, qk=qkb.ptr, gates=gtb.ptr)
     dev.dispatch("lisa_gdn_prep_rows", p, (m, 9), (256,))
-    dev.dispatch("lisa_gdn_scan_rows", p, (VH,), (512,))
+    dev.dispatch("lisa_gdn_scan_rows", p, (VH, 2), (256,))
     dev.dispatch("lisa_gdn_out_rows", p, (m, VH), (128,))
     gated, st, y, _ = orc.gdn_recurrence(co, z, a, b, a_log, dt_bias, nw, s0, m)
     assert np.array_equal(gb.read(np.uint16, m * VH * HD).reshape(m, -1), gated)
