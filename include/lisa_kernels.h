@@ -180,6 +180,7 @@ typedef struct LisaSynthParams {
  * k multiple of 64. */
 #define LISA_GEMM_TILE_M 256
 #define LISA_GEMM_TILE_N 128
+#define LISA_GEMM_TILE_N_WIDE 256 /* lisa_q4_gemm_wide: same contract, 256 x 256 tiles */
 
 typedef struct LisaGemmParams {
   const uint16_t* a;

@@ -1196,110 +1196,127 @@ extern "C" __global__ __launch_bounds__(256) void lisa_attn_merge_m3(LisaAttnPar
 // ===========================================================================
 // q4 GEMM (gemm.metal:152-341 semantics): C[m][n] = sum_k A[m][k] * Wd[n][k],
 // Wd = bf16(fma(scale, q, bias)), bf16 MFMA 32x32x16 with f32 accumulation.
-// 256x128 output tile per workgroup (LISA_GEMM_TILE_M x LISA_GEMM_TILE_N), one
-// 64-wide K step per q4 group. Each wave owns a 128x64 quarter as 4x2 MFMA
-// blocks (accumulators in AGPRs). LDS holds two stages of the A rows and the
-// dequantized W rows (rows padded to 72 bf16, so the 8 lanes of each 128-byte
-// LDS pass read distinct banks); global loads run two K steps ahead in two
-// register sets, and the dequant of step s+1 is written while step s's MFMAs
-// run, so each K step needs one barrier.
+// Output tile 256 x BN per workgroup (lisa_q4_gemm: BN = 128, lisa_q4_gemm_wide:
+// BN = 256), one 64-wide K step per q4 group. The four waves split the tile
+// 2 x 2; each owns a 128 x BN/2 block as 4 x BN/64 MFMA blocks (accumulators in
+// AGPRs). LDS holds two stages of the A rows and the dequantized W rows (rows
+// padded to 72 bf16, so the 8 lanes of each 128-byte LDS pass read distinct
+// banks); global loads run two K steps ahead in two register sets, and the
+// A copy and W dequant of step s+1 are interleaved with step s's MFMAs (the
+// MFMAs run in the matrix core while the VALU works), so each K step needs
+// one barrier. The wide tile reads half the LDS bytes per MFMA; the launcher
+// picks per shape (fewer, longer tiles against the last round on 256 CUs).
 typedef __bf16 lisa_bf16x8 __attribute__((ext_vector_type(8)));
 typedef float lisa_f32x16 __attribute__((ext_vector_type(16)));
-
-constexpr int GEMM_BM = LISA_GEMM_TILE_M, GEMM_BN = LISA_GEMM_TILE_N, GEMM_PAD = 72;
-
-constexpr int GEMM_RA = GEMM_BM * 8 / 256;  // A chunks per thread and K step
 // Native 4 x u32 vectors for the staging registers (HIP's uint4 struct copies
 // lower to memcpy, which keeps loop-carried arrays of them out of registers).
 typedef uint32_t lisa_u32x4 __attribute__((ext_vector_type(4)));
 
-// The step's A chunks and dequantized W row half into one LDS stage.
-DEV void gemm_lstore(uint16_t* as, uint16_t* ws, int tid, const lisa_u32x4* a, lisa_u32x4 w, uint32_t sb) {
+constexpr int GEMM_BM = LISA_GEMM_TILE_M, GEMM_PAD = 72;
+constexpr int GEMM_RA = GEMM_BM * 8 / 256;  // A chunks per thread and K step
+
+template <int BN>
+struct GemmCfg {
+  static constexpr int RW = BN / 128;  // W 16 B chunks (32 nibbles) per thread and K step
+  static constexpr int NB = BN / 64;   // 32-wide N blocks per wave
+};
+
+// A chunks 16 B (row u/8, chunk u%8, u = tid + 256 i) and W chunks (row u/2,
+// half u%2, u = RW tid + r) of one K step into one LDS stage, all at once (the
+// first stage only; later stages are written inside gemm_step).
+template <int BN>
+DEV void gemm_lstore(uint16_t* as, uint16_t* ws, int tid, const lisa_u32x4* a, const lisa_u32x4* w, uint32_t sb) {
+  using G = GemmCfg<BN>;
 #pragma unroll
   for (int i = 0; i < GEMM_RA; ++i) {
     const int u = tid + 256 * i;
     *reinterpret_cast<lisa_u32x4*>(&as[(u >> 3) * GEMM_PAD + (u & 7) * 8]) = a[i];
   }
   const float sc = lo_bf(sb), bi = hi_bf(sb);
-  const uint32_t wd[4] = {w.x, w.y, w.z, w.w};
-  uint16_t* dst = &ws[(tid >> 1) * GEMM_PAD + (tid & 1) * 32];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    float v[8];
+  for (int r = 0; r < G::RW; ++r) {
+    const int u = G::RW * tid + r;
+    uint16_t* dst = &ws[(u >> 1) * GEMM_PAD + (u & 1) * 32];
+    const uint32_t wd[4] = {w[r].x, w[r].y, w[r].z, w[r].w};
 #pragma unroll
-    for (int e = 0; e < 8; ++e) v[e] = lisa_fma(sc, (float)((wd[j] >> (4 * e)) & 0xfu), bi);
-    *reinterpret_cast<uint4*>(dst + 8 * j) =
-        make_uint4(lisa_f32x2_to_bf16x2(v[0], v[1]), lisa_f32x2_to_bf16x2(v[2], v[3]),
-                   lisa_f32x2_to_bf16x2(v[4], v[5]), lisa_f32x2_to_bf16x2(v[6], v[7]));
+    for (int j = 0; j < 4; ++j) {
+      float v[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[e] = lisa_fma(sc, (float)((wd[j] >> (4 * e)) & 0xfu), bi);
+      *reinterpret_cast<uint4*>(dst + 8 * j) =
+          make_uint4(lisa_f32x2_to_bf16x2(v[0], v[1]), lisa_f32x2_to_bf16x2(v[2], v[3]),
+                     lisa_f32x2_to_bf16x2(v[4], v[5]), lisa_f32x2_to_bf16x2(v[6], v[7]));
+    }
   }
 }
 
-// One K step of MFMAs of a wave's 128x64 quarter from one LDS stage; the
-// fragments of sub-step ks+1 are read while the MFMAs of ks issue.
+template <int BN>
 DEV void gemm_frags(const uint16_t* as, const uint16_t* ws, int wm, int wn, int lane, int ks, lisa_bf16x8 (&af)[4],
-                    lisa_bf16x8 (&bf)[2]) {
+                    lisa_bf16x8 (&bf)[GemmCfg<BN>::NB]) {
 #pragma unroll
   for (int i = 0; i < 4; ++i)
     af[i] = *reinterpret_cast<const lisa_bf16x8*>(
         &as[(wm * 128 + i * 32 + (lane & 31)) * GEMM_PAD + ks * 16 + 8 * (lane >> 5)]);
 #pragma unroll
-  for (int j = 0; j < 2; ++j)
+  for (int j = 0; j < GemmCfg<BN>::NB; ++j)
     bf[j] = *reinterpret_cast<const lisa_bf16x8*>(
-        &ws[(wn * 64 + j * 32 + (lane & 31)) * GEMM_PAD + ks * 16 + 8 * (lane >> 5)]);
+        &ws[(wn * (BN / 2) + j * 32 + (lane & 31)) * GEMM_PAD + ks * 16 + 8 * (lane >> 5)]);
 }
 
-// One K step: the MFMAs of a wave's 128x64 quarter from stage (as_r, ws_r),
-// with the next step's stage (as_w, ws_w) written alongside: each sub-step ks
-// reads the fragments of ks+1, issues its 8 MFMAs interleaved with the dequant
-// of W word ks (the MFMAs run in the matrix core while the VALU works), then
-// stores A chunks 2ks, 2ks+1 and the dequantized word.
+// One K step: the MFMAs of the wave's block from stage (as_r, ws_r), with the
+// next step's stage (as_w, ws_w) written alongside. Sub-step ks reads the
+// fragments of ks+1, then issues its MFMAs interleaved with the dequant of W
+// word ks of each of the thread's chunks, and stores A chunks 2ks, 2ks+1.
+template <int BN>
 DEV void gemm_step(const uint16_t* as_r, const uint16_t* ws_r, uint16_t* as_w, uint16_t* ws_w, int tid, int wm, int wn,
-                   int lane, const lisa_u32x4* a, lisa_u32x4 w, uint32_t sb, lisa_f32x16 (&acc)[4][2]) {
-  lisa_bf16x8 af[2][4], bf[2][2];
-  gemm_frags(as_r, ws_r, wm, wn, lane, 0, af[0], bf[0]);
+                   int lane, const lisa_u32x4* a, const lisa_u32x4* w, uint32_t sb,
+                   lisa_f32x16 (&acc)[4][GemmCfg<BN>::NB]) {
+  using G = GemmCfg<BN>;
+  lisa_bf16x8 af[2][4], bf[2][G::NB];
+  gemm_frags<BN>(as_r, ws_r, wm, wn, lane, 0, af[0], bf[0]);
   const float sc = lo_bf(sb), bi = hi_bf(sb);
-  const uint32_t wd[4] = {w.x, w.y, w.z, w.w};
-  uint16_t* dst = &ws_w[(tid >> 1) * GEMM_PAD + (tid & 1) * 32];
 #pragma unroll
   for (int ks = 0; ks < 4; ++ks) {
     const int c = ks & 1;
-    if (ks + 1 < 4) gemm_frags(as_r, ws_r, wm, wn, lane, ks + 1, af[c ^ 1], bf[c ^ 1]);
+    if (ks + 1 < 4) gemm_frags<BN>(as_r, ws_r, wm, wn, lane, ks + 1, af[c ^ 1], bf[c ^ 1]);
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
-      for (int j = 0; j < 2; ++j)
+      for (int j = 0; j < G::NB; ++j)
         acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[c][i], bf[c][j], acc[i][j], 0, 0, 0);
-    float v[8];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) v[e] = lisa_fma(sc, (float)((wd[ks] >> (4 * e)) & 0xfu), bi);
-    const uint4 packed = make_uint4(lisa_f32x2_to_bf16x2(v[0], v[1]), lisa_f32x2_to_bf16x2(v[2], v[3]),
-                                    lisa_f32x2_to_bf16x2(v[4], v[5]), lisa_f32x2_to_bf16x2(v[6], v[7]));
+    for (int r = 0; r < G::RW; ++r) {
+      const uint32_t word = ks == 0 ? w[r].x : ks == 1 ? w[r].y : ks == 2 ? w[r].z : w[r].w;
+      float v[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[e] = lisa_fma(sc, (float)((word >> (4 * e)) & 0xfu), bi);
+      const int u = G::RW * tid + r;
+      *reinterpret_cast<uint4*>(&ws_w[(u >> 1) * GEMM_PAD + (u & 1) * 32 + 8 * ks]) =
+          make_uint4(lisa_f32x2_to_bf16x2(v[0], v[1]), lisa_f32x2_to_bf16x2(v[2], v[3]),
+                     lisa_f32x2_to_bf16x2(v[4], v[5]), lisa_f32x2_to_bf16x2(v[6], v[7]));
+    }
 #pragma unroll
     for (int i = 2 * ks; i < 2 * ks + 2; ++i) {
       const int u = tid + 256 * i;
       *reinterpret_cast<lisa_u32x4*>(&as_w[(u >> 3) * GEMM_PAD + (u & 7) * 8]) = a[i];
     }
-    *reinterpret_cast<uint4*>(dst + 8 * ks) = packed;
     // issue order within the sub-step: fragment reads, then MFMA/VALU pairs
-    if (ks + 1 < 4) __builtin_amdgcn_sched_group_barrier(0x100, 6, 0);
+    if (ks + 1 < 4) __builtin_amdgcn_sched_group_barrier(0x100, 4 + G::NB, 0);
 #pragma unroll
-    for (int q = 0; q < 8; ++q) {
+    for (int q = 0; q < 4 * G::NB; ++q) {
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);
+      __builtin_amdgcn_sched_group_barrier(0x002, 32 * G::RW / (4 * G::NB) + 1, 0);
     }
-    __builtin_amdgcn_sched_group_barrier(0x200, 3, 0);
+    __builtin_amdgcn_sched_group_barrier(0x200, 2 + G::RW, 0);
   }
 }
 
-// One workgroup per CU (the LDS stages take 108 KB), so the whole register file
-// is available to its four waves.
-extern "C" __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void lisa_q4_gemm(
-    LisaGemmParams p) {
-  __shared__ __attribute__((aligned(16))) uint16_t As[2][GEMM_BM * GEMM_PAD];
-  __shared__ __attribute__((aligned(16))) uint16_t Ws[2][GEMM_BN * GEMM_PAD];
+template <int BN>
+DEV void q4_gemm_body(const LisaGemmParams& p, uint16_t (*As)[GEMM_BM * GEMM_PAD], uint16_t (*Ws)[BN * GEMM_PAD]) {
+  using G = GemmCfg<BN>;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave >> 1, wn = wave & 1;
-  const uint32_t m0 = blockIdx.y * GEMM_BM, n0 = blockIdx.x * GEMM_BN;
+  const uint32_t m0 = blockIdx.y * GEMM_BM, n0 = blockIdx.x * BN;
   const uint32_t K = p.k, nk = K / 64;
 
   const lisa_u32x4* asrc[GEMM_RA];
@@ -1309,45 +1326,45 @@ extern "C" __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(
     const uint32_t row = min(m0 + (uint32_t)(u >> 3), p.m - 1);
     asrc[i] = reinterpret_cast<const lisa_u32x4*>(p.a + (size_t)row * K) + (u & 7);
   }
-  const uint32_t wrow = min(n0 + (uint32_t)(tid >> 1), p.n - 1);
-  const lisa_u32x4* wsrc = reinterpret_cast<const lisa_u32x4*>(p.w + (size_t)wrow * (K / 8)) + (tid & 1);
+  // every W chunk of a thread lies in one row: (RW tid + r) / 2 = RW tid / 2
+  const uint32_t wrow = min(n0 + (uint32_t)((G::RW * tid) >> 1), p.n - 1);
+  const lisa_u32x4* wsrc = reinterpret_cast<const lisa_u32x4*>(p.w + (size_t)wrow * (K / 8)) + ((G::RW * tid) & 1);
   const uint32_t* sbsrc = p.sb + (size_t)wrow * (K / 64);
 
-  lisa_f32x16 acc[4][2];
+  lisa_f32x16 acc[4][G::NB];
 #pragma unroll
   for (int i = 0; i < 4; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
+    for (int j = 0; j < G::NB; ++j)
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
-  // Global loads of one K step into register set (A, W, SB): A 16 B chunks (row
-  // u/8, chunk u%8, u = tid + 256 i), 32 nibbles of W row tid/2 (half tid%2)
-  // and that row's scale/bias word. Steps past the end re-read the last one,
-  // so the loads stay unconditional. Two sets: even steps and odd steps.
-#define GEMM_GLOAD(A, W, SB, STEP)                                     \
-  {                                                                    \
-    const uint32_t st_ = min((uint32_t)(STEP), nk - 1);                \
-    _Pragma("unroll") for (int i = 0; i < GEMM_RA; ++i) A[i] = asrc[i][st_ * 8]; \
-    W = wsrc[st_ * 2];                                                 \
-    SB = sbsrc[st_];                                                   \
+  // Global loads of one K step into register set (A, W, SB). Steps past the
+  // end re-read the last one, so the loads stay unconditional. Two sets: even
+  // steps and odd steps.
+#define GEMM_GLOAD(A, W, SB, STEP)                                                        \
+  {                                                                                       \
+    const uint32_t st_ = min((uint32_t)(STEP), nk - 1);                                   \
+    _Pragma("unroll") for (int i = 0; i < GEMM_RA; ++i) A[i] = asrc[i][st_ * 8];          \
+    _Pragma("unroll") for (int r = 0; r < G::RW; ++r) W[r] = wsrc[st_ * 2 + r];           \
+    SB = sbsrc[st_];                                                                      \
   }
-  lisa_u32x4 a0[GEMM_RA], a1[GEMM_RA], w0, w1;
+  lisa_u32x4 a0[GEMM_RA], a1[GEMM_RA], w0[G::RW], w1[G::RW];
   uint32_t sb0, sb1;
   GEMM_GLOAD(a0, w0, sb0, 0);
   GEMM_GLOAD(a1, w1, sb1, 1);
-  gemm_lstore(As[0], Ws[0], tid, a0, w0, sb0);
+  gemm_lstore<BN>(As[0], Ws[0], tid, a0, w0, sb0);
   __syncthreads();
   // nk is even (k is a multiple of 128): steps go in pairs, one exit
   for (uint32_t step = 0; step < nk; step += 2) {
     // even step: MFMAs on stage 0 while step+1 goes to stage 1 and step+2 loads
     GEMM_GLOAD(a0, w0, sb0, step + 2);
-    gemm_step(As[0], Ws[0], As[1], Ws[1], tid, wm, wn, lane, a1, w1, sb1, acc);
+    gemm_step<BN>(As[0], Ws[0], As[1], Ws[1], tid, wm, wn, lane, a1, w1, sb1, acc);
     __syncthreads();
     // odd step: MFMAs on stage 1 while step+2 goes to stage 0 and step+3 loads
     // (past the last step the stores write data nobody reads)
     GEMM_GLOAD(a1, w1, sb1, step + 3);
-    gemm_step(As[1], Ws[1], As[0], Ws[0], tid, wm, wn, lane, a0, w0, sb0, acc);
+    gemm_step<BN>(As[1], Ws[1], As[0], Ws[0], tid, wm, wn, lane, a0, w0, sb0, acc);
     __syncthreads();
   }
 #undef GEMM_GLOAD
@@ -1355,14 +1372,29 @@ extern "C" __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(
 #pragma unroll
   for (int i = 0; i < 4; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const uint32_t col = n0 + wn * 64 + j * 32 + (lane & 31);
+    for (int j = 0; j < G::NB; ++j) {
+      const uint32_t col = n0 + wn * (BN / 2) + j * 32 + (lane & 31);
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const uint32_t row = m0 + wm * 128 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
         if (row < p.m && col < p.n) p.c[(size_t)row * p.ldc + col] = acc[i][j][r];
       }
     }
+}
+
+// One workgroup per CU (the LDS stages take 108 or 144 KB), so the whole
+// register file is available to its four waves.
+extern "C" __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void lisa_q4_gemm(
+    LisaGemmParams p) {
+  __shared__ __attribute__((aligned(16))) uint16_t As[2][GEMM_BM * GEMM_PAD];
+  __shared__ __attribute__((aligned(16))) uint16_t Ws[2][LISA_GEMM_TILE_N * GEMM_PAD];
+  q4_gemm_body<LISA_GEMM_TILE_N>(p, As, Ws);
+}
+extern "C" __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void lisa_q4_gemm_wide(
+    LisaGemmParams p) {
+  __shared__ __attribute__((aligned(16))) uint16_t As[2][GEMM_BM * GEMM_PAD];
+  __shared__ __attribute__((aligned(16))) uint16_t Ws[2][LISA_GEMM_TILE_N_WIDE * GEMM_PAD];
+  q4_gemm_body<LISA_GEMM_TILE_N_WIDE>(p, As, Ws);
 }
 
 // Per-row kernels. NORM/RESNORM follow the q4 prologue's arithmetic exactly

@@ -100,7 +100,7 @@ struct LisaRunner {
   LisaFunction *qmv_epi[2][7][5] = {};  // K = 5120 with a fixed epilogue: [m3][prologue][epilogue]
   LisaFunction *gdn[2] = {}, *attn_part[2] = {}, *attn_merge[2] = {}, *finalize = nullptr, *synth = nullptr;
   // batched prefill
-  LisaFunction *gemm = nullptr, *rows = nullptr, *conv_rows = nullptr, *gdn_prep_rows = nullptr, *gdn_scan_rows = nullptr,
+  LisaFunction *gemm = nullptr, *gemm_wide = nullptr, *rows = nullptr, *conv_rows = nullptr, *gdn_prep_rows = nullptr, *gdn_scan_rows = nullptr,
                *gdn_out_rows = nullptr, *attn_store_rows = nullptr,
                *attn_partial_rows = nullptr, *attn_merge_rows = nullptr;
   // memory
@@ -695,6 +695,7 @@ extern "C" int lisa_runner_create(const LisaRunnerConfig* cfg, LisaRunner** out)
   LISA_TRY(lisa_function_get(r->mod, "lisa_step_finalize", &r->finalize));
   LISA_TRY(lisa_function_get(r->mod, "lisa_synth_fill", &r->synth));
   LISA_TRY(lisa_function_get(r->mod, "lisa_q4_gemm", &r->gemm));
+  LISA_TRY(lisa_function_get(r->mod, "lisa_q4_gemm_wide", &r->gemm_wide));
   LISA_TRY(lisa_function_get(r->mod, "lisa_rows", &r->rows));
   LISA_TRY(lisa_function_get(r->mod, "lisa_gdn_conv_rows", &r->conv_rows));
   LISA_TRY(lisa_function_get(r->mod, "lisa_gdn_prep_rows", &r->gdn_prep_rows));
@@ -745,7 +746,7 @@ extern "C" void lisa_runner_free(LisaRunner* r) {
     for (auto& b : a)
       for (LisaFunction* f : b) delete f;
   for (LisaFunction* f : {r->gdn[0], r->gdn[1], r->attn_part[0], r->attn_part[1], r->attn_merge[0], r->attn_merge[1],
-                          r->finalize, r->synth, r->gemm, r->rows, r->conv_rows, r->gdn_prep_rows, r->gdn_scan_rows, r->gdn_out_rows, r->attn_store_rows,
+                          r->finalize, r->synth, r->gemm, r->gemm_wide, r->rows, r->conv_rows, r->gdn_prep_rows, r->gdn_scan_rows, r->gdn_out_rows, r->attn_store_rows,
                           r->attn_partial_rows, r->attn_merge_rows})
     delete f;
   lisa_buffer_free(r->pf.buf);
@@ -1120,8 +1121,16 @@ int launch_gemm(LisaRunner* r, const uint16_t* a, uint32_t m, const Q4Dev& w, fl
   g.n = w.n;
   g.k = w.k;
   g.ldc = w.n;
-  return lisa_launch(r->dev, r->gemm, &g, sizeof g, (w.n + LISA_GEMM_TILE_N - 1) / LISA_GEMM_TILE_N,
-                     (m + LISA_GEMM_TILE_M - 1) / LISA_GEMM_TILE_M, 1, 256, 1, 1);
+  // One workgroup per CU: a launch runs in rounds of `cus` tiles. A 256-wide
+  // tile takes about 1.6x a 128-wide one (it reads half the LDS bytes per
+  // MFMA); take it unless its rounds cost more.
+  const uint32_t gm = (m + LISA_GEMM_TILE_M - 1) / LISA_GEMM_TILE_M;
+  const uint32_t gn = (w.n + LISA_GEMM_TILE_N - 1) / LISA_GEMM_TILE_N;
+  const uint32_t gw = (w.n + LISA_GEMM_TILE_N_WIDE - 1) / LISA_GEMM_TILE_N_WIDE;
+  const uint32_t cus = r->dev->cu_count > 0 ? (uint32_t)r->dev->cu_count : 256;
+  const uint32_t rn = (gn * gm + cus - 1) / cus, rw = (gw * gm + cus - 1) / cus;
+  if (rw * 16 <= rn * 10) return lisa_launch(r->dev, r->gemm_wide, &g, sizeof g, gw, gm, 1, 256, 1, 1);
+  return lisa_launch(r->dev, r->gemm, &g, sizeof g, gn, gm, 1, 256, 1, 1);
 }
 
 int launch_rows(LisaRunner* r, LisaRowsParams& p, uint32_t gx, uint32_t m) {

@@ -30,35 +30,41 @@ def dev(pkg):
     return pkg.Device(0)
 
 
-def gemm(pkg, dev, a_bf16, q, m):
+GEMM_KERNELS = ["lisa_q4_gemm", "lisa_q4_gemm_wide"]
+
+
+def gemm(pkg, dev, a_bf16, q, m, kernel="lisa_q4_gemm"):
     out = dev.buffer(m * q.n * 4)
     ab = dev.upload(a_bf16)
     p = pkg.GemmParams(ab.ptr, q.wbuf.ptr, q.sbbuf.ptr, out.ptr, m, q.n, q.k, q.n)
-    tm, tn = pkg.GEMM_TILE_M, pkg.GEMM_TILE_N
-    dev.dispatch("lisa_q4_gemm", p, ((q.n + tn - 1) // tn, (m + tm - 1) // tm), (256,))
+    tm = pkg.GEMM_TILE_M
+    tn = pkg.GEMM_TILE_N_WIDE if kernel.endswith("_wide") else pkg.GEMM_TILE_N
+    dev.dispatch(kernel, p, ((q.n + tn - 1) // tn, (m + tm - 1) // tm), (256,))
     return out.read(np.float32, m * q.n).reshape(m, q.n)
 
 
+@pytest.mark.parametrize("kernel", GEMM_KERNELS)
 @pytest.mark.parametrize("M,N,K", [(37, 200, 1024), (128, 512, 5120), (300, 48, 5120), (5, 256, 17408),
-                                   (512, 384, 6144)])
-def test_gemm_matches_oracle(pkg, orc, dev, M, N, K):
+                                   (512, 384, 6144), (260, 300, 1024)])
+def test_gemm_matches_oracle(pkg, orc, dev, M, N, K, kernel):
     rng = np.random.default_rng(M * 7 + N + K)
     w, s, b = rand_q4(rng, N, K)
     a = bf16(rng.standard_normal((M, K)).astype(np.float32))
-    got = gemm(pkg, dev, a, DevQ4(dev, w, s, b), M)
+    got = gemm(pkg, dev, a, DevQ4(dev, w, s, b), M, kernel)
     want = orc.q4_gemm(a, w, s, b, N, K, M)
     rms = np.sqrt(np.mean(want.astype(np.float64) ** 2))
     assert np.max(np.abs(got - want)) <= 1e-5 * np.sqrt(K / 64) * rms
 
 
-def test_gemm_exact_integer_case(pkg, orc, dev):
+@pytest.mark.parametrize("kernel", GEMM_KERNELS)
+def test_gemm_exact_integer_case(pkg, orc, dev, kernel):
     rng = np.random.default_rng(3)
     M, N, K = 70, 130, 2048
     w = rng.integers(0, 2**32, size=(N, K // 8), dtype=np.uint64).astype(np.uint32)
     a = bf16(rng.integers(-4, 5, size=(M, K)).astype(np.float32))
     s = bf16(rng.choice(np.array([0.5, 1.0, 2.0], np.float32), size=(N, K // 64)))
     b = bf16(rng.choice(np.array([-8.0, -4.0, 0.0, 1.0], np.float32), size=(N, K // 64)))
-    got = gemm(pkg, dev, a, DevQ4(dev, w, s, b), M)
+    got = gemm(pkg, dev, a, DevQ4(dev, w, s, b), M, kernel)
     assert np.array_equal(got, orc.q4_gemm(a, w, s, b, N, K, M))
 
 
