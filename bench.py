@@ -115,6 +115,53 @@ def calibrate_copy(mb):
           flush=True)
 
 
+GEMM_SHAPES = [(2048, INTER, HIDDEN, "mlp gate (and up)"), (2048, HIDDEN, INTER, "mlp down"),
+               (2048, 12288, HIDDEN, "attention q")]
+BF16_PEAK_TFLOPS = 2500.0
+
+
+def gemm_phase(pkg, reps=10):
+    """The prefill q4 GEMM alone on config 3's 2048-row shapes, both tile
+    variants, timed with HIP events over `reps` back-to-back dispatches;
+    random MLX-affine weights and bf16 activations uploaded from the host."""
+    dev = pkg.Device(0)
+    L = pkg.lib()
+    rng = np.random.default_rng(0x6E33)
+    ev0, ev1 = pkg.C.c_void_p(), pkg.C.c_void_p()
+    pkg._check(L.lisa_event_create(pkg.C.byref(ev0)))
+    pkg._check(L.lisa_event_create(pkg.C.byref(ev1)))
+    out = []
+    for (m, n, k, what) in GEMM_SHAPES:
+        w = rng.integers(0, 2**32, size=(n, k // 8), dtype=np.uint64).astype(np.uint32)
+        sc = rng.uniform(0.005, 0.02, size=(n, k // 64)).astype(np.float32).view(np.uint32) >> 16
+        bi = rng.uniform(-0.1, 0.1, size=(n, k // 64)).astype(np.float32).view(np.uint32) >> 16
+        wb, sbb = dev.upload(w), dev.upload((sc | (bi << 16)).astype(np.uint32))
+        a = rng.standard_normal((m, k)).astype(np.float32).view(np.uint32) >> 16
+        ab, cb = dev.upload(a.astype(np.uint16)), dev.buffer(m * n * 4)
+        p = pkg.GemmParams(ab.ptr, wb.ptr, sbb.ptr, cb.ptr, m, n, k, n)
+        best = None
+        for kern, tn in (("lisa_q4_gemm", pkg.GEMM_TILE_N), ("lisa_q4_gemm_wide", pkg.GEMM_TILE_N_WIDE)):
+            grid = ((n + tn - 1) // tn, (m + pkg.GEMM_TILE_M - 1) // pkg.GEMM_TILE_M)
+            dev.dispatch(kern, p, grid, (256,))
+            pkg._check(L.lisa_event_record(ev0, dev.h))
+            for _ in range(reps):
+                dev.dispatch(kern, p, grid, (256,), wait=False)
+            pkg._check(L.lisa_event_record(ev1, dev.h))
+            dev.synchronize()
+            ms = pkg.C.c_float()
+            pkg._check(L.lisa_event_elapsed_ms(ev0, ev1, pkg.C.byref(ms)))
+            us = 1e3 * ms.value / reps
+            tflops = 2.0 * m * n * k / (us * 1e-6) / 1e12
+            row = {"m": m, "n": n, "k": k, "what": what, "kernel": kern, "us": round(us, 1),
+                   "tflops": round(tflops, 1), "mfma_frac": round(tflops / BF16_PEAK_TFLOPS, 4)}
+            out.append(row)
+            print(f"[bench] gemm {what} {m}x{n}x{k} {kern}: {us:.1f} us, {tflops:.1f} TFLOP/s", file=sys.stderr,
+                  flush=True)
+        del wb, sbb, ab, cb
+    return {"shapes": out, "peak_tflops": BF16_PEAK_TFLOPS, "dtype": "bf16 MFMA, f32 accumulate",
+            "note": "dequantized q4 weights; peak = dense bf16 MFMA of MI355X"}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -126,6 +173,8 @@ def main():
     ap.add_argument("--profile-steps", type=int, default=4)
     ap.add_argument("--prefill-tokens", type=int, default=2048,
                     help="config 3 prompt length for the prefill phase (0 skips it)")
+    ap.add_argument("--gemm-only", action="store_true", help="only time the prefill q4 GEMM kernels")
+    ap.add_argument("--no-gemm", action="store_true", help="skip the prefill q4 GEMM phase")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="only run the plain copy kernel over MIB MiB (counter calibration)")
     args = ap.parse_args()
@@ -140,6 +189,9 @@ def main():
         return
 
     pkg = load("lisa_rs_amd", ROOT / "lisa-rs_amd" / "__init__.py", ROOT / "lisa-rs_amd")
+    if args.gemm_only:
+        print(json.dumps({"prefill_gemm": gemm_phase(pkg)}), flush=True)
+        return
     K, W = args.steps, args.warmup
     capacity = max(CTX + max(K, args.profile_steps, args.cpu_steps) + W + 16, args.prefill_tokens + 16)
     t0 = time.time()
@@ -238,6 +290,8 @@ def main():
     if prefill:
         result["target_prefill_tok_s"] = prefill["tok_s"]
         result["prefill"] = prefill
+    if not args.no_gemm:
+        result["prefill_gemm"] = gemm_phase(pkg)
 
     if not args.no_cpu and args.cpu_steps > 0:
         orc = load("lisa_oracle", ROOT / "oracle" / "oracle.py")
