@@ -790,23 +790,34 @@ DEV void gdn_gates(float braw, float araw, uint16_t dt_bias, uint16_t a_log, flo
   decay = lisa_expf(-lisa_expf(bf2f(a_log)) * dt);
 }
 
+// Quarter dot of 32: (r0 + r1) + (r2 + r3) over four ascending fma runs of 8
+// (independent chains, so the dependent latency is 8 fmas, not 32).
+DEV float gdn_dot32(const float (&S)[32], const float* vec) {
+  float r[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    float p = S[8 * j] * vec[8 * j];
+#pragma unroll
+    for (int k = 8 * j + 1; k < 8 * j + 8; ++k) p = lisa_fma(S[k], vec[k], p);
+    r[j] = p;
+  }
+  return (r[0] + r[1]) + (r[2] + r[3]);
+}
+
 // One time step of state row v, quarter q (S = the row's 32 elements 32q..32q+31;
 // kq, qq = the matching 32 elements of k and q): decay, delta rule, readout.
-// Returns the row's readout (the four quarters combined by xor 1, 2).
+// Returns the row's readout (the four quarters combined by xor 1, 2, which is
+// (q0 + q1) + (q2 + q3) on every lane).
 DEV float gdn_row_step(float (&S)[32], const float* kq, const float* qq, float vval, float beta, float decay) {
 #pragma unroll
   for (int k = 0; k < 32; ++k) S[k] = S[k] * decay;
-  float pk = S[0] * kq[0];
-#pragma unroll
-  for (int k = 1; k < 32; ++k) pk = lisa_fma(S[k], kq[k], pk);
+  float pk = gdn_dot32(S, kq);
   pk = pk + xor_lane<1>(pk);
   pk = pk + xor_lane<2>(pk);
   const float delta = (vval - pk) * beta;
 #pragma unroll
   for (int k = 0; k < 32; ++k) S[k] = lisa_fma(delta, kq[k], S[k]);
-  float py = S[0] * qq[0];
-#pragma unroll
-  for (int k = 1; k < 32; ++k) py = lisa_fma(S[k], qq[k], py);
+  float py = gdn_dot32(S, qq);
   py = py + xor_lane<1>(py);
   py = py + xor_lane<2>(py);
   return py;
@@ -886,8 +897,8 @@ DEV void gdn_body(const LisaGdnParams& p) {
 //   key head into qk [m][2][2048], beta and decay into gates [m][48][2];
 // lisa_gdn_scan_rows (grid (48, 2) x 256, 64 state rows per workgroup): the
 //   sequential delta-rule scan, with no barrier in the time loop (each state
-//   row only needs the precomputed inputs), one wave per SIMD, the next row's
-//   inputs loaded while the current one is reduced;
+//   row only needs the precomputed inputs), one wave per SIMD, each row's
+//   inputs loaded eight rows ahead;
 //   readout y (bf16 values) into y_out [m][6144];
 // lisa_gdn_out_rows (grid (m, 48) x 128): gated RMSNorm of y into gated.
 extern "C" __global__ __launch_bounds__(256) void lisa_gdn_prep_rows(LisaGdnParams p) {
@@ -912,16 +923,20 @@ extern "C" __global__ __launch_bounds__(256) void lisa_gdn_prep_rows(LisaGdnPara
 // Per-row inputs of the scan as one lane sees them: its 16 B of the row's k
 // (lanes 0-31) or q (lanes 32-63) of the key head, the head's (beta, decay) and
 // the state row's v value.
+// (native vector types: HIP's float4 struct copies lower to memcpy, which keeps
+// an array of these out of registers)
+typedef float lisa_f32x4 __attribute__((ext_vector_type(4)));
+typedef float lisa_f32x2 __attribute__((ext_vector_type(2)));
 struct GdnRowIn {
-  float4 kq;
-  float2 g;
+  lisa_f32x4 kq;
+  lisa_f32x2 g;
   float v;
 };
 
 DEV void gdn_row_load(const LisaGdnParams& p, int t, int h, int kh, int v, int lane, GdnRowIn& in) {
   const int which = lane < 32 ? 1 : 0;  // k, then q
-  in.kq = reinterpret_cast<const float4*>(p.qk + ((size_t)t * 2 + which) * LISA_GDN_KEY_DIM + kh * 128)[lane & 31];
-  in.g = reinterpret_cast<const float2*>(p.gates)[(size_t)t * LISA_GDN_VH + h];
+  in.kq = reinterpret_cast<const lisa_f32x4*>(p.qk + ((size_t)t * 2 + which) * LISA_GDN_KEY_DIM + kh * 128)[lane & 31];
+  in.g = reinterpret_cast<const lisa_f32x2*>(p.gates)[(size_t)t * LISA_GDN_VH + h];
   in.v = p.conv_out[(size_t)t * LISA_GDN_CONV_DIM + 2 * LISA_GDN_KEY_DIM + h * 128 + v];
 }
 
@@ -931,7 +946,7 @@ extern "C" __global__ __launch_bounds__(256) void lisa_gdn_scan_rows(LisaGdnPara
   const int tid = threadIdx.x, v = blockIdx.y * 64 + (tid >> 2), q = tid & 3, lane = tid & 63, wave = tid >> 6;
   // each wave stages the row's k and q in its own LDS slot (a wave reads only
   // what it wrote, so no workgroup barrier is needed)
-  __shared__ float4 kqs[4][64];
+  __shared__ lisa_f32x4 kqs[4][64];
   float* srow = p.state + (size_t)h * 128 * 128 + (size_t)v * 128 + 32 * q;
   float S[32];
 #pragma unroll
@@ -944,23 +959,30 @@ extern "C" __global__ __launch_bounds__(256) void lisa_gdn_scan_rows(LisaGdnPara
     float kv[32], qv[32];
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      const float4 k4 = kqs[wave][8 * q + i], q4 = kqs[wave][32 + 8 * q + i];
+      const lisa_f32x4 k4 = kqs[wave][8 * q + i], q4 = kqs[wave][32 + 8 * q + i];
       kv[4 * i] = k4.x; kv[4 * i + 1] = k4.y; kv[4 * i + 2] = k4.z; kv[4 * i + 3] = k4.w;
       qv[4 * i] = q4.x; qv[4 * i + 1] = q4.y; qv[4 * i + 2] = q4.z; qv[4 * i + 3] = q4.w;
     }
     const float py = gdn_row_step(S, kv, qv, in.v, in.g.x, in.g.y);
     if (q == 0) p.y_out[(size_t)t * LISA_GDN_VALUE_DIM + h * 128 + v] = lisa_bf16r(py);
   };
-  // two input sets in turn: the next row's loads are in flight during a step
-  GdnRowIn ia, ib;
-  gdn_row_load(p, 0, h, kh, v, lane, ia);
-  for (int t = 0; t < rows; t += 2) {
-    gdn_row_load(p, min(t + 1, rows - 1), h, kh, v, lane, ib);
-    step(ia, t);
-    if (t + 1 >= rows) break;
-    gdn_row_load(p, min(t + 2, rows - 1), h, kh, v, lane, ia);
-    step(ib, t + 1);
+  // a ring of eight input sets: row t's inputs are loaded eight rows ahead, so
+  // the scan never waits on a memory round trip
+  constexpr int D = 8;
+  GdnRowIn in[D];
+#pragma unroll
+  for (int j = 0; j < D; ++j) gdn_row_load(p, min(j, rows - 1), h, kh, v, lane, in[j]);
+  const int full = rows / D * D;
+  for (int t0 = 0; t0 < full; t0 += D) {
+#pragma unroll
+    for (int j = 0; j < D; ++j) {
+      step(in[j], t0 + j);
+      gdn_row_load(p, min(t0 + j + D, rows - 1), h, kh, v, lane, in[j]);
+    }
   }
+#pragma unroll
+  for (int j = 0; j < D - 1; ++j)
+    if (full + j < rows) step(in[j], full + j);
 #pragma unroll
   for (int i = 0; i < 8; ++i)
     reinterpret_cast<float4*>(srow)[i] = make_float4(S[4 * i], S[4 * i + 1], S[4 * i + 2], S[4 * i + 3]);

@@ -464,22 +464,27 @@ void orc_gdn_recurrence(const float* conv_out, const float* z, const float* a, c
       for (int v = 0; v < HD; ++v) {
         float* row = S + (size_t)v * HD;
         for (int k = 0; k < HD; ++k) row[k] = row[k] * decay;
-        float pk[4], pq[4];
-        for (int q = 0; q < 4; ++q) {
-          float p = row[32 * q] * kn[32 * q];
-          for (int k = 32 * q + 1; k < 32 * q + 32; ++k) p = lisa_fma(row[k], kn[k], p);
-          pk[q] = p;
-        }
-        const float kv = (pk[0] + pk[1]) + (pk[2] + pk[3]);
+        // row . vector over 128: quarters of 32, each the sum (r0 + r1) + (r2 + r3)
+        // of four ascending fma runs of 8; quarters combined (q0 + q1) + (q2 + q3)
+        auto dot128 = [&](const float* vec) {
+          float pqr[4];
+          for (int q = 0; q < 4; ++q) {
+            float r[4];
+            for (int j = 0; j < 4; ++j) {
+              const int k0 = 32 * q + 8 * j;
+              float p = row[k0] * vec[k0];
+              for (int k = k0 + 1; k < k0 + 8; ++k) p = lisa_fma(row[k], vec[k], p);
+              r[j] = p;
+            }
+            pqr[q] = (r[0] + r[1]) + (r[2] + r[3]);
+          }
+          return (pqr[0] + pqr[1]) + (pqr[2] + pqr[3]);
+        };
+        const float kv = dot128(kn);
         const float vval = co[2 * LISA_GDN_KEY_DIM + h * HD + v];
         const float delta = (vval - kv) * beta;
         for (int k = 0; k < HD; ++k) row[k] = lisa_fma(delta, kn[k], row[k]);
-        for (int q = 0; q < 4; ++q) {
-          float p = row[32 * q] * qn[32 * q];
-          for (int k = 32 * q + 1; k < 32 * q + 32; ++k) p = lisa_fma(row[k], qn[k], p);
-          pq[q] = p;
-        }
-        y[v] = bfr((pq[0] + pq[1]) + (pq[2] + pq[3]));
+        y[v] = bfr(dot128(qn));
       }
       if (y_out)
         for (int v = 0; v < HD; ++v) y_out[(size_t)t * LISA_GDN_VALUE_DIM + h * HD + v] = y[v];
