@@ -341,6 +341,37 @@ DEV void x_process(unsigned char* lds, int m, const ProRaw<R>& raw) {
   }
 }
 
+// Plain x of a split-K launch, per wave: only the wave's own K range (chunks
+// [128 it0, 128 it1) of each row, lane-strided, clamped past the end), staged in
+// its slice of the LDS row with its X_g; a wave reads only LDS it wrote, so no
+// workgroup barrier comes between the staging and the dot products.
+template <int K, int M>
+struct WaveX {
+  static constexpr int RW = 2 * QmvCfg<K, M>::IMAX;  // chunks per lane
+};
+
+template <int K, int M>
+DEV void xw_load(const LisaQmvParams& p, int m, int it0, int it1, int lane, uint4 (&raw)[WaveX<K, M>::RW]) {
+  const uint4* src = reinterpret_cast<const uint4*>(p.x_in + (size_t)m * K);
+#pragma unroll
+  for (int i = 0; i < WaveX<K, M>::RW; ++i) raw[i] = src[min(128 * it0 + lane + 64 * i, 128 * it1 - 1)];
+}
+
+template <int K, int M>
+DEV void xw_process(unsigned char* lds, int m, int it0, int it1, int lane, const uint4 (&raw)[WaveX<K, M>::RW]) {
+  using C = QmvCfg<K, M>;
+  float* gsum = reinterpret_cast<float*>(lds + C::XBYTES);
+#pragma unroll
+  for (int i = 0; i < WaveX<K, M>::RW; ++i) {
+    const int c = 128 * it0 + lane + 64 * i;
+    const bool valid = c < 128 * it1;
+    float x[8];
+    unpack_bf8(raw[i], x);
+    if (valid) put_chunk<K, M>(lds, m, 8 * c, x);
+    put_gsum<K, M>(gsum, m, 8 * c, valid, x);
+  }
+}
+
 template <int K, int M, int MODE, int R>
 DEV void pro_load(const LisaQmvParams& p, int m, ProRaw<R>& raw) {
   if constexpr (MODE == LISA_PRO_LOADX) x_load<K, M, R>(p, m, raw);
@@ -564,20 +595,32 @@ DEV void qmv_body(const LisaQmvParams& p, unsigned char* lds) {
   const int it1 = C::SPLIT ? (C::ITER * (wv + 1)) / 4 : C::ITER;
   const TileRef tr = tile_ref<K>(p, tile_ok ? tile : tiles - 1, rp);
 
-  ProRaw<C::RR> raw;
+  // split-K plain-x launches stage x per wave (see xw_load)
+  constexpr bool WAVEX = C::SPLIT && MODE == LISA_PRO_LOADX;
+  ProRaw<WAVEX ? 1 : C::RR> raw;
+  uint4 xr[WaveX<K, M>::RW];
   // issue order: prologue loads, then the weight stream (the fences keep the
   // scheduler from interleaving them, so the prologue waits only for its own).
   // A normalizing prologue holds many registers while it works, so only the
   // first iteration's weights are in flight across it: the rest are issued
   // after it, which roughly halves the register count and doubles the waves
   // resident per SIMD (every workgroup of the launch then runs in one round).
-  pro_load<K, M, MODE, C::RR>(p, 0, raw);
+  if constexpr (WAVEX) xw_load<K, M>(p, 0, it0, it1, lane, xr);
+  else pro_load<K, M, MODE, WAVEX ? 1 : C::RR>(p, 0, raw);
   __builtin_amdgcn_sched_barrier(0);
   Unit<C::IMAX> u;
   constexpr int EARLY = MODE == LISA_PRO_LOADX ? C::IMAX : 1;
   load_unit<K, C::IMAX>(u, tr, it0, it1, li, 0, EARLY);
   __builtin_amdgcn_sched_barrier(0);
-  qmv_prologue<K, M, MODE, C::RR>(p, lds, raw);
+  if constexpr (WAVEX) {
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+      if (m > 0) xw_load<K, M>(p, m, it0, it1, lane, xr);
+      xw_process<K, M>(lds, m, it0, it1, lane, xr);
+    }
+  } else {
+    qmv_prologue<K, M, MODE, WAVEX ? 1 : C::RR>(p, lds, raw);
+  }
   __builtin_amdgcn_sched_barrier(0);
   load_unit<K, C::IMAX>(u, tr, it0, it1, li, EARLY, C::IMAX);
   // epilogue inputs: read here behind the weights for plain-x launches; under a
