@@ -115,6 +115,145 @@ def calibrate_copy(mb):
           flush=True)
 
 
+FILL_WORDS, FILL_BF16, FILL_F32, FILL_SB, FILL_KV = range(5)  # lisa_kernels.h LISA_FILL_*
+DIST_NORMAL = 2  # lisa_synth.h LISA_DIST_NORMAL
+
+
+def synth_fill(pkg, dev, buf, n, kind, key, key2=0, capacity=0, filled=0):
+    p = pkg.SynthParams(buf.ptr, n, key, key2, kind, DIST_NORMAL, 0.0, 1.0, capacity, filled)
+    dev.dispatch("lisa_synth_fill", p, (4096,), (256,))
+
+
+def timed(pkg, dev, launch, reps):
+    """Mean µs of `reps` back-to-back launches (launch(i) issues launch i), HIP
+    events around the batch on the device stream."""
+    L = pkg.lib()
+    ev0, ev1 = pkg.C.c_void_p(), pkg.C.c_void_p()
+    pkg._check(L.lisa_event_create(pkg.C.byref(ev0)))
+    pkg._check(L.lisa_event_create(pkg.C.byref(ev1)))
+    launch(0)
+    dev.synchronize()
+    pkg._check(L.lisa_event_record(ev0, dev.h))
+    for i in range(reps):
+        launch(i)
+    pkg._check(L.lisa_event_record(ev1, dev.h))
+    dev.synchronize()
+    ms = pkg.C.c_float()
+    pkg._check(L.lisa_event_elapsed_ms(ev0, ev1, pkg.C.byref(ms)))
+    return 1e3 * ms.value / reps
+
+
+def kernel_configs(pkg, copies=8, reps=40):
+    """BASELINE configs 0 and 2 as single launches over `copies` rotating
+    weight / KV copies (together larger than the 256 MB infinity cache, so the
+    bytes come from HBM): config 0 = one q4 QMV, K = 5120, N = 17408, M = 1;
+    config 2 = the decode attention pair (split-K partials + merge) at
+    contexts 4096 and 32768."""
+    dev = pkg.Device(0)
+    out = {}
+    N, K = INTER, HIDDEN
+    ws = [dev.buffer(N * K // 2) for _ in range(copies)]
+    sbs = [dev.buffer(N * K // 64 * 4) for _ in range(copies)]
+    for c in range(copies):
+        synth_fill(pkg, dev, ws[c], N * K // 8, FILL_WORDS, 0xC0 + c)
+        synth_fill(pkg, dev, sbs[c], N * K // 64, FILL_SB, 0xC8 + c, 0xD0 + c)
+    x, y = dev.buffer(K * 2), dev.buffer(N * 4)
+    synth_fill(pkg, dev, x, K, FILL_BF16, 0xE0)
+    params = []
+    tiles = N // 8
+    for c in range(copies):
+        p = pkg.QmvParams()
+        p.pro_mode = pkg.PRO_LOADX
+        p.x_in = x.ptr
+        m = p.mats[0]
+        m.w, m.sb, m.out, m.rows, m.kind = ws[c].ptr, sbs[c].ptr, y.ptr, N, pkg.EPI_STORE
+        p.tile_start[0], p.tile_start[1], p.n_mats, p.ksplit = 0, tiles, 1, 1
+        params.append(p)
+    us = timed(pkg, dev, lambda i: dev.dispatch("lisa_qmv_k5120_m1_x", params[i % copies], ((tiles + 3) // 4,),
+                                                (256,), wait=False), reps)
+    qbytes = N * K * 0.5625 + K * 2 + N * 4
+    out["config0_qmv"] = {"shape": "M=1 K=5120 N=17408", "us": round(us, 2), "bytes": int(qbytes),
+                          "gbps": round(qbytes / us / 1e3, 1), "frac": round(qbytes / us / 1e3 / HBM_PEAK_GBS, 4)}
+    del ws, sbs
+    for ctx in (4096, 32768):
+        cap = ctx + 1
+        s_max = (cap + 63) // 64
+        kvb = 4 * cap * 256 * 2
+        kcs = [dev.buffer(kvb) for _ in range(copies)]
+        vcs = [dev.buffer(kvb) for _ in range(copies)]
+        for c in range(copies):
+            synth_fill(pkg, dev, kcs[c], 4 * (ctx - 1) * 256, FILL_KV, 0x100 + c, capacity=cap, filled=ctx - 1)
+            synth_fill(pkg, dev, vcs[c], 4 * (ctx - 1) * 256, FILL_KV, 0x200 + c, capacity=cap, filled=ctx - 1)
+        qp, kr, vr = dev.buffer(12288 * 4), dev.buffer(1024 * 4), dev.buffer(1024 * 4)
+        qn, kn = dev.buffer(512), dev.buffer(512)
+        synth_fill(pkg, dev, qp, 12288, FILL_F32, 0x300)
+        synth_fill(pkg, dev, kr, 1024, FILL_F32, 0x301)
+        synth_fill(pkg, dev, vr, 1024, FILL_F32, 0x302)
+        synth_fill(pkg, dev, qn, 256, FILL_BF16, 0x303)
+        synth_fill(pkg, dev, kn, 256, FILL_BF16, 0x304)
+        po, pm = dev.buffer(24 * s_max * 256 * 4), dev.buffer(24 * s_max * 2 * 4)
+        pos, g = dev.upload(np.array([ctx - 1, 0, 0, 0], np.uint32)), dev.buffer(6144 * 2)
+        aps = []
+        for c in range(copies):
+            a = pkg.AttnParams()
+            a.q_proj, a.k_raw, a.v_raw, a.q_norm_w, a.k_norm_w = qp.ptr, kr.ptr, vr.ptr, qn.ptr, kn.ptr
+            a.key_cache, a.value_cache = kcs[c].ptr, vcs[c].ptr
+            a.part_o, a.part_ml, a.pos, a.gated = po.ptr, pm.ptr, pos.ptr, g.ptr
+            a.capacity, a.s_max = cap, s_max
+            aps.append(a)
+
+        def launch(i):
+            dev.dispatch("lisa_attn_partial_m1", aps[i % copies], (s_max, 4), (256,), wait=False)
+            dev.dispatch("lisa_attn_merge_m1", aps[i % copies], (24, 1), (256,), wait=False)
+
+        us = timed(pkg, dev, launch, reps)
+        abytes = 2 * 4 * ctx * 256 * 2 + 24 * s_max * 258 * 4 * 2
+        out[f"config2_attention_ctx{ctx}"] = {"us": round(us, 2), "bytes": int(abytes),
+                                              "gbps": round(abytes / us / 1e3, 1),
+                                              "frac": round(abytes / us / 1e3 / HBM_PEAK_GBS, 4),
+                                              "note": "partial + merge launches; KV read + slice partials"}
+        del kcs, vcs
+    out["method"] = (f"{copies} rotating copies, {reps} back-to-back launches between HIP events (no graph), "
+                     "bf16/f32 inputs from the seeded device generator")
+    return out
+
+
+def speculative_phase(pkg, steps=128, p_accept=0.6, seed=0x5EED):
+    """MTP block-3 speculative decoding on the config-3 model
+    at ctx 4096, drafts forced to a seeded Bernoulli(p_accept) agreement with
+    the target-only greedy stream (speculative/mod.rs:102-198); the emitted
+    stream must equal that greedy stream."""
+    cap = CTX + 2 * steps + 64
+    r = pkg.Runner(layers=LAYERS, vocab=VOCAB, capacity=cap, seed=SEED, with_mtp=True, use_graph=True)
+    try:
+        r.fill_state(CTX, CTX_SEED)
+        am, hid = r.forward_token_decode(FIRST_TOKEN, want_hidden=True)
+        truth = [am] + list(r.decode_greedy(am, steps - 1))
+        r.fill_state(CTX, CTX_SEED)
+        am2, hid2 = r.forward_token_decode(FIRST_TOKEN, want_hidden=True)
+        seed_tok = r.mtp_forward(am2, 0, 0)
+        seed_hidden = (r.mtp_normalized().astype(np.uint32) << 16).view(np.float32)
+        L = pkg.lib()
+        dev = L.lisa_runner_device(r.h)
+        ev0, ev1 = pkg.C.c_void_p(), pkg.C.c_void_p()
+        pkg._check(L.lisa_event_create(pkg.C.byref(ev0)))
+        pkg._check(L.lisa_event_create(pkg.C.byref(ev1)))
+        pkg._check(L.lisa_device_synchronize(dev))
+        pkg._check(L.lisa_event_record(ev0, dev))
+        toks, st = r.generate_greedy_block3(am2, hid2, seed_tok, seed_hidden, steps, force_truth=truth,
+                                            force_seed=seed, p_accept=p_accept)
+        pkg._check(L.lisa_event_record(ev1, dev))
+        pkg._check(L.lisa_device_synchronize(dev))
+        ms = pkg.C.c_float()
+        pkg._check(L.lisa_event_elapsed_ms(ev0, ev1, pkg.C.byref(ms)))
+    finally:
+        r.close()
+    return {"speculative_decode_tok_s": round(steps / (ms.value / 1e3), 2),
+            "acceptance": round(st["accepted_drafts"] / max(1, st["drafted_tokens"]), 4),
+            "tokens": steps, "rounds": st["rounds"], "target_forwards": st["target_forwards"],
+            "exact_match": bool(list(toks) == truth), "p_accept_forced": p_accept}
+
+
 GEMM_SHAPES = [(2048, INTER, HIDDEN, "mlp gate (and up)"), (2048, HIDDEN, INTER, "mlp down"),
                (2048, 12288, HIDDEN, "attention q")]
 BF16_PEAK_TFLOPS = 2500.0
@@ -174,6 +313,9 @@ def main():
     ap.add_argument("--prefill-tokens", type=int, default=2048,
                     help="config 3 prompt length for the prefill phase (0 skips it)")
     ap.add_argument("--gemm-only", action="store_true", help="only time the prefill q4 GEMM kernels")
+    ap.add_argument("--no-extra", action="store_true",
+                    help="skip the per-config kernels (configs 0, 2) and the speculative phase (config 4)")
+    ap.add_argument("--repeats", type=int, default=5, help="repeats of the timed region for the median")
     ap.add_argument("--no-gemm", action="store_true", help="skip the prefill q4 GEMM phase")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="only run the plain copy kernel over MIB MiB (counter calibration)")
@@ -226,6 +368,20 @@ def main():
     gbps = bpt * tok_s / 1e9
     print(f"[bench] {K} steps: {ms_per_step:.3f} ms/token (host {1e3 * t_host / K:.3f}), {tok_s:.1f} tok/s, "
           f"{gbps:.0f} GB/s", file=sys.stderr, flush=True)
+    # the same timed region again from the same state, for the median of the runs
+    rep_tok_s = [tok_s]
+    for _ in range(max(0, args.repeats - 1)):
+        runner.fill_state(CTX, CTX_SEED)
+        pkg._check(L.lisa_device_synchronize(dev))
+        pkg._check(L.lisa_event_record(ev0, dev))
+        rep_tokens = runner.decode_greedy(FIRST_TOKEN, K)
+        pkg._check(L.lisa_event_record(ev1, dev))
+        pkg._check(L.lisa_event_elapsed_ms(ev0, ev1, pkg.C.byref(ms)))
+        rep_tok_s.append(K / (ms.value / 1e3))
+        if list(rep_tokens) != list(tokens):
+            raise SystemExit("bench.py: a repeat of the timed region produced different tokens")
+    repeats = {"n": len(rep_tok_s), "median_tok_s": round(float(np.median(rep_tok_s)), 3),
+               "min_tok_s": round(min(rep_tok_s), 3), "max_tok_s": round(max(rep_tok_s), 3)}
 
     # per-launch profile (eager, hipEvents around every launch)
     runner.fill_state(CTX, CTX_SEED)
@@ -286,12 +442,20 @@ def main():
                      "kernel": ROOFLINE_KERNEL + " (MLP gate/up + SwiGLU)",
                      "bytes_per_launch": gate_up_bytes(), "avg_launch_us": round(gu_avg_s * 1e6, 2)},
         "kernels_us_per_token": kernels_us,
+        "repeats": repeats,
     }
     if prefill:
         result["target_prefill_tok_s"] = prefill["tok_s"]
         result["prefill"] = prefill
     if not args.no_gemm:
         result["prefill_gemm"] = gemm_phase(pkg)
+    if not args.no_extra:
+        result["kernel_configs"] = kernel_configs(pkg)
+        spec = speculative_phase(pkg)
+        result["speculative_decode_tok_s"] = spec["speculative_decode_tok_s"]
+        result["acceptance"] = spec["acceptance"]
+        result["speculative"] = spec
+        print(f"[bench] configs {result['kernel_configs']}; speculative {spec}", file=sys.stderr, flush=True)
 
     if not args.no_cpu and args.cpu_steps > 0:
         orc = load("lisa_oracle", ROOT / "oracle" / "oracle.py")
@@ -309,8 +473,10 @@ def main():
         cpu_s = time.perf_counter() - t_cpu
         model.close()
         cpu_tok_s = args.cpu_steps / cpu_s
+        cpu_gbps = bytes_per_token(CTX + (args.cpu_steps + 1) / 2.0) * cpu_tok_s / 1e9
         result["cpu_baseline"] = {
-            "value": round(cpu_tok_s, 4), "unit": "tok/s", "cores": orc.threads(), "kind": "port",
+            "value": round(cpu_tok_s, 4), "unit": "tok/s", "gbps": round(cpu_gbps, 2), "cores": orc.threads(),
+            "kind": "port",
             "sample": f"{args.cpu_steps} M=1 decode steps of the full 64-layer model at ctx {CTX} "
                       f"(same weights, context and first token as the GPU run)"}
         result["exact_match"] = bool(list(tokens[: args.cpu_steps]) == cpu_tokens)
