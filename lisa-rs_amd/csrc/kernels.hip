@@ -1056,28 +1056,48 @@ extern "C" __global__ __launch_bounds__(512) void lisa_gdn_recurrence_m3(LisaGdn
 // l, l+64, l+128, l+192; the sum of squares is tree64 of each element column
 // then (W0+W1)+(W2+W3) — the rows-of-256 tree with one element per thread
 // (attention.metal:99-114, 118-155).
-DEV void head_norm_rope_wave(const float* raw, const uint16_t* w, uint32_t pos, int lane, float out[4]) {
+// The pieces of head_norm_rope_wave, so a wave can issue the loads of all of
+// its heads before the first one is processed and share the rotation of a
+// position across heads.
+DEV void hnr_load(const float* raw, const uint16_t* w, int lane, float (&v)[4], float (&wv)[4]) {
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    v[j] = raw[lane + 64 * j];
+    wv[j] = bf2f(w[lane + 64 * j]);
+  }
+}
+
+DEV void rope_sincos(uint32_t pos, int lane, float& s, float& c) {
+  const float angle = (float)pos * kRopeInvFreq[lane & 31];
+  lisa_sincosf(angle, &s, &c);
+}
+
+DEV void hnr_finish(const float (&raw)[4], const float (&wv)[4], float s, float c, int lane, float out[4]) {
   float v[4], wsum[4];
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
-    v[j] = lisa_bf16r(raw[lane + 64 * j]);
+    v[j] = lisa_bf16r(raw[j]);
     wsum[j] = tree64(v[j] * v[j]);
   }
   const float tot = (wsum[0] + wsum[1]) + (wsum[2] + wsum[3]);
   const float inv = lisa_rsqrt(tot / 256.0f + LISA_EPS);
   float n[4];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) n[j] = (v[j] * inv) * bf2f(w[lane + 64 * j]);
+  for (int j = 0; j < 4; ++j) n[j] = (v[j] * inv) * wv[j];
   const float other = xor_lane<32>(n[0]);  // n[l+32] for l<32, n[l-32] for l>=32
-  const float angle = (float)pos * kRopeInvFreq[lane & 31];
-  float s, c;
-  lisa_sincosf(angle, &s, &c);
   if (lane < 32)
     out[0] = lisa_bf16r(n[0] * c - other * s);
   else
     out[0] = lisa_bf16r(n[0] * c + other * s);
 #pragma unroll
   for (int j = 1; j < 4; ++j) out[j] = lisa_bf16r(n[j]);
+}
+
+DEV void head_norm_rope_wave(const float* raw, const uint16_t* w, uint32_t pos, int lane, float out[4]) {
+  float v[4], wv[4], s, c;
+  hnr_load(raw, w, lane, v, wv);
+  rope_sincos(pos, lane, s, c);
+  hnr_finish(v, wv, s, c, lane, out);
 }
 
 // Scores of one (row, head) over a slice of n cached tokens by one wave (lane =
@@ -1140,6 +1160,15 @@ DEV void attn_partial_body(const LisaAttnParams& p) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const size_t cache_base = (size_t)kvh * p.capacity * HD;
 
+  // 0. the raw query heads of this wave (pairs pr = wave + 4j of row t = pr / 6,
+  // head i = pr % 6), loaded before anything else
+  constexpr int QP = (6 * M + 3) / 4;
+  float qraw[QP][4], qw[QP][4];
+#pragma unroll
+  for (int j = 0; j < QP; ++j) {
+    const int pr = min(wave + 4 * j, 6 * M - 1), t = pr / 6, i = pr % 6;
+    hnr_load(p.q_proj + (size_t)t * LISA_ATT_Q_OUT + (kvh * 6 + i) * 512, p.q_norm_w, lane, qraw[j], qw[j]);
+  }
   // 1. rows of the slice already in the cache (positions < base); a full slice
   // issues all of its loads before the first LDS store
   const int nold = (base > t0) ? (int)min((uint32_t)T, base - t0) : 0;
@@ -1186,13 +1215,20 @@ DEV void attn_partial_body(const LisaAttnParams& p) {
       }
     }
   }
-  // 3. normalized, rotated queries of the 6 heads sharing this KV head
-  for (int pr = wave; pr < 6 * M; pr += 4) {
-    const int t = pr / 6, i = pr % 6, h = kvh * 6 + i;
-    float qo[4];
-    head_norm_rope_wave(p.q_proj + (size_t)t * LISA_ATT_Q_OUT + h * 512, p.q_norm_w, base + t, lane, qo);
+  // 3. normalized, rotated queries of the 6 heads sharing this KV head (one
+  // rotation per row position)
+  float rs[M], rc[M];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) qv[(t * 6 + i) * HD + lane + 64 * j] = qo[j];
+  for (int t = 0; t < M; ++t) rope_sincos(base + t, lane, rs[t], rc[t]);
+#pragma unroll
+  for (int j = 0; j < QP; ++j) {
+    const int pr = wave + 4 * j;
+    if (pr >= 6 * M) break;
+    const int t = pr / 6, i = pr % 6;
+    float qo[4];
+    hnr_finish(qraw[j], qw[j], rs[t], rc[t], lane, qo);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) qv[(t * 6 + i) * HD + lane + 64 * e] = qo[e];
   }
   __syncthreads();
   // 4. scores and slice softmax statistics: lane = token of the slice
