@@ -33,9 +33,17 @@ __constant__ float kRopeInvFreq[LISA_ROPE_PAIRS] = LISA_ROPE_INV_FREQ_TABLE;
 // ---------------------------------------------------------------------------
 // cross-lane helpers
 // ---------------------------------------------------------------------------
+// v of lane l ^ MASK. Masks 1 and 2 are DPP quad permutes and 8 is a DPP
+// rotate by 8 within each row of 16 ((l + 8) mod 16 = l ^ 8), so those steps
+// fold into the consuming VALU op; 4 and 16 use ds_swizzle, 32 ds_bpermute.
 template <int MASK>
 DEV float xor_lane(float v) {
-  if constexpr (MASK >= 32) {
+  if constexpr (MASK == 1 || MASK == 2 || MASK == 8) {
+    constexpr int ctrl = MASK == 1 ? 0xb1 /* quad_perm [1,0,3,2] */
+                         : MASK == 2 ? 0x4e /* quad_perm [2,3,0,1] */
+                                     : 0x128 /* row_ror:8 */;
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), ctrl, 0xf, 0xf, false));
+  } else if constexpr (MASK >= 32) {
     return __shfl_xor(v, MASK, 64);
   } else {
     // ds_swizzle bitmask mode: and_mask = 0x1f, or_mask = 0, xor_mask = MASK.
@@ -106,11 +114,13 @@ DEV float hi_bf(uint32_t u) { return __uint_as_float(u & 0xffff0000u); }
 // keep the register count low enough for the whole grid to be resident), and
 // the dispatcher balances the tail.
 //
-// x lives in LDS (f32, or bf16 for K = 17408), one copy per input row, in
-// 64-element groups padded to 272 (f32) or 144 (bf16) bytes: the 16 lanes of a
-// row-group read 16 consecutive groups at the same offset, and the padding
-// puts them on disjoint banks, so every read address is a per-lane base plus
-// an immediate. X_g follows it.
+// x lives in LDS as f32 in 64-element groups padded to 272 bytes: the 16 lanes
+// of a row-group read 16 consecutive groups at the same offset, and the
+// padding puts them on disjoint banks, so every read address is a per-lane
+// base plus an immediate. X_g follows it. Launches with a workgroup prologue
+// (K = 5120, the MTP fc) stage every input row whole, once per workgroup;
+// split-K plain-x launches stage x per wave and per group iteration instead
+// (WaveSlot below).
 
 template <int K, int M>
 struct QmvCfg {
@@ -118,20 +128,43 @@ struct QmvCfg {
   static constexpr int ITER = G / 16;
   static constexpr bool SPLIT = (K != LISA_HIDDEN);
   static constexpr int IMAX = SPLIT ? (ITER + 3) / 4 : ITER;
-  static constexpr bool XF32 = (K != LISA_INTER);
   static constexpr int NCH = K / 8;                 // 8-element chunks of x
   static constexpr int RX = (NCH + 255) / 256;      // chunk rounds per thread (plain x)
   static constexpr bool NORMK = (K == LISA_HIDDEN || K == 2 * LISA_HIDDEN);
   static constexpr int RR = (NORMK && RX < 3) ? 3 : RX;
-  static constexpr int GSTRIDE = XF32 ? 272 : 144;  // bytes per padded 64-group
+  static constexpr int GSTRIDE = 272;               // bytes per padded 64-group
   static constexpr int ROWBYTES = G * GSTRIDE;
   static constexpr int XBYTES = M * ROWBYTES;
   static constexpr int GBYTES = M * G * 4;
   static constexpr int RBYTES = 64 * 4;
   static constexpr int KBYTES = 4 * 8 * M * 4;
-  static constexpr int BYTES = XBYTES + GBYTES + RBYTES + KBYTES;
   static_assert(G % 16 == 0, "K must be a multiple of 1024");
 };
+
+// Split-K plain-x launches: each wave converts, for one group iteration at a
+// time, the 1024 x values [1024 ii, 1024 ii + 1024) of every input row to f32
+// in its own LDS slot (16 padded groups per row, then the 16 X_g per row);
+// lane l converts values [16 l, 16 l + 16), a quarter of group l / 4. The
+// bf16 unpack then happens once per wave rather than once per row-group, and
+// a wave reads only LDS it wrote, so no workgroup barrier is involved.
+template <int M>
+struct WaveSlot {
+  static constexpr int ROWB = 16 * 272;
+  static constexpr int XB = M * ROWB;
+  static constexpr int BYTES = XB + M * 16 * 4;
+};
+
+template <int K, int M, int MODE>
+DEV constexpr bool qmv_wave_staged() {
+  return QmvCfg<K, M>::SPLIT && MODE == LISA_PRO_LOADX;
+}
+
+template <int K, int M, int MODE>
+DEV constexpr int qmv_lds_bytes() {
+  using C = QmvCfg<K, M>;
+  return (qmv_wave_staged<K, M, MODE>() ? 4 * WaveSlot<M>::BYTES : C::XBYTES + C::GBYTES) + C::RBYTES +
+         C::KBYTES;
+}
 
 // The 5120-wide segments a normalizing prologue reads: 640 chunks of 8, thread
 // t owns chunks t, t + 256, t + 512 (< 640).
@@ -165,12 +198,13 @@ DEV void put_chunk(unsigned char* lds, int m, int k0, const float (&x)[8]) {
   using C = QmvCfg<K, M>;
   const int g = k0 >> 6, j = (k0 >> 3) & 7;
   unsigned char* base = lds + m * C::ROWBYTES + g * C::GSTRIDE;
-  if constexpr (C::XF32) {
-    *reinterpret_cast<float4*>(base + 32 * j) = make_float4(x[0], x[1], x[2], x[3]);
-    *reinterpret_cast<float4*>(base + 32 * j + 16) = make_float4(x[4], x[5], x[6], x[7]);
-  } else {
-    *reinterpret_cast<uint4*>(base + 16 * j) = pack_bf8(x);
-  }
+  *reinterpret_cast<float4*>(base + 32 * j) = make_float4(x[0], x[1], x[2], x[3]);
+  *reinterpret_cast<float4*>(base + 32 * j + 16) = make_float4(x[4], x[5], x[6], x[7]);
+}
+
+// Sum of eight values, pairs first: the distance-1, 2, 4 levels of the X_g tree.
+DEV float sum8(const float (&x)[8]) {
+  return ((x[0] + x[1]) + (x[2] + x[3])) + ((x[4] + x[5]) + (x[6] + x[7]));
 }
 
 // X_g of the chunk's group: ascending-distance tree over the 64 values
@@ -178,7 +212,7 @@ DEV void put_chunk(unsigned char* lds, int m, int k0, const float (&x)[8]) {
 // the group's chunks). Every lane calls it; lane c%8 == 0 stores.
 template <int K, int M>
 DEV void put_gsum(float* gsum, int m, int k0, bool valid, const float (&x)[8]) {
-  float s = ((x[0] + x[1]) + (x[2] + x[3])) + ((x[4] + x[5]) + (x[6] + x[7]));
+  float s = sum8(x);
   s = s + xor_lane<1>(s);
   s = s + xor_lane<2>(s);
   s = s + xor_lane<4>(s);
@@ -341,36 +375,51 @@ DEV void x_process(unsigned char* lds, int m, const ProRaw<R>& raw) {
   }
 }
 
-// Plain x of a split-K launch, per wave: only the wave's own K range (chunks
-// [128 it0, 128 it1) of each row, lane-strided, clamped past the end), staged in
-// its slice of the LDS row with its X_g; a wave reads only LDS it wrote, so no
-// workgroup barrier comes between the staging and the dot products.
+// Raw x of a split-K plain-x launch for the wave's group iterations: for
+// iteration i (clamped into the wave's range like its weights) and row m, lane
+// l loads the 16 bf16 values [1024 ii + 16 l, 1024 ii + 16 l + 16).
 template <int K, int M>
-struct WaveX {
-  static constexpr int RW = 2 * QmvCfg<K, M>::IMAX;  // chunks per lane
-};
-
-template <int K, int M>
-DEV void xw_load(const LisaQmvParams& p, int m, int it0, int it1, int lane, uint4 (&raw)[WaveX<K, M>::RW]) {
-  const uint4* src = reinterpret_cast<const uint4*>(p.x_in + (size_t)m * K);
+DEV void wx_load(const LisaQmvParams& p, int it0, int it1, int lane, uint4 (&xr)[QmvCfg<K, M>::IMAX][M][2]) {
 #pragma unroll
-  for (int i = 0; i < WaveX<K, M>::RW; ++i) raw[i] = src[min(128 * it0 + lane + 64 * i, 128 * it1 - 1)];
-}
-
-template <int K, int M>
-DEV void xw_process(unsigned char* lds, int m, int it0, int it1, int lane, const uint4 (&raw)[WaveX<K, M>::RW]) {
-  using C = QmvCfg<K, M>;
-  float* gsum = reinterpret_cast<float*>(lds + C::XBYTES);
+  for (int i = 0; i < QmvCfg<K, M>::IMAX; ++i) {
+    const int ii = max(min(it0 + i, it1 - 1), 0);
 #pragma unroll
-  for (int i = 0; i < WaveX<K, M>::RW; ++i) {
-    const int c = 128 * it0 + lane + 64 * i;
-    const bool valid = c < 128 * it1;
-    float x[8];
-    unpack_bf8(raw[i], x);
-    if (valid) put_chunk<K, M>(lds, m, 8 * c, x);
-    put_gsum<K, M>(gsum, m, 8 * c, valid, x);
+    for (int m = 0; m < M; ++m) {
+      const uint4* src = reinterpret_cast<const uint4*>(p.x_in + (size_t)m * K) + 128 * ii + 2 * lane;
+      xr[i][m][0] = src[0];
+      xr[i][m][1] = src[1];
+    }
   }
 }
+
+// One iteration's x into the wave's slot: f32 values, and X_g as the
+// ascending-distance tree (distances 1, 2, 4 inside each 8-value chunk by sum8,
+// 8 inside the lane, 16 and 32 across the group's four lanes).
+template <int M>
+DEV void wx_stage(unsigned char* slot, int lane, const uint4 (&xr)[M][2]) {
+  const int gl = lane >> 2, q = lane & 3;
+  float* gs = reinterpret_cast<float*>(slot + WaveSlot<M>::XB);
+#pragma unroll
+  for (int m = 0; m < M; ++m) {
+    float a[8], b[8];
+    unpack_bf8(xr[m][0], a);
+    unpack_bf8(xr[m][1], b);
+    unsigned char* dst = slot + m * WaveSlot<M>::ROWB + gl * 272 + q * 64;
+    *reinterpret_cast<float4*>(dst) = make_float4(a[0], a[1], a[2], a[3]);
+    *reinterpret_cast<float4*>(dst + 16) = make_float4(a[4], a[5], a[6], a[7]);
+    *reinterpret_cast<float4*>(dst + 32) = make_float4(b[0], b[1], b[2], b[3]);
+    *reinterpret_cast<float4*>(dst + 48) = make_float4(b[4], b[5], b[6], b[7]);
+    float s = sum8(a) + sum8(b);
+    s = s + xor_lane<1>(s);
+    s = s + xor_lane<2>(s);
+    if (q == 0) gs[m * 16 + gl] = s;
+  }
+}
+
+// Orders the wave's own LDS writes and reads around a slot hand-over (LDS
+// operations of one wave complete in issue order; this keeps the compiler from
+// moving them across).
+DEV void wave_lds_fence() { __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront"); }
 
 template <int K, int M, int MODE, int R>
 DEV void pro_load(const LisaQmvParams& p, int m, ProRaw<R>& raw) {
@@ -494,12 +543,12 @@ DEV void load_unit(Unit<IMAX>& u, const TileRef& t, int it0, int it1, int li, in
   }
 }
 
-// One group of the lane's two rows against the M staged x rows.
-template <int K, int M>
-DEV void group_dot2(const unsigned char* lds, int g, const uint4& a0, const uint4& b0, const uint4& a1,
+// One group of the lane's two rows against the M staged x rows: x of row m,
+// group g at xs + m * ROWB + 272 g, its X_g at gsum[m * GROW + g].
+template <int ROWB, int GROW, int M>
+DEV void group_dot2(const unsigned char* xs, int g, const uint4& a0, const uint4& b0, const uint4& a1,
                     const uint4& b1, uint32_t sb0, uint32_t sb1, const float* gsum, float (&T0)[M],
                     float (&T1)[M]) {
-  using C = QmvCfg<K, M>;
   const uint32_t w0[8] = {a0.x, a0.y, a0.z, a0.w, b0.x, b0.y, b0.z, b0.w};
   const uint32_t w1[8] = {a1.x, a1.y, a1.z, a1.w, b1.x, b1.y, b1.z, b1.w};
   float lo0[M], hi0[M], lo1[M], hi1[M];
@@ -515,15 +564,11 @@ DEV void group_dot2(const unsigned char* lds, int g, const uint4& a0, const uint
 #pragma unroll
     for (int m = 0; m < M; ++m) {
       float x[8];
-      const unsigned char* base = lds + m * C::ROWBYTES + g * C::GSTRIDE;
-      if constexpr (C::XF32) {
-        const float4 xa = *reinterpret_cast<const float4*>(base + 32 * j);
-        const float4 xb = *reinterpret_cast<const float4*>(base + 32 * j + 16);
-        x[0] = xa.x; x[1] = xa.y; x[2] = xa.z; x[3] = xa.w;
-        x[4] = xb.x; x[5] = xb.y; x[6] = xb.z; x[7] = xb.w;
-      } else {
-        unpack_bf8(*reinterpret_cast<const uint4*>(base + 16 * j), x);
-      }
+      const unsigned char* base = xs + m * ROWB + g * 272;
+      const float4 xa = *reinterpret_cast<const float4*>(base + 32 * j);
+      const float4 xb = *reinterpret_cast<const float4*>(base + 32 * j + 16);
+      x[0] = xa.x; x[1] = xa.y; x[2] = xa.z; x[3] = xa.w;
+      x[4] = xb.x; x[5] = xb.y; x[6] = xb.z; x[7] = xb.w;
       lo0[m] = fmix_lo(x[0], p0, lo0[m]);
       lo0[m] = fmix_lo(x[2], p2, lo0[m]);
       lo0[m] = fmix_hi(x[4], p0, lo0[m]);
@@ -546,7 +591,7 @@ DEV void group_dot2(const unsigned char* lds, int g, const uint4& a0, const uint
   const float s1 = lo_bf(sb1) * 16777216.0f, bb1 = hi_bf(sb1);
 #pragma unroll
   for (int m = 0; m < M; ++m) {
-    const float xg = gsum[m * C::G + g];
+    const float xg = gsum[m * GROW + g];
     T0[m] = T0[m] + lisa_fma(s0, lo0[m] + hi0[m] * 0.0625f, bb0 * xg);
     T1[m] = T1[m] + lisa_fma(s1, lo1[m] + hi1[m] * 0.0625f, bb1 * xg);
   }
@@ -581,8 +626,10 @@ DEV void epi_preload(const LisaQmvParams& p, const TileRef& tr, int li, EpiPre<M
 template <int K, int M, int MODE, int EPI>
 DEV void qmv_body(const LisaQmvParams& p, unsigned char* lds) {
   using C = QmvCfg<K, M>;
+  // split-K plain-x launches stage x per wave and per group iteration (WaveSlot)
+  constexpr bool WAVEX = qmv_wave_staged<K, M, MODE>();
   const float* gsum = reinterpret_cast<const float*>(lds + C::XBYTES);
-  float* red = const_cast<float*>(gsum) + M * C::G;
+  float* red = reinterpret_cast<float*>(lds + (WAVEX ? 4 * WaveSlot<M>::BYTES : C::XBYTES + C::GBYTES));
   float* kred = red + 64;  // [4 waves][8 rows][M]
 
   // wv is wave-uniform: keeping it scalar keeps the matrix lookup on scalar loads
@@ -595,32 +642,22 @@ DEV void qmv_body(const LisaQmvParams& p, unsigned char* lds) {
   const int it1 = C::SPLIT ? (C::ITER * (wv + 1)) / 4 : C::ITER;
   const TileRef tr = tile_ref<K>(p, tile_ok ? tile : tiles - 1, rp);
 
-  // split-K plain-x launches stage x per wave (see xw_load)
-  constexpr bool WAVEX = C::SPLIT && MODE == LISA_PRO_LOADX;
   ProRaw<WAVEX ? 1 : C::RR> raw;
-  uint4 xr[WaveX<K, M>::RW];
+  uint4 xr[WAVEX ? C::IMAX : 1][M][2];
   // issue order: prologue loads, then the weight stream (the fences keep the
   // scheduler from interleaving them, so the prologue waits only for its own).
   // A normalizing prologue holds many registers while it works, so only the
   // first iteration's weights are in flight across it: the rest are issued
   // after it, which roughly halves the register count and doubles the waves
   // resident per SIMD (every workgroup of the launch then runs in one round).
-  if constexpr (WAVEX) xw_load<K, M>(p, 0, it0, it1, lane, xr);
+  if constexpr (WAVEX) wx_load<K, M>(p, it0, it1, lane, xr);
   else pro_load<K, M, MODE, WAVEX ? 1 : C::RR>(p, 0, raw);
   __builtin_amdgcn_sched_barrier(0);
   Unit<C::IMAX> u;
   constexpr int EARLY = MODE == LISA_PRO_LOADX ? C::IMAX : 1;
   load_unit<K, C::IMAX>(u, tr, it0, it1, li, 0, EARLY);
   __builtin_amdgcn_sched_barrier(0);
-  if constexpr (WAVEX) {
-#pragma unroll
-    for (int m = 0; m < M; ++m) {
-      if (m > 0) xw_load<K, M>(p, m, it0, it1, lane, xr);
-      xw_process<K, M>(lds, m, it0, it1, lane, xr);
-    }
-  } else {
-    qmv_prologue<K, M, MODE, WAVEX ? 1 : C::RR>(p, lds, raw);
-  }
+  if constexpr (!WAVEX) qmv_prologue<K, M, MODE, WAVEX ? 1 : C::RR>(p, lds, raw);
   __builtin_amdgcn_sched_barrier(0);
   load_unit<K, C::IMAX>(u, tr, it0, it1, li, EARLY, C::IMAX);
   // epilogue inputs: read here behind the weights for plain-x launches; under a
@@ -633,11 +670,22 @@ DEV void qmv_body(const LisaQmvParams& p, unsigned char* lds) {
   float T0[M], T1[M];
 #pragma unroll
   for (int m = 0; m < M; ++m) { T0[m] = 0.0f; T1[m] = 0.0f; }
+  unsigned char* slot = lds + wv * WaveSlot<M>::BYTES;
 #pragma unroll
-  for (int i = 0; i < C::IMAX; ++i)
-    if (it0 + i < it1)
-      group_dot2<K, M>(lds, 16 * (it0 + i) + li, u.a0[i], u.b0[i], u.a1[i], u.b1[i], u.s0[i], u.s1[i], gsum, T0,
-                       T1);
+  for (int i = 0; i < C::IMAX; ++i) {
+    if (it0 + i < it1) {
+      if constexpr (WAVEX) {
+        wx_stage<M>(slot, lane, xr[i]);
+        wave_lds_fence();
+        group_dot2<WaveSlot<M>::ROWB, 16, M>(slot, li, u.a0[i], u.b0[i], u.a1[i], u.b1[i], u.s0[i], u.s1[i],
+                                              reinterpret_cast<const float*>(slot + WaveSlot<M>::XB), T0, T1);
+        wave_lds_fence();
+      } else {
+        group_dot2<C::ROWBYTES, C::G, M>(lds, 16 * (it0 + i) + li, u.a0[i], u.b0[i], u.a1[i], u.b1[i], u.s0[i],
+                                         u.s1[i], gsum, T0, T1);
+      }
+    }
+  }
 #pragma unroll
   for (int m = 0; m < M; ++m) { T0[m] = tree16(T0[m]); T1[m] = tree16(T1[m]); }
 
@@ -772,13 +820,13 @@ DEV void qmv_body(const LisaQmvParams& p, unsigned char* lds) {
 // lisa_qmv_k5120_m<M>_<resnorm|prenorm>_<gateup|argmax> (MLP gate/up, lm_head).
 #define QMV_KERNEL(K, M, MODE, NAME)                                                             \
   extern "C" __global__ __launch_bounds__(256) void lisa_qmv_k##K##_m##M##_##NAME(LisaQmvParams p) { \
-    __shared__ __attribute__((aligned(16))) unsigned char lds[QmvCfg<K, M>::BYTES];                \
+    __shared__ __attribute__((aligned(16))) unsigned char lds[qmv_lds_bytes<K, M, MODE>()];        \
     qmv_body<K, M, MODE, -1>(p, lds);                                                            \
   }
 #define QMV_KERNEL_EPI(K, M, MODE, NAME, EPI, ENAME)                                             \
   extern "C" __global__ __launch_bounds__(256) void lisa_qmv_k##K##_m##M##_##NAME##_##ENAME(       \
       LisaQmvParams p) {                                                                         \
-    __shared__ __attribute__((aligned(16))) unsigned char lds[QmvCfg<K, M>::BYTES];                \
+    __shared__ __attribute__((aligned(16))) unsigned char lds[qmv_lds_bytes<K, M, MODE>()];        \
     qmv_body<K, M, MODE, EPI>(p, lds);                                                           \
   }
 
