@@ -646,20 +646,27 @@ DEV void qmv_body(const LisaQmvParams& p, unsigned char* lds) {
   uint4 xr[WAVEX ? C::IMAX : 1][M][2];
   // issue order: prologue loads, then the weight stream (the fences keep the
   // scheduler from interleaving them, so the prologue waits only for its own).
-  // A normalizing prologue holds many registers while it works, so only the
-  // first iteration's weights are in flight across it: the rest are issued
-  // after it, which roughly halves the register count and doubles the waves
-  // resident per SIMD (every workgroup of the launch then runs in one round).
+  // The weights are software-pipelined two group iterations deep: the loads of
+  // iteration i + 2 are issued as soon as iteration i has been consumed. A
+  // wave that issued its whole stream up front would stall at issue (the
+  // memory pipeline backs up) and could not start its dot products until the
+  // last load had gone out, so its arithmetic would pile up at the end of the
+  // launch; two iterations in flight per wave keep the pipeline full. A
+  // normalizing prologue holds many registers while it works, so only the
+  // first iteration is in flight across it, which keeps the register count low
+  // enough for every workgroup of the launch to be resident in one round.
+  // Non-split plain-x launches (small and rare) issue their whole stream first.
   if constexpr (WAVEX) wx_load<K, M>(p, it0, it1, lane, xr);
   else pro_load<K, M, MODE, WAVEX ? 1 : C::RR>(p, 0, raw);
   __builtin_amdgcn_sched_barrier(0);
   Unit<C::IMAX> u;
-  constexpr int EARLY = MODE == LISA_PRO_LOADX ? C::IMAX : 1;
+  constexpr int DEPTH = MODE == LISA_PRO_LOADX && !WAVEX ? C::IMAX : (C::IMAX < 2 ? C::IMAX : 2);
+  constexpr int EARLY = MODE == LISA_PRO_LOADX ? DEPTH : 1;
   load_unit<K, C::IMAX>(u, tr, it0, it1, li, 0, EARLY);
   __builtin_amdgcn_sched_barrier(0);
   if constexpr (!WAVEX) qmv_prologue<K, M, MODE, WAVEX ? 1 : C::RR>(p, lds, raw);
   __builtin_amdgcn_sched_barrier(0);
-  load_unit<K, C::IMAX>(u, tr, it0, it1, li, EARLY, C::IMAX);
+  load_unit<K, C::IMAX>(u, tr, it0, it1, li, EARLY, DEPTH);
   // epilogue inputs: read here behind the weights for plain-x launches; under a
   // normalizing prologue registers are too scarce, and they are read at the end
   constexpr bool PRE = MODE == LISA_PRO_LOADX;
@@ -684,6 +691,11 @@ DEV void qmv_body(const LisaQmvParams& p, unsigned char* lds) {
         group_dot2<C::ROWBYTES, C::G, M>(lds, 16 * (it0 + i) + li, u.a0[i], u.b0[i], u.a1[i], u.b1[i], u.s0[i],
                                          u.s1[i], gsum, T0, T1);
       }
+    }
+    if (i + DEPTH < C::IMAX) {
+      __builtin_amdgcn_sched_barrier(0);
+      load_unit<K, C::IMAX>(u, tr, it0, it1, li, i + DEPTH, i + DEPTH + 1);
+      __builtin_amdgcn_sched_barrier(0);
     }
   }
 #pragma unroll
