@@ -20,7 +20,8 @@
  * SB u32[N][K/64] with SB = scale_bf16 | bias_bf16 << 16 (one load per group).
  * One launch covers up to 4 matrices that share the input x; the virtual row
  * space is split into 8-row tiles, each matrix owning a contiguous tile range
- * [tile_start[e], tile_start[e+1]). ksplit is 4 when the launch has at most
+ * [tile_start[e], tile_start[e+1]), tile_start[n_mats] the total.
+ * ksplit is 4 when the launch has at most
  * 8192 virtual rows (the N=5120 projections), else 1: a fixed rule, so the
  * summation order of every output is a function of the launch shape. */
 #define LISA_QMV_MAX_MATS 4

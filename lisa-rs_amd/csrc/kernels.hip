@@ -491,31 +491,70 @@ struct Unit {
 };
 
 struct TileRef {
-  int e;
   uint32_t r0, r1;
   bool v0, v1;
   const uint4 *wp0, *wp1;
   const uint32_t *sp0, *sp1;
+  void* out;
+  uint32_t rows, kind;
 };
 
+// Tile count of a launch, tile_start[n_mats], selected from the entries
+// rather than indexed (an indexed read would wait for n_mats first).
+DEV uint32_t qmv_tiles(const LisaQmvParams& p) {
+  uint32_t t = p.tile_start[0];
+#pragma unroll
+  for (int i = 1; i <= LISA_QMV_MAX_MATS; ++i) t = (uint32_t)i == p.n_mats ? p.tile_start[i] : t;
+  return t;
+}
+
+// The matrix of a tile comes from independent comparisons against the
+// tile_start entries below n_mats, and its fields are selected from all
+// matrices' fields, so the kernel-argument reads form one round trip instead
+// of a chain of dependent ones ahead of the first weight load.
 template <int K>
 DEV TileRef tile_ref(const LisaQmvParams& p, uint32_t tile, int rp) {
   constexpr int G = K / 64;
-  TileRef t;
-  int e = 0;
-  while (e + 1 < (int)p.n_mats && tile >= p.tile_start[e + 1]) ++e;
-  t.e = e;
-  const uint32_t lt = tile - p.tile_start[e];
-  const uint32_t rows = p.mats[e].rows;
-  const uint32_t *w0, *w1, *s0, *s1;
-  if (p.mats[e].kind == LISA_EPI_GATEUP) {
-    t.r0 = t.r1 = lt * 4 + rp;
-    w0 = p.mats[e].w; s0 = p.mats[e].sb; w1 = p.mats[e].w2; s1 = p.mats[e].sb2;
-  } else {
-    t.r0 = lt * 8 + 2 * rp;
-    t.r1 = t.r0 + 1;
-    w0 = w1 = p.mats[e].w; s0 = s1 = p.mats[e].sb;
+  constexpr int NM = LISA_QMV_MAX_MATS;
+  uint32_t ts[NM];
+  const uint32_t* mw[NM];
+  const uint32_t* msb[NM];
+  const uint32_t* mw2[NM];
+  const uint32_t* msb2[NM];
+  void* mout[NM];
+  uint32_t mrows[NM], mkind[NM];
+#pragma unroll
+  for (int i = 0; i < NM; ++i) {
+    ts[i] = p.tile_start[i];
+    mw[i] = p.mats[i].w; msb[i] = p.mats[i].sb; mw2[i] = p.mats[i].w2; msb2[i] = p.mats[i].sb2;
+    mout[i] = p.mats[i].out; mrows[i] = p.mats[i].rows; mkind[i] = p.mats[i].kind;
+    // keeps the compiler from deferring the up-projection reads into a branch
+    asm volatile("" : : "s"(mw2[i]), "s"(msb2[i]), "s"(mout[i]));
   }
+  int e = 0;
+#pragma unroll
+  for (int i = 1; i < NM; ++i) e += ((uint32_t)i < p.n_mats && tile >= ts[i]) ? 1 : 0;
+  uint32_t t0 = ts[0];
+  const uint32_t *w = mw[0], *sb = msb[0], *w2 = mw2[0], *sb2 = msb2[0];
+  void* out = mout[0];
+  uint32_t rows = mrows[0], kind = mkind[0];
+#pragma unroll
+  for (int i = 1; i < NM; ++i) {
+    const bool is = e == i;
+    t0 = is ? ts[i] : t0;
+    w = is ? mw[i] : w; sb = is ? msb[i] : sb; w2 = is ? mw2[i] : w2; sb2 = is ? msb2[i] : sb2;
+    out = is ? mout[i] : out; rows = is ? mrows[i] : rows; kind = is ? mkind[i] : kind;
+  }
+  TileRef t;
+  t.out = out;
+  t.rows = rows;
+  t.kind = kind;
+  const uint32_t lt = tile - t0;
+  const bool pair = kind == LISA_EPI_GATEUP;
+  t.r0 = pair ? lt * 4 + rp : lt * 8 + 2 * rp;
+  t.r1 = pair ? t.r0 : t.r0 + 1;
+  const uint32_t *w0 = w, *s0 = sb;
+  const uint32_t *w1 = pair ? w2 : w, *s1 = pair ? sb2 : sb;
   t.v0 = t.r0 < rows;
   t.v1 = t.r1 < rows;
   const uint32_t c0 = t.v0 ? t.r0 : rows - 1, c1 = t.v1 ? t.r1 : rows - 1;
@@ -609,7 +648,7 @@ struct EpiPre {
 
 template <int M, int EPI>
 DEV void epi_preload(const LisaQmvParams& p, const TileRef& tr, int li, EpiPre<M>& e) {
-  const uint32_t kind = EPI >= 0 ? (uint32_t)EPI : p.mats[tr.e].kind;
+  const uint32_t kind = EPI >= 0 ? (uint32_t)EPI : tr.kind;
   if (kind == LISA_EPI_RESID) {
     const uint32_t r = tr.v1 ? tr.r0 : 0;
 #pragma unroll
@@ -635,13 +674,11 @@ DEV void qmv_body(const LisaQmvParams& p, unsigned char* lds) {
   // wv is wave-uniform: keeping it scalar keeps the matrix lookup on scalar loads
   const int tid = threadIdx.x, lane = tid & 63, wv = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int li = lane & 15, rp = lane >> 4;
-  const uint32_t tiles = p.tile_start[p.n_mats];
+  const uint32_t tiles = qmv_tiles(p);
   const uint32_t tile = C::SPLIT ? blockIdx.x : blockIdx.x * 4 + wv;
   const bool tile_ok = tile < tiles;
   const int it0 = C::SPLIT ? (C::ITER * wv) / 4 : 0;
   const int it1 = C::SPLIT ? (C::ITER * (wv + 1)) / 4 : C::ITER;
-  const TileRef tr = tile_ref<K>(p, tile_ok ? tile : tiles - 1, rp);
-
   ProRaw<WAVEX ? 1 : C::RR> raw;
   uint4 xr[WAVEX ? C::IMAX : 1][M][2];
   // issue order: prologue loads, then the weight stream (the fences keep the
@@ -659,6 +696,7 @@ DEV void qmv_body(const LisaQmvParams& p, unsigned char* lds) {
   if constexpr (WAVEX) wx_load<K, M>(p, it0, it1, lane, xr);
   else pro_load<K, M, MODE, WAVEX ? 1 : C::RR>(p, 0, raw);
   __builtin_amdgcn_sched_barrier(0);
+  const TileRef tr = tile_ref<K>(p, tile_ok ? tile : tiles - 1, rp);
   Unit<C::IMAX> u;
   constexpr int DEPTH = MODE == LISA_PRO_LOADX && !WAVEX ? C::IMAX : (C::IMAX < 2 ? C::IMAX : 2);
   constexpr int EARLY = MODE == LISA_PRO_LOADX ? DEPTH : 1;
@@ -667,12 +705,11 @@ DEV void qmv_body(const LisaQmvParams& p, unsigned char* lds) {
   if constexpr (!WAVEX) qmv_prologue<K, M, MODE, WAVEX ? 1 : C::RR>(p, lds, raw);
   __builtin_amdgcn_sched_barrier(0);
   load_unit<K, C::IMAX>(u, tr, it0, it1, li, EARLY, DEPTH);
-  // epilogue inputs: read here behind the weights for plain-x launches; under a
-  // normalizing prologue registers are too scarce, and they are read at the end
-  constexpr bool PRE = MODE == LISA_PRO_LOADX;
+  // epilogue inputs (residual pair, GDN conv state and taps): read here,
+  // behind the first weights, so the epilogue does not start with a memory
+  // round trip
   EpiPre<M> pre;
-  if constexpr (PRE)
-    if (!C::SPLIT || wv == 0) epi_preload<M, EPI>(p, tr, li, pre);
+  if (!C::SPLIT || wv == 0) epi_preload<M, EPI>(p, tr, li, pre);
 
   float T0[M], T1[M];
 #pragma unroll
@@ -729,10 +766,8 @@ DEV void qmv_body(const LisaQmvParams& p, unsigned char* lds) {
 #pragma unroll
   for (int m = 0; m < M; ++m) { best_v[m] = -INFINITY; best_i[m] = 0xffffffffu; }
 
-  if constexpr (!PRE)
-    if (active) epi_preload<M, EPI>(p, tr, li, pre);
   if (active) {
-    const LisaQ4Mat& mt = p.mats[tr.e];
+    const struct { void* out; uint32_t rows, kind; } mt{tr.out, tr.rows, tr.kind};
     const uint32_t r0 = tr.r0, r1 = tr.r1;
     const bool v0 = tr.v0, v1 = tr.v1;
     switch (EPI >= 0 ? (uint32_t)EPI : mt.kind) {

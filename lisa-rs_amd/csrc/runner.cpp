@@ -374,6 +374,7 @@ struct MatSpec {
 int launch_qmv(LisaRunner* r, int m_rows, uint32_t K, LisaQmvParams& p, const std::vector<MatSpec>& mats) {
   const int ki = k_index(K);
   if (ki < 0) return lisa_fail(LISA_E_ARG, "no q4 kernel for K=%u", K);
+  if (mats.empty() || mats.size() > LISA_QMV_MAX_MATS) return lisa_fail(LISA_E_ARG, "q4 launch of %zu matrices", mats.size());
   if (p.pro_mode > LISA_PRO_PRENORM) return lisa_fail(LISA_E_ARG, "bad q4 prologue mode %u", p.pro_mode);
   LisaFunction* fn = r->qmv[m_rows == 3 ? 1 : 0][ki][p.pro_mode];
   // a launch whose matrices all share one epilogue uses the specialized kernel when there is one
