@@ -80,6 +80,16 @@ DEV float max64(float v) {
 }
 
 DEV float bf2f(uint16_t h) { return lisa_bf16_to_f32(h); }
+
+// A device word every lane needs (the decode position) as a vector load: the
+// index is an opaque zero, so the load is not turned into a scalar load, which
+// would wait behind the argument-block loads and other scalar loads (several
+// dependent round trips). Issue it first; read it with readfirstlane.
+DEV uint32_t vload_u32(const uint32_t* ptr) {
+  int zero;
+  asm volatile("v_mov_b32 %0, 0" : "=v"(zero));
+  return ptr[zero];
+}
 DEV float lo_bf(uint32_t u) { return __uint_as_float(u << 16); }
 DEV float hi_bf(uint32_t u) { return __uint_as_float(u & 0xffff0000u); }
 
@@ -974,6 +984,28 @@ DEV void gdn_body(const LisaGdnParams& p) {
   const int h = blockIdx.x, kh = h / (LISA_GDN_VH / LISA_GDN_KH);
   const int tid = threadIdx.x, v = tid >> 2, q = tid & 3, lane = tid & 63, wave = tid >> 6;
   __shared__ float qn[128], kn[128], ybuf[128], sc[4];
+  // Loads return in issue order within a wave: every row's small inputs go
+  // first (q on wave 0 / k on wave 1 of the key head, the state row's v value,
+  // z and the norm weight; the gate inputs are uniform, scalar loads), then
+  // the 128 B of state this thread owns, so the norms and gates are formed
+  // while the state arrives.
+  float c0[M], c1[M], vval[M], zraw[M], braw[M], araw[M];
+  float nwt = 0.0f;
+#pragma unroll
+  for (int t = 0; t < M; ++t) {
+    const float* co = p.conv_out + (size_t)t * LISA_GDN_CONV_DIM;
+    const float* src = co + (wave == 0 ? 0 : LISA_GDN_KEY_DIM) + kh * 128;
+    c0[t] = 0.0f;
+    c1[t] = 0.0f;
+    if (wave < 2) { c0[t] = src[lane]; c1[t] = src[lane + 64]; }
+    vval[t] = co[2 * LISA_GDN_KEY_DIM + h * 128 + v];
+    zraw[t] = 0.0f;
+    if (tid < 128) zraw[t] = p.z[(size_t)t * LISA_GDN_VALUE_DIM + h * 128 + tid];
+    braw[t] = p.b[(size_t)t * LISA_GDN_VH + h];
+    araw[t] = p.a[(size_t)t * LISA_GDN_VH + h];
+  }
+  if (tid < 128) nwt = bf2f(p.norm_w[tid]);
+  __builtin_amdgcn_sched_barrier(0);
   float* srow = p.state + (size_t)h * 128 * 128 + (size_t)v * 128 + 32 * q;
   float S[32];
 #pragma unroll
@@ -981,35 +1013,35 @@ DEV void gdn_body(const LisaGdnParams& p) {
     const float4 f = reinterpret_cast<const float4*>(srow)[i];
     S[4 * i] = f.x; S[4 * i + 1] = f.y; S[4 * i + 2] = f.z; S[4 * i + 3] = f.w;
   }
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
   for (int t = 0; t < rows; ++t) {
-    const float* co = p.conv_out + (size_t)t * LISA_GDN_CONV_DIM;
-    // every global read of this row is issued here, ahead of the dependent chain
-    const float* src = co + (wave == 0 ? 0 : LISA_GDN_KEY_DIM) + kh * 128;
-    float c0 = 0.0f, c1 = 0.0f;
-    if (wave < 2) { c0 = src[lane]; c1 = src[lane + 64]; }
-    const float vval = co[2 * LISA_GDN_KEY_DIM + h * 128 + v];
     const size_t o = (size_t)t * LISA_GDN_VALUE_DIM + h * 128 + tid;
-    float zraw = 0.0f, nwt = 0.0f;
-    if (tid < 128) { zraw = p.z[o]; nwt = bf2f(p.norm_w[tid]); }
     if (wave < 2) {
       // q (wave 0) / k (wave 1) RMS with tree128, scaled 1/128 and 1/sqrt(128)
       float n0, n1;
-      gdn_qk_norm(c0, c1, wave == 0 ? p.q_scale : p.k_scale, n0, n1);
+      gdn_qk_norm(c0[t], c1[t], wave == 0 ? p.q_scale : p.k_scale, n0, n1);
       float* dst = wave == 0 ? qn : kn;
       dst[lane] = n0;
       dst[lane + 64] = n1;
     } else if (tid == 128) {
-      gdn_gates(p.b[(size_t)t * LISA_GDN_VH + h], p.a[(size_t)t * LISA_GDN_VH + h], p.dt_bias[h], p.a_log[h], sc[0],
-                sc[1]);
+      gdn_gates(braw[t], araw[t], p.dt_bias[h], p.a_log[h], sc[0], sc[1]);
     }
     __syncthreads();
-    const float py = gdn_row_step(S, kn + 32 * q, qn + 32 * q, vval, sc[0], sc[1]);
+    const float py = gdn_row_step(S, kn + 32 * q, qn + 32 * q, vval[t], sc[0], sc[1]);
     if (q == 0) ybuf[v] = lisa_bf16r(py);
     if (p.capture && p.slots && t + 1 < rows) {
       float4* dst = reinterpret_cast<float4*>(p.slots + (size_t)t * p.slot_stride + (size_t)h * 128 * 128 +
                                               (size_t)v * 128 + 32 * q);
 #pragma unroll
       for (int i = 0; i < 8; ++i) dst[i] = make_float4(S[4 * i], S[4 * i + 1], S[4 * i + 2], S[4 * i + 3]);
+    }
+    // the state is final after the last row: its 64 KB per workgroup go out
+    // now and drain while the gated norm runs
+    if (t + 1 == rows) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+        reinterpret_cast<float4*>(srow)[i] = make_float4(S[4 * i], S[4 * i + 1], S[4 * i + 2], S[4 * i + 3]);
     }
     __syncthreads();
     if (wave == 0) {
@@ -1020,14 +1052,11 @@ DEV void gdn_body(const LisaGdnParams& p) {
     __syncthreads();
     if (tid < 128) {
       const float y = ybuf[tid];
-      p.gated[o] = gdn_gated(y, sc[2], nwt, zraw);
+      p.gated[o] = gdn_gated(y, sc[2], nwt, zraw[t]);
       if (p.y_out) p.y_out[o] = y;
     }
-    __syncthreads();
+    if (t + 1 < rows) __syncthreads();
   }
-#pragma unroll
-  for (int i = 0; i < 8; ++i)
-    reinterpret_cast<float4*>(srow)[i] = make_float4(S[4 * i], S[4 * i + 1], S[4 * i + 2], S[4 * i + 3]);
 }
 
 // Prefill over rows, in three launches with the arithmetic of gdn_body:
@@ -1167,6 +1196,12 @@ DEV void rope_sincos(uint32_t pos, int lane, float& s, float& c) {
   lisa_sincosf(angle, &s, &c);
 }
 
+// The same rotation with the lane's inverse frequency kRopeInvFreq[lane % 32]
+// already loaded.
+DEV void rope_sincos_f(uint32_t pos, float inv_freq, float& s, float& c) {
+  lisa_sincosf((float)pos * inv_freq, &s, &c);
+}
+
 DEV void hnr_finish(const float (&raw)[4], const float (&wv)[4], float s, float c, int lane, float out[4]) {
   float v[4], wsum[4];
 #pragma unroll
@@ -1241,22 +1276,29 @@ DEV void slice_pv(const float* pb6, const uint16_t* Vt, int n, int tid, float (&
   }
 }
 
+// Loads return in issue order within a wave, so the partial issues them
+// smallest and most urgent first: the decode position (a vector load, see
+// vload_u32), the raw query heads, the lane's RoPE frequency (constant-index
+// scalar loads: a vector table load is sunk to its first use), the appended
+// rows' raw key and value, and then every K and V row of the slice, clamped
+// below the capacity, before the position is known.
+typedef uint32_t lisa_u32x4 __attribute__((ext_vector_type(4)));
 template <int M>
 DEV void attn_partial_body(const LisaAttnParams& p) {
   constexpr int T = LISA_ATT_SLICE, HD = LISA_ATT_HD, KP = HD + 8;
-  const uint32_t base = *p.pos;
   const int s = blockIdx.x, kvh = blockIdx.y;
   const uint32_t t0 = (uint32_t)s * T;
-  if (t0 >= base + M) return;
   __shared__ __attribute__((aligned(16))) uint16_t Kt[T * KP];
   __shared__ __attribute__((aligned(16))) uint16_t Vt[T * HD];
   __shared__ __attribute__((aligned(16))) float qv[M * 6 * HD];
   __shared__ float pb[M * 6 * T];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const size_t cache_base = (size_t)kvh * p.capacity * HD;
+  const uint32_t pos_v = vload_u32(p.pos);
 
   // 0. the raw query heads of this wave (pairs pr = wave + 4j of row t = pr / 6,
-  // head i = pr % 6), loaded before anything else
+  // head i = pr % 6), the RoPE frequency, and wave t < M: row t's raw key, its
+  // norm weights and raw value
   constexpr int QP = (6 * M + 3) / 4;
   float qraw[QP][4], qw[QP][4];
 #pragma unroll
@@ -1264,45 +1306,54 @@ DEV void attn_partial_body(const LisaAttnParams& p) {
     const int pr = min(wave + 4 * j, 6 * M - 1), t = pr / 6, i = pr % 6;
     hnr_load(p.q_proj + (size_t)t * LISA_ATT_Q_OUT + (kvh * 6 + i) * 512, p.q_norm_w, lane, qraw[j], qw[j]);
   }
-  // 1. rows of the slice already in the cache (positions < base); a full slice
-  // issues all of its loads before the first LDS store
-  const int nold = (base > t0) ? (int)min((uint32_t)T, base - t0) : 0;
-  if (nold == T) {
-    constexpr int R = T * (HD / 8) / 256;
-    uint4 kr[R], vr[R];
+  float inv_freq = 0.0f;
 #pragma unroll
-    for (int i = 0; i < R; ++i) {
-      const int c = tid + 256 * i, row = c / (HD / 8), col = (c % (HD / 8)) * 8;
-      const size_t off = cache_base + (size_t)(t0 + row) * HD + col;
-      kr[i] = *reinterpret_cast<const uint4*>(p.key_cache + off);
-      vr[i] = *reinterpret_cast<const uint4*>(p.value_cache + off);
-    }
+  for (int j = 0; j < LISA_ROPE_PAIRS; ++j) inv_freq = (lane & 31) == j ? kRopeInvFreq[j] : inv_freq;
+  const int wr = min(wave, M - 1);
+  float nkraw[4], nkw[4], nvraw[4];
+  hnr_load(p.k_raw + (size_t)wr * LISA_ATT_KV_OUT + kvh * HD, p.k_norm_w, lane, nkraw, nkw);
 #pragma unroll
-    for (int i = 0; i < R; ++i) {
-      const int c = tid + 256 * i, row = c / (HD / 8), col = (c % (HD / 8)) * 8;
-      *reinterpret_cast<uint4*>(&Kt[row * KP + col]) = kr[i];
-      *reinterpret_cast<uint4*>(&Vt[row * HD + col]) = vr[i];
-    }
-  } else {
-    for (int c = tid; c < nold * (HD / 8); c += 256) {
-      const int row = c / (HD / 8), col = (c % (HD / 8)) * 8;
-      const size_t off = cache_base + (size_t)(t0 + row) * HD + col;
-      *reinterpret_cast<uint4*>(&Kt[row * KP + col]) = *reinterpret_cast<const uint4*>(p.key_cache + off);
-      *reinterpret_cast<uint4*>(&Vt[row * HD + col]) = *reinterpret_cast<const uint4*>(p.value_cache + off);
+  for (int j = 0; j < 4; ++j) nvraw[j] = p.v_raw[(size_t)wr * LISA_ATT_KV_OUT + kvh * HD + lane + 64 * j];
+  __builtin_amdgcn_sched_barrier(0);
+  // 1. every row of the slice (chunk c = tid + 256 i: row c / 32, columns
+  // 8 (c % 32) ..), clamped below the capacity (native vector types: HIP's
+  // uint4 struct copies lower to memcpy, which keeps an array of them out of
+  // registers)
+  constexpr int R = T * (HD / 8) / 256;
+  lisa_u32x4 kr[R], vr[R];
+#pragma unroll
+  for (int i = 0; i < R; ++i) {
+    const int c = tid + 256 * i, row = c / (HD / 8), col = (c % (HD / 8)) * 8;
+    const size_t off = cache_base + (size_t)min(t0 + row, p.capacity - 1) * HD + col;
+    kr[i] = *reinterpret_cast<const lisa_u32x4*>(p.key_cache + off);
+    vr[i] = *reinterpret_cast<const lisa_u32x4*>(p.value_cache + off);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  const uint32_t base = __builtin_amdgcn_readfirstlane(pos_v);
+  if (t0 >= base + M) return;
+  // rows already in the cache (positions < base) go to LDS; the rows this step
+  // appends are written below, later rows lie past every row's context
+#pragma unroll
+  for (int i = 0; i < R; ++i) {
+    const int c = tid + 256 * i, row = c / (HD / 8), col = (c % (HD / 8)) * 8;
+    if (t0 + row < base) {
+      *reinterpret_cast<lisa_u32x4*>(&Kt[row * KP + col]) = kr[i];
+      *reinterpret_cast<lisa_u32x4*>(&Vt[row * HD + col]) = vr[i];
     }
   }
   // 2. rows appended by this step that fall into the slice (kv_cache_store_decode)
   if (wave < M) {
     const uint32_t pos = base + wave;
     if (pos >= t0 && pos < t0 + T && pos < p.capacity) {
-      float kr[4];
-      head_norm_rope_wave(p.k_raw + (size_t)wave * LISA_ATT_KV_OUT + kvh * HD, p.k_norm_w, pos, lane, kr);
+      float kn[4], rs, rc;
+      rope_sincos_f(pos, inv_freq, rs, rc);
+      hnr_finish(nkraw, nkw, rs, rc, lane, kn);
       const int row = (int)(pos - t0);
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const int d = lane + 64 * j;
-        const uint16_t kb = lisa_f32_to_bf16(kr[j]);
-        const uint16_t vb = lisa_f32_to_bf16(p.v_raw[(size_t)wave * LISA_ATT_KV_OUT + kvh * HD + d]);
+        const uint16_t kb = lisa_f32_to_bf16(kn[j]);
+        const uint16_t vb = lisa_f32_to_bf16(nvraw[j]);
         Kt[row * KP + d] = kb;
         Vt[row * HD + d] = vb;
         p.key_cache[cache_base + (size_t)pos * HD + d] = kb;
@@ -1314,7 +1365,7 @@ DEV void attn_partial_body(const LisaAttnParams& p) {
   // rotation per row position)
   float rs[M], rc[M];
 #pragma unroll
-  for (int t = 0; t < M; ++t) rope_sincos(base + t, lane, rs[t], rc[t]);
+  for (int t = 0; t < M; ++t) rope_sincos_f(base + t, inv_freq, rs[t], rc[t]);
 #pragma unroll
   for (int j = 0; j < QP; ++j) {
     const int pr = wave + 4 * j;
@@ -1352,10 +1403,17 @@ DEV void attn_partial_body(const LisaAttnParams& p) {
 }
 
 #define ATT_MAX_SLICES 1024
+// Flash merge of the slice partials of one (head, row) in ascending slice order
+// (attention.metal:611-641): weights w_s = exp2(log2e (m_s - max m)), output
+// (sum w_s o_s) / (sum w_s den_s), both as fma chains; then the output gate.
+// The output gate's input is loaded ahead of the slice statistics, which gate
+// everything else.
 template <int M>
 DEV void attn_merge_body(const LisaAttnParams& p) {
   const int h = blockIdx.x, t = blockIdx.y, tid = threadIdx.x;
-  const uint32_t ctx = *p.pos + t + 1;
+  const uint32_t pos_v = vload_u32(p.pos);
+  const float graw = p.q_proj[(size_t)t * LISA_ATT_Q_OUT + h * 512 + 256 + tid];
+  const uint32_t ctx = __builtin_amdgcn_readfirstlane(pos_v) + t + 1;
   const int used = (int)((ctx + LISA_ATT_SLICE - 1) / LISA_ATT_SLICE);
   __shared__ float ws[ATT_MAX_SLICES], dn[ATT_MAX_SLICES], red[4];
   const float* ml = p.part_ml + ((size_t)t * LISA_ATT_QH + h) * p.s_max * 2;
@@ -1378,7 +1436,7 @@ DEV void attn_merge_body(const LisaAttnParams& p) {
     tot = lisa_fma(ws[s], dn[s], tot);
   }
   const float o = res / tot;
-  const float g = lisa_bf16r(p.q_proj[(size_t)t * LISA_ATT_Q_OUT + h * 512 + 256 + tid]);
+  const float g = lisa_bf16r(graw);
   p.gated[(size_t)t * LISA_ATT_OUT + h * LISA_ATT_HD + tid] = lisa_f32_to_bf16(o * lisa_sigmoid_exp2(g));
 }
 
