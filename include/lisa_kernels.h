@@ -33,8 +33,9 @@ enum {
   LISA_PRO_CAST = 3,    /* r = bf16(o_in); x = RMSNorm(r) */
   LISA_PRO_NORM = 4,    /* r = h_in; x = RMSNorm(r) */
   LISA_PRO_MTPFC = 5,   /* x = [RMSNorm(embed(tok), norm_w) | RMSNorm(x_in, norm_w2)] */
-  LISA_PRO_PRENORM = 6  /* x = RMSNorm(h_in) with the statistic from the producer's tile
-                           partials ss_part[M][640] (residual already added, EPI_RESID) */
+  LISA_PRO_PRENORM = 6  /* x = RMSNorm(h_in) of residual rows an EPI_RESID launch produced;
+                           the statistic sums per-8-row tile partials
+                           ((r0^2+r1^2)+(r2^2+r3^2))+((r4^2+r5^2)+(r6^2+r7^2)) */
 };
 
 enum {
@@ -43,8 +44,7 @@ enum {
   LISA_EPI_CONV = 2,   /* GDN qkv: causal conv + SiLU -> out f32[M][rows], conv state update */
   LISA_EPI_ARGMAX = 3, /* out f32 logits[M][rows] + per-workgroup (max, idx) partials */
   LISA_EPI_RESID = 4   /* rows of the 5120-wide residual: h_in[m][j] <- bf16(h_in[m][j] +
-                          bf16(y)) in place, plus one sum of squares per 8-row tile in
-                          ss_part[m][tile] (for a PRENORM consumer) */
+                          bf16(y)) in place (normalized by a PRENORM consumer) */
 };
 
 typedef struct LisaQ4Mat {
@@ -84,7 +84,6 @@ typedef struct LisaQmvParams {
   uint32_t pro_mode;
   uint32_t capture;
   uint32_t ksplit; /* 1 or 4: waves of a workgroup split K of one tile */
-  float* ss_part;  /* EPI_RESID writes / PRENORM reads: [M][640] tile sums of squares */
 } LisaQmvParams;
 
 /* ---- GDN recurrence + gated RMSNorm --------------------------------------

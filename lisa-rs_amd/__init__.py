@@ -70,8 +70,7 @@ class QmvParams(C.Structure):
                 ("conv_slot_stride", C.c_uint64),
                 ("am_val", C.c_uint64), ("am_idx", C.c_uint64),
                 ("mats", Q4Mat * 4), ("tile_start", C.c_uint32 * 5),
-                ("n_mats", C.c_uint32), ("pro_mode", C.c_uint32), ("capture", C.c_uint32), ("ksplit", C.c_uint32),
-                ("ss_part", C.c_uint64)]
+                ("n_mats", C.c_uint32), ("pro_mode", C.c_uint32), ("capture", C.c_uint32), ("ksplit", C.c_uint32)]
 
 
 class GdnParams(C.Structure):

@@ -284,8 +284,6 @@ DEV void seg_load(const LisaQmvParams& p, int m, ProRaw<R>& raw) {
     raw.w[i] = reinterpret_cast<const uint4*>(nw)[c];
     if constexpr (src == SEG_RESNORM || src == SEG_NORM || src == SEG_PRENORM)
       raw.a[i] = reinterpret_cast<const uint4*>(hsrc)[c];
-    if constexpr (src == SEG_PRENORM)  // this thread's tile partials t, t+256, t+512
-      raw.b[i].x = __float_as_uint(p.ss_part[(size_t)m * kSegChunks + c]);
     if constexpr (src == SEG_RESNORM || src == SEG_CAST) {
       raw.b[i] = reinterpret_cast<const uint4*>(osrc)[2 * c];
       raw.c[i] = reinterpret_cast<const uint4*>(osrc)[2 * c + 1];
@@ -333,8 +331,14 @@ DEV void seg_process(const LisaQmvParams& p, unsigned char* lds, int m, const Pr
       if constexpr (src != SEG_PRENORM)
         if (valid) ss = ss + r * r;
     }
-    if constexpr (src == SEG_PRENORM)
-      if (valid) ss = ss + __uint_as_float(raw.b[i].x);
+    if constexpr (src == SEG_PRENORM) {
+      // the 8-row tile sum of squares of the residual-producing launch,
+      // ((r0^2 + r1^2) + (r2^2 + r3^2)) + ((r4^2 + r5^2) + (r6^2 + r7^2)),
+      // formed here from the chunk's residual values
+      const float part = ((hv[0] * hv[0] + hv[1] * hv[1]) + (hv[2] * hv[2] + hv[3] * hv[3])) +
+                         ((hv[4] * hv[4] + hv[5] * hv[5]) + (hv[6] * hv[6] + hv[7] * hv[7]));
+      if (valid) ss = ss + part;
+    }
   }
   const float inv = seg_rms_inv(ss, red, tid);
   const bool writer = blockIdx.x == 0;
@@ -807,22 +811,16 @@ DEV void qmv_body(const LisaQmvParams& p, unsigned char* lds) {
         break;
       }
       case LISA_EPI_RESID: {
-        // r = bf16(h + bf16(y)) in place; tile partial ((s0 + s1) + (s2 + s3)),
-        // s_rp = r_{2rp}^2 + r_{2rp+1}^2 over the four row-groups (lanes 0, 16, 32, 48)
+        // r = bf16(h + bf16(y)) in place
         uint16_t* hres = const_cast<uint16_t*>(p.h_in);  // read-write for this epilogue
 #pragma unroll
         for (int m = 0; m < M; ++m) {
-          float ra = 0.0f, rb = 0.0f;
           if (li == 0 && v0 && v1) {
-            ra = lisa_bf16r(lo_bf(pre.h[m]) + lisa_bf16r(T0[m]));
-            rb = lisa_bf16r(hi_bf(pre.h[m]) + lisa_bf16r(T1[m]));
+            const float ra = lisa_bf16r(lo_bf(pre.h[m]) + lisa_bf16r(T0[m]));
+            const float rb = lisa_bf16r(hi_bf(pre.h[m]) + lisa_bf16r(T1[m]));
             hres[(size_t)m * LISA_HIDDEN + r0] = lisa_f32_to_bf16(ra);
             hres[(size_t)m * LISA_HIDDEN + r1] = lisa_f32_to_bf16(rb);
           }
-          float sq = ra * ra + rb * rb;
-          sq = sq + xor_lane<16>(sq);
-          sq = sq + xor_lane<32>(sq);
-          if (lane == 0) p.ss_part[(size_t)m * (LISA_HIDDEN / 8) + tr.r0 / 8] = sq;
         }
         break;
       }

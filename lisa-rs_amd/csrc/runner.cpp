@@ -62,7 +62,6 @@ struct MtpDev {
 struct Ctx {
   int rows = 1;
   uint16_t *H, *gated, *act, *xnorm, *cond;  // H: residual rows, updated in place
-  float* ss;  // tile sums of squares of the residual rows [rows][640]
   float *B, *conv_out, *z, *a, *b, *q_proj, *k_raw, *v_raw, *part_o, *part_ml, *logits, *am_val;
   uint32_t *am_idx, *tokens, *argmax, *pos, *step, *history;
 };
@@ -337,7 +336,6 @@ void plan_state(LisaRunner* r, Arena& A) {
 void plan_ctx(LisaRunner* r, Arena& A, Ctx& c, int rows) {
   c.rows = rows;
   c.H = A.take<uint16_t>((size_t)3 * LISA_HIDDEN);
-  c.ss = A.take<float>((size_t)rows * (LISA_HIDDEN / 8));
   c.B = A.take<float>((size_t)rows * LISA_HIDDEN);
   c.conv_out = A.take<float>((size_t)rows * LISA_GDN_CONV_DIM);
   c.z = A.take<float>((size_t)rows * LISA_GDN_VALUE_DIM);
@@ -409,25 +407,23 @@ int launch_qmv(LisaRunner* r, int m_rows, uint32_t K, LisaQmvParams& p, const st
   return lisa_launch(r->dev, fn, &p, sizeof p, grid, 1, 1, 256, 1, 1);
 }
 
-// Consumer of the residual rows: x = RMSNorm(c.H) from the tile partials the
-// producing launch left in c.ss.
+// Consumer of the residual rows: x = RMSNorm(c.H), the statistic from 8-row
+// tile partials of the updated rows.
 LisaQmvParams pro_prenorm(Ctx& c, const uint16_t* w) {
   LisaQmvParams p{};
   p.pro_mode = LISA_PRO_PRENORM;
   p.h_in = c.H;
-  p.ss_part = c.ss;
   p.norm_w = w;
   return p;
 }
 
 // Producer of the residual rows: c.H += y (bf16 residual add, runner.rs
-// encode_residual), tile partials into c.ss.
+// encode_residual).
 int launch_resid(LisaRunner* r, Ctx& c, int m, uint32_t K, const uint16_t* x, const Q4Dev& w) {
   LisaQmvParams p{};
   p.pro_mode = LISA_PRO_LOADX;
   p.x_in = x;
   p.h_in = c.H;
-  p.ss_part = c.ss;
   return launch_qmv(r, m, K, p, {{&w, nullptr, nullptr, LISA_EPI_RESID}});
 }
 

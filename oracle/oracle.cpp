@@ -716,8 +716,8 @@ static void embed_rows(const OrcModel* M, const uint32_t* tokens, int m, std::ve
   }
 }
 
-// tiles: the statistic comes from the residual-add launch's tile partials
-// (every decode-path norm except the one after the embedding).
+// tiles: the statistic is summed from per-8-row tile partials of the residual
+// rows (every decode-path norm except the one after the embedding).
 static void norm_rows(const std::vector<float>& h, int m, const std::vector<uint16_t>& w,
                       std::vector<XPrep>& xp, std::vector<uint16_t>* keep = nullptr, bool tiles = false) {
   xp.resize(m);

@@ -160,9 +160,9 @@ def test_qmv_resnorm_gateup(pkg, orc, dev, M):
 @pytest.mark.parametrize("M", [1, 3])
 def test_qmv_resid_then_prenorm_gateup(pkg, orc, dev, M):
     """The decode path's split residual: an out_proj-shaped launch (K=6144)
-    adds its rows into the residual in place and leaves per-tile sums of
-    squares; the gate/up launch normalizes from those partials
-    (norm.metal:10-57 statistic, mlp.metal:6-17)."""
+    adds its rows into the residual in place; the gate/up launch normalizes
+    the updated rows with the per-8-row tile statistic (norm.metal:10-57,
+    mlp.metal:6-17)."""
     rng = np.random.default_rng(70 + M)
     K, H, N = 6144, 5120, 17408
     ow, osc, ob = rand_q4(rng, H, K)
@@ -172,10 +172,9 @@ def test_qmv_resid_then_prenorm_gateup(pkg, orc, dev, M):
     h = bf16((rng.standard_normal((M, H)) * 4).astype(np.float32))
     nw = bf16(rng.uniform(0.9, 1.1, H).astype(np.float32))
     xb, hb, nb = dev.upload(x), dev.upload(h), dev.upload(nw)
-    ss = dev.buffer(M * (H // 8) * 4)
     p = pkg.QmvParams()
     p.pro_mode = pkg.PRO_LOADX
-    p.x_in, p.h_in, p.ss_part = xb.ptr, hb.ptr, ss.ptr
+    p.x_in, p.h_in = xb.ptr, hb.ptr
     ks, _ = launch_qmv(pkg, dev, K, M, p, [(DevQ4(dev, ow, osc, ob), None, 0, pkg.EPI_RESID)])
     y = orc.q4_linear(x, ow, osc, ob, H, K, M, ks)
     r = np.stack([orc.residual(h[m], y[m]) for m in range(M)])
@@ -183,7 +182,7 @@ def test_qmv_resid_then_prenorm_gateup(pkg, orc, dev, M):
     act, xo = dev.buffer(M * N * 2), dev.buffer(M * H * 2)
     q = pkg.QmvParams()
     q.pro_mode = pkg.PRO_PRENORM
-    q.h_in, q.ss_part, q.norm_w, q.x_out = hb.ptr, ss.ptr, nb.ptr, xo.ptr
+    q.h_in, q.norm_w, q.x_out = hb.ptr, nb.ptr, xo.ptr
     ks2, _ = launch_qmv(pkg, dev, H, M, q, [(DevQ4(dev, gw, gs, gb), DevQ4(dev, uw, us, ub), act.ptr, pkg.EPI_GATEUP)])
     xn = np.stack([orc.rms_norm_tiles(r[m], nw) for m in range(M)])
     assert np.array_equal(xo.read(np.uint16, M * H).reshape(M, H), xn)
