@@ -781,6 +781,16 @@ DEV void qmv_body(const LisaQmvParams& p, unsigned char* lds) {
   for (int m = 0; m < M; ++m) { best_v[m] = -INFINITY; best_i[m] = 0xffffffffu; }
 
   if (active) {
+    // the preloaded epilogue inputs are first used here: without this, their
+    // conversions are hoisted to the loads and the wave waits for its whole
+    // weight stream right after issuing it
+    if (EPI < 0 || EPI == LISA_EPI_RESID || EPI == LISA_EPI_CONV) {
+#pragma unroll
+      for (int m = 0; m < M; ++m) asm volatile("" : "+v"(pre.h[m]));
+#pragma unroll
+      for (int i = 0; i < 3; ++i) asm volatile("" : "+v"(pre.cs[i]));
+      asm volatile("" : "+v"(pre.cw.x), "+v"(pre.cw.y));
+    }
     const struct { void* out; uint32_t rows, kind; } mt{tr.out, tr.rows, tr.kind};
     const uint32_t r0 = tr.r0, r1 = tr.r1;
     const bool v0 = tr.v0, v1 = tr.v1;
