@@ -332,9 +332,9 @@ DEV void seg_process(const LisaQmvParams& p, unsigned char* lds, int m, const Pr
         if (valid) ss = ss + r * r;
     }
     if constexpr (src == SEG_PRENORM) {
-      // the 8-row tile sum of squares of the residual-producing launch,
+      // the 8-row tile sum of squares of the residual rows,
       // ((r0^2 + r1^2) + (r2^2 + r3^2)) + ((r4^2 + r5^2) + (r6^2 + r7^2)),
-      // formed here from the chunk's residual values
+      // formed from the chunk's residual values this prologue already holds
       const float part = ((hv[0] * hv[0] + hv[1] * hv[1]) + (hv[2] * hv[2] + hv[3] * hv[3])) +
                          ((hv[4] * hv[4] + hv[5] * hv[5]) + (hv[6] * hv[6] + hv[7] * hv[7]));
       if (valid) ss = ss + part;

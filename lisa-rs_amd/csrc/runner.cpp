@@ -10,8 +10,8 @@
 //                       qmv[o_proj + residual add]
 //   every layer       : qmv[post RMSNorm -> gate/up -> SwiGLU];  qmv[down + residual add]
 //   final             : qmv[final RMSNorm -> lm_head -> argmax partials];  step_finalize
-// A residual-add epilogue updates the residual rows in place and leaves one
-// sum of squares per 8-row tile; the next launch's RMSNorm prologue sums those.
+// A residual-add epilogue updates the residual rows in place; the next launch's
+// RMSNorm prologue forms the sum of squares from the residual rows it reads.
 // 5 launches per GDN layer, 6 per attention layer, 2 final (338 for 64 layers)
 // against the reference's 852 dispatches (runner.rs:568-582, 1248-1592).
 #include <hip/hip_runtime.h>
