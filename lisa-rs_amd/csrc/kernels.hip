@@ -926,7 +926,9 @@ QMV_KERNEL_EPI(5120, 3, LISA_PRO_PRENORM, prenorm, LISA_EPI_ARGMAX, argmax)
 // ===========================================================================
 // GDN recurrence (gdn.metal:245-328) + gates (gdn.metal:170-205) + gated
 // RMSNorm (gdn.metal:367-391). One workgroup per value head, 512 threads:
-// thread (v, q) = (tid/4, tid%4) owns state row v, columns [32q, 32q+32).
+// thread (v, q) = (tid/4, tid%4) owns 32 elements of state row v: the quarter
+// [32q, 32q+32) in the prefill scan, the runs q, q+4, q+8, q+12 of 8 in the
+// decode step (gdn_row_step_il).
 // ===========================================================================
 // M = 0: the row count comes from p.m_rows (prefill).
 // q or k of one key head (gdn.metal q/k norm): RMS over 128 values as tree64 of
@@ -979,6 +981,42 @@ DEV float gdn_row_step(float (&S)[32], const float* kq, const float* qq, float v
   return py;
 }
 
+// The same time step with the row's sixteen runs of 8 interleaved over its four
+// lanes: lane q owns runs q, q+4, q+8, q+12, S[8j + e] = element 8(q + 4j) + e,
+// so in each 16-byte load or store the four lanes of a row touch one 128-byte
+// line (with quarters of 32 contiguous per lane they touch four). kq and qq
+// point at element 8q. Every run is the same ascending fma chain of 8; quarter
+// j (runs 4j..4j+3, one on each lane) is (r0 + r1) + (r2 + r3) by xor 1, 2, and
+// the row is (Q0 + Q1) + (Q2 + Q3): the sums of gdn_dot32 and its xor 1, 2
+// steps, bit for bit.
+DEV float gdn_dot_il(const float (&S)[32], const float* vec) {
+  float Q[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    float r = S[8 * j] * vec[32 * j];
+#pragma unroll
+    for (int e = 1; e < 8; ++e) r = lisa_fma(S[8 * j + e], vec[32 * j + e], r);
+    r = r + xor_lane<1>(r);
+    Q[j] = r + xor_lane<2>(r);
+  }
+  return (Q[0] + Q[1]) + (Q[2] + Q[3]);
+}
+
+DEV float gdn_row_step_il(float (&S)[32], const float* kq, const float* qq, float vval, float beta, float decay) {
+#pragma unroll
+  for (int k = 0; k < 32; ++k) S[k] = S[k] * decay;
+  const float pk = gdn_dot_il(S, kq);
+  const float delta = (vval - pk) * beta;
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) S[8 * j + e] = lisa_fma(delta, kq[32 * j + e], S[8 * j + e]);
+  return gdn_dot_il(S, qq);
+}
+
+// Element offset of the lane's 16-byte chunk i (0..7) of its state row.
+DEV int gdn_il_chunk(int q, int i) { return 8 * q + 32 * (i >> 1) + 4 * (i & 1); }
+
 // Gated RMSNorm output of one element: bf16(bf16(y rinv w) silu(bf16 z)).
 DEV uint16_t gdn_gated(float y, float rinv, float nw, float zraw) {
   const float n = lisa_bf16r((y * rinv) * nw);
@@ -1014,11 +1052,11 @@ DEV void gdn_body(const LisaGdnParams& p) {
   }
   if (tid < 128) nwt = bf2f(p.norm_w[tid]);
   __builtin_amdgcn_sched_barrier(0);
-  float* srow = p.state + (size_t)h * 128 * 128 + (size_t)v * 128 + 32 * q;
+  float* srow = p.state + (size_t)h * 128 * 128 + (size_t)v * 128;
   float S[32];
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
-    const float4 f = reinterpret_cast<const float4*>(srow)[i];
+    const float4 f = *reinterpret_cast<const float4*>(srow + gdn_il_chunk(q, i));
     S[4 * i] = f.x; S[4 * i + 1] = f.y; S[4 * i + 2] = f.z; S[4 * i + 3] = f.w;
   }
   __builtin_amdgcn_sched_barrier(0);
@@ -1036,20 +1074,20 @@ DEV void gdn_body(const LisaGdnParams& p) {
       gdn_gates(braw[t], araw[t], p.dt_bias[h], p.a_log[h], sc[0], sc[1]);
     }
     __syncthreads();
-    const float py = gdn_row_step(S, kn + 32 * q, qn + 32 * q, vval[t], sc[0], sc[1]);
+    const float py = gdn_row_step_il(S, kn + 8 * q, qn + 8 * q, vval[t], sc[0], sc[1]);
     if (q == 0) ybuf[v] = lisa_bf16r(py);
     if (p.capture && p.slots && t + 1 < rows) {
-      float4* dst = reinterpret_cast<float4*>(p.slots + (size_t)t * p.slot_stride + (size_t)h * 128 * 128 +
-                                              (size_t)v * 128 + 32 * q);
+      float* dst = p.slots + (size_t)t * p.slot_stride + (size_t)h * 128 * 128 + (size_t)v * 128;
 #pragma unroll
-      for (int i = 0; i < 8; ++i) dst[i] = make_float4(S[4 * i], S[4 * i + 1], S[4 * i + 2], S[4 * i + 3]);
+      for (int i = 0; i < 8; ++i)
+        *reinterpret_cast<float4*>(dst + gdn_il_chunk(q, i)) = make_float4(S[4 * i], S[4 * i + 1], S[4 * i + 2], S[4 * i + 3]);
     }
     // the state is final after the last row: its 64 KB per workgroup go out
     // now and drain while the gated norm runs
     if (t + 1 == rows) {
 #pragma unroll
       for (int i = 0; i < 8; ++i)
-        reinterpret_cast<float4*>(srow)[i] = make_float4(S[4 * i], S[4 * i + 1], S[4 * i + 2], S[4 * i + 3]);
+        *reinterpret_cast<float4*>(srow + gdn_il_chunk(q, i)) = make_float4(S[4 * i], S[4 * i + 1], S[4 * i + 2], S[4 * i + 3]);
     }
     __syncthreads();
     if (wave == 0) {
