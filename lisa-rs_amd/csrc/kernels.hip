@@ -1322,12 +1322,76 @@ DEV void slice_pv(const float* pb6, const uint16_t* Vt, int n, int tid, float (&
   }
 }
 
+// Scores of one row for two heads a, b of the same KV head over a slice (lane =
+// token): each K chunk is read and widened once for both heads; per head the
+// four accumulators over d mod 4 and every later step are those of
+// slice_scores.
+DEV void slice_scores2(const float* qa, const float* qb, const uint16_t* Kt, int kp, int n, int lane,
+                       float* pba, float* pbb, float* mla, float* mlb) {
+  float sa = -INFINITY, sb = -INFINITY;
+  if (lane < n) {
+    const uint16_t* kr = Kt + lane * kp;
+    float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
+    float b0 = 0.0f, b1 = 0.0f, b2 = 0.0f, b3 = 0.0f;
+#pragma unroll 2
+    for (int d = 0; d < LISA_ATT_HD; d += 8) {
+      const uint4 kk = *reinterpret_cast<const uint4*>(kr + d);
+      const float4 xa = *reinterpret_cast<const float4*>(qa + d);
+      const float4 ya = *reinterpret_cast<const float4*>(qa + d + 4);
+      const float4 xb = *reinterpret_cast<const float4*>(qb + d);
+      const float4 yb = *reinterpret_cast<const float4*>(qb + d + 4);
+      const float k0 = lo_bf(kk.x), k1 = hi_bf(kk.x), k2 = lo_bf(kk.y), k3 = hi_bf(kk.y);
+      const float k4 = lo_bf(kk.z), k5 = hi_bf(kk.z), k6 = lo_bf(kk.w), k7 = hi_bf(kk.w);
+      a0 = lisa_fma(xa.x, k0, a0); a1 = lisa_fma(xa.y, k1, a1); a2 = lisa_fma(xa.z, k2, a2); a3 = lisa_fma(xa.w, k3, a3);
+      b0 = lisa_fma(xb.x, k0, b0); b1 = lisa_fma(xb.y, k1, b1); b2 = lisa_fma(xb.z, k2, b2); b3 = lisa_fma(xb.w, k3, b3);
+      a0 = lisa_fma(ya.x, k4, a0); a1 = lisa_fma(ya.y, k5, a1); a2 = lisa_fma(ya.z, k6, a2); a3 = lisa_fma(ya.w, k7, a3);
+      b0 = lisa_fma(yb.x, k4, b0); b1 = lisa_fma(yb.y, k5, b1); b2 = lisa_fma(yb.z, k6, b2); b3 = lisa_fma(yb.w, k7, b3);
+    }
+    sa = ((a0 + a1) + (a2 + a3)) * 0.0625f;
+    sb = ((b0 + b1) + (b2 + b3)) * 0.0625f;
+  }
+  const float ma = max64(sa), mb = max64(sb);
+  const float pa = (lane < n) ? lisa_exp2f(1.4426950408889634f * (sa - ma)) : 0.0f;
+  const float pbv = (lane < n) ? lisa_exp2f(1.4426950408889634f * (sb - mb)) : 0.0f;
+  const float da = tree64(pa), db = tree64(pbv);
+  pba[lane] = pa;
+  pbb[lane] = pbv;
+  if (lane == 0) {
+    mla[0] = ma;
+    mla[1] = da;
+    mlb[0] = mb;
+    mlb[1] = db;
+  }
+}
+
+// P.V of one row over the slice for three heads (rows of pb3 T apart) and the
+// two output dimensions 2dp, 2dp+1: one 32-bit V read per token serves six
+// chains, each the ascending token chain of slice_pv.
+DEV void slice_pv3(const float* pb3, const uint16_t* Vt, int n, int dp, float (&acc)[3][2]) {
+#pragma unroll
+  for (int i = 0; i < 3; ++i) acc[i][0] = acc[i][1] = 0.0f;
+#pragma unroll 4
+  for (int tok = 0; tok < n; ++tok) {
+    const uint32_t vw = *reinterpret_cast<const uint32_t*>(Vt + tok * LISA_ATT_HD + 2 * dp);
+    const float v0 = lo_bf(vw), v1 = hi_bf(vw);
+#pragma unroll
+    for (int i = 0; i < 3; ++i) {
+      const float pv = pb3[i * LISA_ATT_SLICE + tok];
+      acc[i][0] = lisa_fma(pv, v0, acc[i][0]);
+      acc[i][1] = lisa_fma(pv, v1, acc[i][1]);
+    }
+  }
+}
+
 // Loads return in issue order within a wave, so the partial issues them
 // smallest and most urgent first: the decode position (a vector load, see
 // vload_u32), the raw query heads, the lane's RoPE frequency (constant-index
 // scalar loads: a vector table load is sunk to its first use), the appended
 // rows' raw key and value, and then every K and V row of the slice, clamped
-// below the capacity, before the position is known.
+// below the capacity, before the position is known. The queries are normalized
+// and rotated, and the appended rows written, while the slice is in flight.
+// Scores: one wave per pair of heads; P.V: thread (dp, hg) = (tid % 128,
+// tid / 128) owns dimensions 2dp, 2dp+1 of heads 3hg..3hg+2.
 typedef uint32_t lisa_u32x4 __attribute__((ext_vector_type(4)));
 template <int M>
 DEV void attn_partial_body(const LisaAttnParams& p) {
@@ -1337,7 +1401,7 @@ DEV void attn_partial_body(const LisaAttnParams& p) {
   __shared__ __attribute__((aligned(16))) uint16_t Kt[T * KP];
   __shared__ __attribute__((aligned(16))) uint16_t Vt[T * HD];
   __shared__ __attribute__((aligned(16))) float qv[M * 6 * HD];
-  __shared__ float pb[M * 6 * T];
+  __shared__ __attribute__((aligned(16))) float pb[M * 6 * T];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const size_t cache_base = (size_t)kvh * p.capacity * HD;
   const uint32_t pos_v = vload_u32(p.pos);
@@ -1377,37 +1441,7 @@ DEV void attn_partial_body(const LisaAttnParams& p) {
   __builtin_amdgcn_sched_barrier(0);
   const uint32_t base = __builtin_amdgcn_readfirstlane(pos_v);
   if (t0 >= base + M) return;
-  // rows already in the cache (positions < base) go to LDS; the rows this step
-  // appends are written below, later rows lie past every row's context
-#pragma unroll
-  for (int i = 0; i < R; ++i) {
-    const int c = tid + 256 * i, row = c / (HD / 8), col = (c % (HD / 8)) * 8;
-    if (t0 + row < base) {
-      *reinterpret_cast<lisa_u32x4*>(&Kt[row * KP + col]) = kr[i];
-      *reinterpret_cast<lisa_u32x4*>(&Vt[row * HD + col]) = vr[i];
-    }
-  }
-  // 2. rows appended by this step that fall into the slice (kv_cache_store_decode)
-  if (wave < M) {
-    const uint32_t pos = base + wave;
-    if (pos >= t0 && pos < t0 + T && pos < p.capacity) {
-      float kn[4], rs, rc;
-      rope_sincos_f(pos, inv_freq, rs, rc);
-      hnr_finish(nkraw, nkw, rs, rc, lane, kn);
-      const int row = (int)(pos - t0);
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int d = lane + 64 * j;
-        const uint16_t kb = lisa_f32_to_bf16(kn[j]);
-        const uint16_t vb = lisa_f32_to_bf16(nvraw[j]);
-        Kt[row * KP + d] = kb;
-        Vt[row * HD + d] = vb;
-        p.key_cache[cache_base + (size_t)pos * HD + d] = kb;
-        p.value_cache[cache_base + (size_t)pos * HD + d] = vb;
-      }
-    }
-  }
-  // 3. normalized, rotated queries of the 6 heads sharing this KV head (one
+  // 2. normalized, rotated queries of the 6 heads sharing this KV head (one
   // rotation per row position)
   float rs[M], rc[M];
 #pragma unroll
@@ -1422,28 +1456,63 @@ DEV void attn_partial_body(const LisaAttnParams& p) {
 #pragma unroll
     for (int e = 0; e < 4; ++e) qv[(t * 6 + i) * HD + lane + 64 * e] = qo[e];
   }
+  // 3. rows appended by this step that fall into the slice (kv_cache_store_decode)
+  if (wave < M) {
+    const uint32_t pos = base + wave;
+    if (pos >= t0 && pos < t0 + T && pos < p.capacity) {
+      float kn[4];
+      hnr_finish(nkraw, nkw, rs[wave], rc[wave], lane, kn);
+      const int row = (int)(pos - t0);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int d = lane + 64 * j;
+        const uint16_t kb = lisa_f32_to_bf16(kn[j]);
+        const uint16_t vb = lisa_f32_to_bf16(nvraw[j]);
+        Kt[row * KP + d] = kb;
+        Vt[row * HD + d] = vb;
+        p.key_cache[cache_base + (size_t)pos * HD + d] = kb;
+        p.value_cache[cache_base + (size_t)pos * HD + d] = vb;
+      }
+    }
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  // 4. rows already in the cache (positions < base) go to LDS; later rows lie
+  // past every row's context
+#pragma unroll
+  for (int i = 0; i < R; ++i) {
+    const int c = tid + 256 * i, row = c / (HD / 8), col = (c % (HD / 8)) * 8;
+    if (t0 + row < base) {
+      *reinterpret_cast<lisa_u32x4*>(&Kt[row * KP + col]) = kr[i];
+      *reinterpret_cast<lisa_u32x4*>(&Vt[row * HD + col]) = vr[i];
+    }
+  }
   __syncthreads();
-  // 4. scores and slice softmax statistics: lane = token of the slice
-  for (int pr = wave; pr < 6 * M; pr += 4) {
-    const int t = pr / 6, i = pr % 6, h = kvh * 6 + i;
+  // 5. scores and slice softmax statistics: item (row t, head pair k) per wave,
+  // lane = token of the slice
+  for (int it = wave; it < 3 * M; it += 4) {
+    const int t = it / 3, i = 2 * (it % 3), h = kvh * 6 + i;
     const uint32_t ctx = base + t + 1;
     if (ctx <= t0) continue;
     const int n = (int)min((uint32_t)T, ctx - t0);
-    slice_scores(qv + (t * 6 + i) * HD, Kt, KP, n, lane, pb + (t * 6 + i) * T,
-                 p.part_ml + (((size_t)t * LISA_ATT_QH + h) * p.s_max + s) * 2);
+    const float* qa = qv + (t * 6 + i) * HD;
+    float* ml = p.part_ml + (((size_t)t * LISA_ATT_QH + h) * p.s_max + s) * 2;
+    slice_scores2(qa, qa + HD, Kt, KP, n, lane, pb + (t * 6 + i) * T, pb + (t * 6 + i + 1) * T, ml,
+                  ml + (size_t)p.s_max * 2);
   }
   __syncthreads();
-  // 5. P.V: thread = output dimension
+  // 6. P.V
+  const int dp = tid & 127, hg = tid >> 7;
   for (int t = 0; t < M; ++t) {
     const uint32_t ctx = base + t + 1;
     if (ctx <= t0) continue;
     const int n = (int)min((uint32_t)T, ctx - t0);
-    float acc[6];
-    slice_pv(pb + t * 6 * T, Vt, n, tid, acc);
+    float acc[3][2];
+    slice_pv3(pb + (t * 6 + 3 * hg) * T, Vt, n, dp, acc);
 #pragma unroll
-    for (int i = 0; i < 6; ++i) {
-      const int h = kvh * 6 + i;
-      p.part_o[(((size_t)t * LISA_ATT_QH + h) * p.s_max + s) * HD + tid] = acc[i];
+    for (int i = 0; i < 3; ++i) {
+      const int h = kvh * 6 + 3 * hg + i;
+      *reinterpret_cast<float2*>(p.part_o + (((size_t)t * LISA_ATT_QH + h) * p.s_max + s) * HD + 2 * dp) =
+          make_float2(acc[i][0], acc[i][1]);
     }
   }
 }
@@ -1452,31 +1521,39 @@ DEV void attn_partial_body(const LisaAttnParams& p) {
 // Flash merge of the slice partials of one (head, row) in ascending slice order
 // (attention.metal:611-641): weights w_s = exp2(log2e (m_s - max m)), output
 // (sum w_s o_s) / (sum w_s den_s), both as fma chains; then the output gate.
-// The output gate's input is loaded ahead of the slice statistics, which gate
-// everything else.
+// The output gate's input and the statistics of the first 256 slices (index
+// clamped to the allocated s_max slices) are loaded before the position is
+// known, so the statistics do not wait for it.
 template <int M>
 DEV void attn_merge_body(const LisaAttnParams& p) {
   const int h = blockIdx.x, t = blockIdx.y, tid = threadIdx.x;
   const uint32_t pos_v = vload_u32(p.pos);
   const float graw = p.q_proj[(size_t)t * LISA_ATT_Q_OUT + h * 512 + 256 + tid];
-  const uint32_t ctx = __builtin_amdgcn_readfirstlane(pos_v) + t + 1;
-  const int used = (int)((ctx + LISA_ATT_SLICE - 1) / LISA_ATT_SLICE);
   __shared__ float ws[ATT_MAX_SLICES], dn[ATT_MAX_SLICES], red[4];
   const float* ml = p.part_ml + ((size_t)t * LISA_ATT_QH + h) * p.s_max * 2;
-  float mx = -INFINITY;
-  for (int s = tid; s < used; s += 256) mx = fmaxf(mx, ml[2 * s]);
+  const int s0 = min(tid, (int)p.s_max - 1);
+  const float m0 = ml[2 * s0], d0 = ml[2 * s0 + 1];
+  __builtin_amdgcn_sched_barrier(0);
+  const uint32_t ctx = __builtin_amdgcn_readfirstlane(pos_v) + t + 1;
+  const int used = (int)((ctx + LISA_ATT_SLICE - 1) / LISA_ATT_SLICE);
+  float mx = tid < used ? m0 : -INFINITY;
+  for (int s = tid + 256; s < used; s += 256) mx = fmaxf(mx, ml[2 * s]);
   mx = max64(mx);
   if ((tid & 63) == 0) red[tid >> 6] = mx;
   __syncthreads();
   const float gmax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-  for (int s = tid; s < used; s += 256) {
+  if (tid < used) {
+    ws[tid] = lisa_exp2f(1.4426950408889634f * (m0 - gmax));
+    dn[tid] = d0;
+  }
+  for (int s = tid + 256; s < used; s += 256) {
     ws[s] = lisa_exp2f(1.4426950408889634f * (ml[2 * s] - gmax));
     dn[s] = ml[2 * s + 1];
   }
   __syncthreads();
   const float* po = p.part_o + ((size_t)t * LISA_ATT_QH + h) * p.s_max * LISA_ATT_HD + tid;
   float res = 0.0f, tot = 0.0f;
-#pragma unroll 16
+#pragma unroll 32
   for (int s = 0; s < used; ++s) {
     res = lisa_fma(ws[s], po[(size_t)s * LISA_ATT_HD], res);
     tot = lisa_fma(ws[s], dn[s], tot);
