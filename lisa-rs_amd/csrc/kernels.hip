@@ -1108,10 +1108,12 @@ DEV void gdn_body(const LisaGdnParams& p) {
 // Prefill over rows, in three launches with the arithmetic of gdn_body:
 // lisa_gdn_prep_rows (grid (m, 9) x 256): normalized q and k of every row and
 //   key head into qk [m][2][2048], beta and decay into gates [m][48][2];
-// lisa_gdn_scan_rows (grid (48, 2) x 256, 64 state rows per workgroup): the
+// lisa_gdn_scan_rows (grid (48, 4) x 128, 32 state rows per workgroup): the
 //   sequential delta-rule scan, with no barrier in the time loop (each state
-//   row only needs the precomputed inputs), one wave per SIMD, each row's
-//   inputs loaded eight rows ahead;
+//   row only needs the precomputed inputs), each row's inputs loaded eight
+//   rows ahead. A step is bound by the LDS bytes that bring every thread its
+//   32 k and 32 q values (1 KB per state row), so four workgroups per head on
+//   192 CUs take half the time per step of two on 96;
 //   readout y (bf16 values) into y_out [m][6144];
 // lisa_gdn_out_rows (grid (m, 48) x 128): gated RMSNorm of y into gated.
 extern "C" __global__ __launch_bounds__(256) void lisa_gdn_prep_rows(LisaGdnParams p) {
@@ -1153,13 +1155,13 @@ DEV void gdn_row_load(const LisaGdnParams& p, int t, int h, int kh, int v, int l
   in.v = p.conv_out[(size_t)t * LISA_GDN_CONV_DIM + 2 * LISA_GDN_KEY_DIM + h * 128 + v];
 }
 
-extern "C" __global__ __launch_bounds__(256) void lisa_gdn_scan_rows(LisaGdnParams p) {
+extern "C" __global__ __launch_bounds__(128) void lisa_gdn_scan_rows(LisaGdnParams p) {
   const int rows = (int)p.m_rows;
   const int h = blockIdx.x, kh = h / (LISA_GDN_VH / LISA_GDN_KH);
-  const int tid = threadIdx.x, v = blockIdx.y * 64 + (tid >> 2), q = tid & 3, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, v = blockIdx.y * 32 + (tid >> 2), q = tid & 3, lane = tid & 63, wave = tid >> 6;
   // each wave stages the row's k and q in its own LDS slot (a wave reads only
   // what it wrote, so no workgroup barrier is needed)
-  __shared__ lisa_f32x4 kqs[4][64];
+  __shared__ lisa_f32x4 kqs[2][64];
   float* srow = p.state + (size_t)h * 128 * 128 + (size_t)v * 128 + 32 * q;
   float S[32];
 #pragma unroll
@@ -1276,56 +1278,11 @@ DEV void head_norm_rope_wave(const float* raw, const uint16_t* w, uint32_t pos, 
   hnr_finish(v, wv, s, c, lane, out);
 }
 
-// Scores of one (row, head) over a slice of n cached tokens by one wave (lane =
-// token): q.k with four accumulators over d mod 8 pairs, /16, slice max,
-// p = exp2(log2e (score - max)), denominator tree64 (attention.metal:550-604).
-DEV void slice_scores(const float* qh, const uint16_t* Kt, int kp, int n, int lane, float* pbrow, float* ml) {
-  float score = -INFINITY;
-  if (lane < n) {
-    const uint16_t* kr = Kt + lane * kp;
-    float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
-#pragma unroll 4
-    for (int d = 0; d < LISA_ATT_HD; d += 8) {
-      const uint4 kk = *reinterpret_cast<const uint4*>(kr + d);
-      const float4 qa = *reinterpret_cast<const float4*>(qh + d);
-      const float4 qb = *reinterpret_cast<const float4*>(qh + d + 4);
-      a0 = lisa_fma(qa.x, lo_bf(kk.x), a0);
-      a1 = lisa_fma(qa.y, hi_bf(kk.x), a1);
-      a2 = lisa_fma(qa.z, lo_bf(kk.y), a2);
-      a3 = lisa_fma(qa.w, hi_bf(kk.y), a3);
-      a0 = lisa_fma(qb.x, lo_bf(kk.z), a0);
-      a1 = lisa_fma(qb.y, hi_bf(kk.z), a1);
-      a2 = lisa_fma(qb.z, lo_bf(kk.w), a2);
-      a3 = lisa_fma(qb.w, hi_bf(kk.w), a3);
-    }
-    score = ((a0 + a1) + (a2 + a3)) * 0.0625f;
-  }
-  const float mx = max64(score);
-  const float pv = (lane < n) ? lisa_exp2f(1.4426950408889634f * (score - mx)) : 0.0f;
-  const float den = tree64(pv);
-  pbrow[lane] = pv;
-  if (lane == 0) {
-    ml[0] = mx;
-    ml[1] = den;
-  }
-}
-
-// P.V of one row over the slice for the 6 heads of a KV head; thread = output
-// dimension, tokens in order.
-DEV void slice_pv(const float* pb6, const uint16_t* Vt, int n, int tid, float (&acc)[6]) {
-#pragma unroll
-  for (int i = 0; i < 6; ++i) acc[i] = 0.0f;
-  for (int tok = 0; tok < n; ++tok) {
-    const float vv = bf2f(Vt[tok * LISA_ATT_HD + tid]);
-#pragma unroll
-    for (int i = 0; i < 6; ++i) acc[i] = lisa_fma(pb6[i * LISA_ATT_SLICE + tok], vv, acc[i]);
-  }
-}
-
-// Scores of one row for two heads a, b of the same KV head over a slice (lane =
-// token): each K chunk is read and widened once for both heads; per head the
-// four accumulators over d mod 4 and every later step are those of
-// slice_scores.
+// Scores of one row for two heads a, b of the same KV head over a slice of n
+// cached tokens by one wave (lane = token; attention.metal:550-604): per head
+// q.k with four accumulators over d mod 4, each an ascending fma chain,
+// ((a0 + a1) + (a2 + a3)) / 16, slice max, p = exp2(log2e (score - max)),
+// denominator tree64. Each K chunk is read and widened once for both heads.
 DEV void slice_scores2(const float* qa, const float* qb, const uint16_t* Kt, int kp, int n, int lane,
                        float* pba, float* pbb, float* mla, float* mlb) {
   float sa = -INFINITY, sb = -INFINITY;
@@ -1365,8 +1322,8 @@ DEV void slice_scores2(const float* qa, const float* qb, const uint16_t* Kt, int
 }
 
 // P.V of one row over the slice for three heads (rows of pb3 T apart) and the
-// two output dimensions 2dp, 2dp+1: one 32-bit V read per token serves six
-// chains, each the ascending token chain of slice_pv.
+// two output dimensions 2dp, 2dp+1: six chains acc = fma(p_tok, v_tok, acc)
+// over the tokens in order; one 32-bit V read per token serves all six.
 DEV void slice_pv3(const float* pb3, const uint16_t* Vt, int n, int dp, float (&acc)[3][2]) {
 #pragma unroll
   for (int i = 0; i < 3; ++i) acc[i][0] = acc[i][1] = 0.0f;
@@ -1978,26 +1935,32 @@ extern "C" __global__ __launch_bounds__(256) void lisa_attn_partial_rows(LisaAtt
     qv[e] = bf2f(p.query[((size_t)(r0 + tt) * LISA_ATT_QH + kvh * 6 + i) * HD + d]);
   }
   __syncthreads();
-  for (int pr = wave; pr < nr * 6; pr += 4) {
-    const int tt = pr / 6, i = pr % 6, h = kvh * 6 + i, t = r0 + tt;
+  // scores: item (row tt, head pair) per wave, as the decode partial
+  for (int it = wave; it < nr * 3; it += 4) {
+    const int tt = it / 3, i = 2 * (it % 3), h = kvh * 6 + i, t = r0 + tt;
     const uint32_t ctx = base + t + 1;
     if (ctx <= t0) continue;
     const int n = (int)min((uint32_t)T, ctx - t0);
-    slice_scores(qv + (tt * 6 + i) * HD, Kt, KP, n, lane, pb + (tt * 6 + i) * T,
-                 p.part_ml + (((size_t)t * LISA_ATT_QH + h) * p.s_max + s) * 2);
+    const float* qa = qv + (tt * 6 + i) * HD;
+    float* ml = p.part_ml + (((size_t)t * LISA_ATT_QH + h) * p.s_max + s) * 2;
+    slice_scores2(qa, qa + HD, Kt, KP, n, lane, pb + (tt * 6 + i) * T, pb + (tt * 6 + i + 1) * T, ml,
+                  ml + (size_t)p.s_max * 2);
   }
   __syncthreads();
+  // P.V: thread (dp, hg) owns dimensions 2dp, 2dp+1 of heads 3hg..3hg+2
+  const int dp = tid & 127, hg = tid >> 7;
   for (int tt = 0; tt < nr; ++tt) {
     const int t = r0 + tt;
     const uint32_t ctx = base + t + 1;
     if (ctx <= t0) continue;
     const int n = (int)min((uint32_t)T, ctx - t0);
-    float acc[6];
-    slice_pv(pb + tt * 6 * T, Vt, n, tid, acc);
+    float acc[3][2];
+    slice_pv3(pb + (tt * 6 + 3 * hg) * T, Vt, n, dp, acc);
 #pragma unroll
-    for (int i = 0; i < 6; ++i) {
-      const int h = kvh * 6 + i;
-      p.part_o[(((size_t)t * LISA_ATT_QH + h) * p.s_max + s) * HD + tid] = acc[i];
+    for (int i = 0; i < 3; ++i) {
+      const int h = kvh * 6 + 3 * hg + i;
+      *reinterpret_cast<float2*>(p.part_o + (((size_t)t * LISA_ATT_QH + h) * p.s_max + s) * HD + 2 * dp) =
+          make_float2(acc[i][0], acc[i][1]);
     }
   }
 }
