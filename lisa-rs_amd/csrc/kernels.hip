@@ -926,9 +926,8 @@ QMV_KERNEL_EPI(5120, 3, LISA_PRO_PRENORM, prenorm, LISA_EPI_ARGMAX, argmax)
 // ===========================================================================
 // GDN recurrence (gdn.metal:245-328) + gates (gdn.metal:170-205) + gated
 // RMSNorm (gdn.metal:367-391). One workgroup per value head, 512 threads:
-// thread (v, q) = (tid/4, tid%4) owns 32 elements of state row v: the quarter
-// [32q, 32q+32) in the prefill scan, the runs q, q+4, q+8, q+12 of 8 in the
-// decode step (gdn_row_step_il).
+// thread (v, q) = (tid/4, tid%4) owns the runs q, q+4, q+8, q+12 of 8 of state
+// row v (gdn_row_step_il).
 // ===========================================================================
 // M = 0: the row count comes from p.m_rows (prefill).
 // q or k of one key head (gdn.metal q/k norm): RMS over 128 values as tree64 of
@@ -948,47 +947,17 @@ DEV void gdn_gates(float braw, float araw, uint16_t dt_bias, uint16_t a_log, flo
   decay = lisa_expf(-lisa_expf(bf2f(a_log)) * dt);
 }
 
-// Quarter dot of 32: (r0 + r1) + (r2 + r3) over four ascending fma runs of 8
-// (independent chains, so the dependent latency is 8 fmas, not 32).
-DEV float gdn_dot32(const float (&S)[32], const float* vec) {
-  float r[4];
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    float p = S[8 * j] * vec[8 * j];
-#pragma unroll
-    for (int k = 8 * j + 1; k < 8 * j + 8; ++k) p = lisa_fma(S[k], vec[k], p);
-    r[j] = p;
-  }
-  return (r[0] + r[1]) + (r[2] + r[3]);
-}
-
-// One time step of state row v, quarter q (S = the row's 32 elements 32q..32q+31;
-// kq, qq = the matching 32 elements of k and q): decay, delta rule, readout.
-// Returns the row's readout (the four quarters combined by xor 1, 2, which is
-// (q0 + q1) + (q2 + q3) on every lane).
-DEV float gdn_row_step(float (&S)[32], const float* kq, const float* qq, float vval, float beta, float decay) {
-#pragma unroll
-  for (int k = 0; k < 32; ++k) S[k] = S[k] * decay;
-  float pk = gdn_dot32(S, kq);
-  pk = pk + xor_lane<1>(pk);
-  pk = pk + xor_lane<2>(pk);
-  const float delta = (vval - pk) * beta;
-#pragma unroll
-  for (int k = 0; k < 32; ++k) S[k] = lisa_fma(delta, kq[k], S[k]);
-  float py = gdn_dot32(S, qq);
-  py = py + xor_lane<1>(py);
-  py = py + xor_lane<2>(py);
-  return py;
-}
-
-// The same time step with the row's sixteen runs of 8 interleaved over its four
-// lanes: lane q owns runs q, q+4, q+8, q+12, S[8j + e] = element 8(q + 4j) + e,
-// so in each 16-byte load or store the four lanes of a row touch one 128-byte
-// line (with quarters of 32 contiguous per lane they touch four). kq and qq
-// point at element 8q. Every run is the same ascending fma chain of 8; quarter
-// j (runs 4j..4j+3, one on each lane) is (r0 + r1) + (r2 + r3) by xor 1, 2, and
-// the row is (Q0 + Q1) + (Q2 + Q3): the sums of gdn_dot32 and its xor 1, 2
-// steps, bit for bit.
+// Row dot products of the delta rule (k.S and q.S over a state row of 128, the
+// oracle's order): sixteen ascending fma runs of 8 (r_i over elements 8i..8i+7,
+// the first term a product), quarters Q_j = (r_4j + r_4j+1) + (r_4j+2 + r_4j+3),
+// row = (Q0 + Q1) + (Q2 + Q3). A time step of a state row: S *= decay,
+// delta = (v - k.S) beta, S += delta k, readout q.S.
+// Decode step with the row's sixteen runs interleaved over its four lanes:
+// lane q owns runs q, q+4, q+8, q+12, S[8j + e] = element 8(q + 4j) + e, so in
+// each 16-byte load or store the four lanes of a row touch one 128-byte line
+// (with quarters of 32 contiguous per lane they would touch four). kq and qq
+// point at element 8q. Quarter j (runs 4j..4j+3, one on each lane) is formed
+// by xor 1, 2, and every lane then adds (Q0 + Q1) + (Q2 + Q3).
 DEV float gdn_dot_il(const float (&S)[32], const float* vec) {
   float Q[4];
 #pragma unroll
@@ -1108,12 +1077,13 @@ DEV void gdn_body(const LisaGdnParams& p) {
 // Prefill over rows, in three launches with the arithmetic of gdn_body:
 // lisa_gdn_prep_rows (grid (m, 9) x 256): normalized q and k of every row and
 //   key head into qk [m][2][2048], beta and decay into gates [m][48][2];
-// lisa_gdn_scan_rows (grid (48, 4) x 128, 32 state rows per workgroup): the
-//   sequential delta-rule scan, with no barrier in the time loop (each state
-//   row only needs the precomputed inputs), each row's inputs loaded eight
-//   rows ahead. A step is bound by the LDS bytes that bring every thread its
-//   32 k and 32 q values (1 KB per state row), so four workgroups per head on
-//   192 CUs take half the time per step of two on 96;
+// lisa_gdn_scan_rows (grid (48, 4) x 256, 32 state rows per workgroup, eight
+//   lanes per row with 16 elements each): the sequential delta-rule scan, with
+//   no barrier in the time loop (each state row only needs the precomputed
+//   inputs), each row's inputs loaded eight rows ahead. A step costs the LDS
+//   bytes that bring every lane its k and q values (1 KB per state row) and
+//   the VALU work of the lane's elements, so the head is spread over four
+//   workgroups and each row over eight lanes;
 //   readout y (bf16 values) into y_out [m][6144];
 // lisa_gdn_out_rows (grid (m, 48) x 128): gated RMSNorm of y into gated.
 extern "C" __global__ __launch_bounds__(256) void lisa_gdn_prep_rows(LisaGdnParams p) {
@@ -1155,31 +1125,55 @@ DEV void gdn_row_load(const LisaGdnParams& p, int t, int h, int kh, int v, int l
   in.v = p.conv_out[(size_t)t * LISA_GDN_CONV_DIM + 2 * LISA_GDN_KEY_DIM + h * 128 + v];
 }
 
-extern "C" __global__ __launch_bounds__(128) void lisa_gdn_scan_rows(LisaGdnParams p) {
+// Row dot of the scan over a lane's 16 elements (runs 2o, 2o+1 of its row;
+// lane o = 0..7 of the row): the lane adds its two runs, which is
+// (r_4j + r_4j+1) or (r_4j+2 + r_4j+3) of quarter j = o / 2; xor 1 forms the
+// quarter, xor 2 (Q0 + Q1) or (Q2 + Q3), xor 4 the row.
+DEV float gdn_dot16(const float (&S)[16], const float* vec) {
+  float ra = S[0] * vec[0], rb = S[8] * vec[8];
+#pragma unroll
+  for (int e = 1; e < 8; ++e) {
+    ra = lisa_fma(S[e], vec[e], ra);
+    rb = lisa_fma(S[8 + e], vec[8 + e], rb);
+  }
+  float r = ra + rb;
+  r = r + xor_lane<1>(r);
+  r = r + xor_lane<2>(r);
+  return r + xor_lane<4>(r);
+}
+
+extern "C" __global__ __launch_bounds__(256) void lisa_gdn_scan_rows(LisaGdnParams p) {
   const int rows = (int)p.m_rows;
   const int h = blockIdx.x, kh = h / (LISA_GDN_VH / LISA_GDN_KH);
-  const int tid = threadIdx.x, v = blockIdx.y * 32 + (tid >> 2), q = tid & 3, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, v = blockIdx.y * 32 + (tid >> 3), o = tid & 7, lane = tid & 63, wave = tid >> 6;
   // each wave stages the row's k and q in its own LDS slot (a wave reads only
   // what it wrote, so no workgroup barrier is needed)
-  __shared__ lisa_f32x4 kqs[2][64];
-  float* srow = p.state + (size_t)h * 128 * 128 + (size_t)v * 128 + 32 * q;
-  float S[32];
+  __shared__ lisa_f32x4 kqs[4][64];
+  float* srow = p.state + (size_t)h * 128 * 128 + (size_t)v * 128 + 16 * o;
+  float S[16];
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
+  for (int i = 0; i < 4; ++i) {
     const float4 f = reinterpret_cast<const float4*>(srow)[i];
     S[4 * i] = f.x; S[4 * i + 1] = f.y; S[4 * i + 2] = f.z; S[4 * i + 3] = f.w;
   }
   auto step = [&](const GdnRowIn& in, int t) {
     kqs[wave][lane] = in.kq;
-    float kv[32], qv[32];
+    float kv[16], qv[16];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const lisa_f32x4 k4 = kqs[wave][8 * q + i], q4 = kqs[wave][32 + 8 * q + i];
+    for (int i = 0; i < 4; ++i) {
+      const lisa_f32x4 k4 = kqs[wave][4 * o + i], q4 = kqs[wave][32 + 4 * o + i];
       kv[4 * i] = k4.x; kv[4 * i + 1] = k4.y; kv[4 * i + 2] = k4.z; kv[4 * i + 3] = k4.w;
       qv[4 * i] = q4.x; qv[4 * i + 1] = q4.y; qv[4 * i + 2] = q4.z; qv[4 * i + 3] = q4.w;
     }
-    const float py = gdn_row_step(S, kv, qv, in.v, in.g.x, in.g.y);
-    if (q == 0) p.y_out[(size_t)t * LISA_GDN_VALUE_DIM + h * 128 + v] = lisa_bf16r(py);
+    // the time step on the lane's 16 elements
+#pragma unroll
+    for (int k = 0; k < 16; ++k) S[k] = S[k] * in.g.y;
+    const float pk = gdn_dot16(S, kv);
+    const float delta = (in.v - pk) * in.g.x;
+#pragma unroll
+    for (int k = 0; k < 16; ++k) S[k] = lisa_fma(delta, kv[k], S[k]);
+    const float py = gdn_dot16(S, qv);
+    if (o == 0) p.y_out[(size_t)t * LISA_GDN_VALUE_DIM + h * 128 + v] = lisa_bf16r(py);
   };
   // a ring of eight input sets: row t's inputs are loaded eight rows ahead, so
   // the scan never waits on a memory round trip
@@ -1199,7 +1193,7 @@ extern "C" __global__ __launch_bounds__(128) void lisa_gdn_scan_rows(LisaGdnPara
   for (int j = 0; j < D - 1; ++j)
     if (full + j < rows) step(in[j], full + j);
 #pragma unroll
-  for (int i = 0; i < 8; ++i)
+  for (int i = 0; i < 4; ++i)
     reinterpret_cast<float4*>(srow)[i] = make_float4(S[4 * i], S[4 * i + 1], S[4 * i + 2], S[4 * i + 3]);
 }
 

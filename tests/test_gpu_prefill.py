@@ -156,7 +156,7 @@ def test_gdn_rows_bit_exact(pkg, orc, dev):
                       state=stb.ptr, gated=gb.ptr, y_out=yb.ptr, q_scale=float(np.float32(inv * inv)),
                       k_scale=float(np.float32(inv)), m_rows=m, qk=qkb.ptr, gates=gtb.ptr)
     dev.dispatch("lisa_gdn_prep_rows", p, (m, 9), (256,))
-    dev.dispatch("lisa_gdn_scan_rows", p, (VH, 4), (128,))
+    dev.dispatch("lisa_gdn_scan_rows", p, (VH, 4), (256,))
     dev.dispatch("lisa_gdn_out_rows", p, (m, VH), (128,))
     gated, st, y, _ = orc.gdn_recurrence(co, z, a, b, a_log, dt_bias, nw, s0, m)
     assert np.array_equal(gb.read(np.uint16, m * VH * HD).reshape(m, -1), gated)
