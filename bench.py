@@ -279,12 +279,13 @@ def gemm_phase(pkg, reps=10):
         ab, cb = dev.upload(a.astype(np.uint16)), dev.buffer(m * n * 4)
         p = pkg.GemmParams(ab.ptr, wb.ptr, sbb.ptr, cb.ptr, m, n, k, n)
         best = None
-        for kern, tn in (("lisa_q4_gemm", pkg.GEMM_TILE_N), ("lisa_q4_gemm_wide", pkg.GEMM_TILE_N_WIDE)):
+        for kern, tn, nt in (("lisa_q4_gemm", pkg.GEMM_TILE_N, 256),
+                             ("lisa_q4_gemm_wide", pkg.GEMM_TILE_N_WIDE, pkg.GEMM_THREADS_WIDE)):
             grid = ((n + tn - 1) // tn, (m + pkg.GEMM_TILE_M - 1) // pkg.GEMM_TILE_M)
-            dev.dispatch(kern, p, grid, (256,))
+            dev.dispatch(kern, p, grid, (nt,))
             pkg._check(L.lisa_event_record(ev0, dev.h))
             for _ in range(reps):
-                dev.dispatch(kern, p, grid, (256,), wait=False)
+                dev.dispatch(kern, p, grid, (nt,), wait=False)
             pkg._check(L.lisa_event_record(ev1, dev.h))
             dev.synchronize()
             ms = pkg.C.c_float()

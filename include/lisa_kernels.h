@@ -177,10 +177,12 @@ typedef struct LisaSynthParams {
  * lisa_q4_gemm: C[m][n] (f32, row stride ldc) = A[m][k] (bf16) . deq(W)[n][k]
  * with deq = bf16(fma(scale, q, bias)) (gemm.metal:238-266), bf16 MFMA with f32
  * accumulation. Grid (ceil(n / LISA_GEMM_TILE_N), ceil(m / LISA_GEMM_TILE_M)) x 256;
- * k multiple of 64. */
+ * k multiple of 64. lisa_q4_gemm_wide: same contract, 256 x LISA_GEMM_TILE_N_WIDE
+ * tiles, LISA_GEMM_THREADS_WIDE threads. */
 #define LISA_GEMM_TILE_M 256
 #define LISA_GEMM_TILE_N 128
-#define LISA_GEMM_TILE_N_WIDE 256 /* lisa_q4_gemm_wide: same contract, 256 x 256 tiles */
+#define LISA_GEMM_TILE_N_WIDE 256
+#define LISA_GEMM_THREADS_WIDE 512
 
 typedef struct LisaGemmParams {
   const uint16_t* a;

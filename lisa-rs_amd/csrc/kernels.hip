@@ -1524,16 +1524,16 @@ extern "C" __global__ __launch_bounds__(256) void lisa_attn_merge_m3(LisaAttnPar
 // ===========================================================================
 // q4 GEMM (gemm.metal:152-341 semantics): C[m][n] = sum_k A[m][k] * Wd[n][k],
 // Wd = bf16(fma(scale, q, bias)), bf16 MFMA 32x32x16 with f32 accumulation.
-// Output tile 256 x BN per workgroup (lisa_q4_gemm: BN = 128, lisa_q4_gemm_wide:
-// BN = 256), one 64-wide K step per q4 group. The four waves split the tile
-// 2 x 2; each owns a 128 x BN/2 block as 4 x BN/64 MFMA blocks (accumulators in
-// AGPRs). LDS holds two stages of the A rows and the dequantized W rows (rows
+// Output tile 256 x BN per workgroup (lisa_q4_gemm: BN = 128, 4 waves;
+// lisa_q4_gemm_wide: BN = 256, 8 waves), one 64-wide K step per q4 group. The
+// waves split the tile 2 x 2 or 2 x 4; each owns a 128 x 64 block as 4 x 2 MFMA
+// blocks (accumulators in AGPRs). LDS holds two stages of the A rows and the dequantized W rows (rows
 // padded to 72 bf16, so the 8 lanes of each 128-byte LDS pass read distinct
 // banks); global loads run two K steps ahead in two register sets, and the
 // A copy and W dequant of step s+1 are interleaved with step s's MFMAs (the
 // MFMAs run in the matrix core while the VALU works), so each K step needs
-// one barrier. The wide tile reads half the LDS bytes per MFMA; the launcher
-// picks per shape (fewer, longer tiles against the last round on 256 CUs).
+// one barrier. The launcher picks the tile per shape (fewer, longer tiles
+// against the last round on 256 CUs).
 typedef __bf16 lisa_bf16x8 __attribute__((ext_vector_type(8)));
 typedef float lisa_f32x16 __attribute__((ext_vector_type(16)));
 // Native 4 x u32 vectors for the staging registers (HIP's uint4 struct copies
@@ -1541,23 +1541,25 @@ typedef float lisa_f32x16 __attribute__((ext_vector_type(16)));
 typedef uint32_t lisa_u32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int GEMM_BM = LISA_GEMM_TILE_M, GEMM_PAD = 72;
-constexpr int GEMM_RA = GEMM_BM * 8 / 256;  // A chunks per thread and K step
 
-template <int BN>
+// NT threads (4 or 8 waves): waves split the 256 x BN tile WM x WN; each wave
+// owns a 128 x BN/WN block as 4 x NB MFMA blocks.
+template <int BN, int NT>
 struct GemmCfg {
-  static constexpr int RW = BN / 128;  // W 16 B chunks (32 nibbles) per thread and K step
-  static constexpr int NB = BN / 64;   // 32-wide N blocks per wave
+  static constexpr int WAVES = NT / 64;
+  static constexpr int WN = WAVES / 2;                 // waves along N (2 or 4)
+  static constexpr int RA = GEMM_BM * 8 / NT;          // A chunks per thread and K step
+  static constexpr int RW = BN * 2 / NT;               // W 16 B chunks per thread and K step
+  static constexpr int NB = BN / WN / 32;              // 32-wide N blocks per wave
+  static_assert(RA % 4 == 0 && RW >= 1 && NB >= 1, "tile");
 };
 
-// A chunks 16 B (row u/8, chunk u%8, u = tid + 256 i) and W chunks (row u/2,
-// half u%2, u = RW tid + r) of one K step into one LDS stage, all at once (the
-// first stage only; later stages are written inside gemm_step).
-template <int BN>
+template <int BN, int NT>
 DEV void gemm_lstore(uint16_t* as, uint16_t* ws, int tid, const lisa_u32x4* a, const lisa_u32x4* w, uint32_t sb) {
-  using G = GemmCfg<BN>;
+  using G = GemmCfg<BN, NT>;
 #pragma unroll
-  for (int i = 0; i < GEMM_RA; ++i) {
-    const int u = tid + 256 * i;
+  for (int i = 0; i < G::RA; ++i) {
+    const int u = tid + NT * i;
     *reinterpret_cast<lisa_u32x4*>(&as[(u >> 3) * GEMM_PAD + (u & 7) * 8]) = a[i];
   }
   const float sc = lo_bf(sb), bi = hi_bf(sb);
@@ -1578,35 +1580,32 @@ DEV void gemm_lstore(uint16_t* as, uint16_t* ws, int tid, const lisa_u32x4* a, c
   }
 }
 
-template <int BN>
+template <int BN, int NT>
 DEV void gemm_frags(const uint16_t* as, const uint16_t* ws, int wm, int wn, int lane, int ks, lisa_bf16x8 (&af)[4],
-                    lisa_bf16x8 (&bf)[GemmCfg<BN>::NB]) {
+                    lisa_bf16x8 (&bf)[GemmCfg<BN, NT>::NB]) {
+  using G = GemmCfg<BN, NT>;
 #pragma unroll
   for (int i = 0; i < 4; ++i)
     af[i] = *reinterpret_cast<const lisa_bf16x8*>(
         &as[(wm * 128 + i * 32 + (lane & 31)) * GEMM_PAD + ks * 16 + 8 * (lane >> 5)]);
 #pragma unroll
-  for (int j = 0; j < GemmCfg<BN>::NB; ++j)
+  for (int j = 0; j < G::NB; ++j)
     bf[j] = *reinterpret_cast<const lisa_bf16x8*>(
-        &ws[(wn * (BN / 2) + j * 32 + (lane & 31)) * GEMM_PAD + ks * 16 + 8 * (lane >> 5)]);
+        &ws[(wn * (BN / G::WN) + j * 32 + (lane & 31)) * GEMM_PAD + ks * 16 + 8 * (lane >> 5)]);
 }
 
-// One K step: the MFMAs of the wave's block from stage (as_r, ws_r), with the
-// next step's stage (as_w, ws_w) written alongside. Sub-step ks reads the
-// fragments of ks+1, then issues its MFMAs interleaved with the dequant of W
-// word ks of each of the thread's chunks, and stores A chunks 2ks, 2ks+1.
-template <int BN>
+template <int BN, int NT>
 DEV void gemm_step(const uint16_t* as_r, const uint16_t* ws_r, uint16_t* as_w, uint16_t* ws_w, int tid, int wm, int wn,
                    int lane, const lisa_u32x4* a, const lisa_u32x4* w, uint32_t sb,
-                   lisa_f32x16 (&acc)[4][GemmCfg<BN>::NB]) {
-  using G = GemmCfg<BN>;
+                   lisa_f32x16 (&acc)[4][GemmCfg<BN, NT>::NB]) {
+  using G = GemmCfg<BN, NT>;
   lisa_bf16x8 af[2][4], bf[2][G::NB];
-  gemm_frags<BN>(as_r, ws_r, wm, wn, lane, 0, af[0], bf[0]);
+  gemm_frags<BN, NT>(as_r, ws_r, wm, wn, lane, 0, af[0], bf[0]);
   const float sc = lo_bf(sb), bi = hi_bf(sb);
 #pragma unroll
   for (int ks = 0; ks < 4; ++ks) {
     const int c = ks & 1;
-    if (ks + 1 < 4) gemm_frags<BN>(as_r, ws_r, wm, wn, lane, ks + 1, af[c ^ 1], bf[c ^ 1]);
+    if (ks + 1 < 4) gemm_frags<BN, NT>(as_r, ws_r, wm, wn, lane, ks + 1, af[c ^ 1], bf[c ^ 1]);
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
@@ -1624,37 +1623,35 @@ DEV void gemm_step(const uint16_t* as_r, const uint16_t* ws_r, uint16_t* as_w, u
                      lisa_f32x2_to_bf16x2(v[4], v[5]), lisa_f32x2_to_bf16x2(v[6], v[7]));
     }
 #pragma unroll
-    for (int i = 2 * ks; i < 2 * ks + 2; ++i) {
-      const int u = tid + 256 * i;
+    for (int i = ks * (G::RA / 4); i < (ks + 1) * (G::RA / 4); ++i) {
+      const int u = tid + NT * i;
       *reinterpret_cast<lisa_u32x4*>(&as_w[(u >> 3) * GEMM_PAD + (u & 7) * 8]) = a[i];
     }
-    // issue order within the sub-step: fragment reads, then MFMA/VALU pairs
     if (ks + 1 < 4) __builtin_amdgcn_sched_group_barrier(0x100, 4 + G::NB, 0);
 #pragma unroll
     for (int q = 0; q < 4 * G::NB; ++q) {
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
       __builtin_amdgcn_sched_group_barrier(0x002, 32 * G::RW / (4 * G::NB) + 1, 0);
     }
-    __builtin_amdgcn_sched_group_barrier(0x200, 2 + G::RW, 0);
+    __builtin_amdgcn_sched_group_barrier(0x200, G::RA / 4 + G::RW, 0);
   }
 }
 
-template <int BN>
+template <int BN, int NT>
 DEV void q4_gemm_body(const LisaGemmParams& p, uint16_t (*As)[GEMM_BM * GEMM_PAD], uint16_t (*Ws)[BN * GEMM_PAD]) {
-  using G = GemmCfg<BN>;
+  using G = GemmCfg<BN, NT>;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
+  const int wm = wave / G::WN, wn = wave % G::WN;
   const uint32_t m0 = blockIdx.y * GEMM_BM, n0 = blockIdx.x * BN;
   const uint32_t K = p.k, nk = K / 64;
 
-  const lisa_u32x4* asrc[GEMM_RA];
+  const lisa_u32x4* asrc[G::RA];
 #pragma unroll
-  for (int i = 0; i < GEMM_RA; ++i) {
-    const int u = tid + 256 * i;
+  for (int i = 0; i < G::RA; ++i) {
+    const int u = tid + NT * i;
     const uint32_t row = min(m0 + (uint32_t)(u >> 3), p.m - 1);
     asrc[i] = reinterpret_cast<const lisa_u32x4*>(p.a + (size_t)row * K) + (u & 7);
   }
-  // every W chunk of a thread lies in one row: (RW tid + r) / 2 = RW tid / 2
   const uint32_t wrow = min(n0 + (uint32_t)((G::RW * tid) >> 1), p.n - 1);
   const lisa_u32x4* wsrc = reinterpret_cast<const lisa_u32x4*>(p.w + (size_t)wrow * (K / 8)) + ((G::RW * tid) & 1);
   const uint32_t* sbsrc = p.sb + (size_t)wrow * (K / 64);
@@ -1667,41 +1664,33 @@ DEV void q4_gemm_body(const LisaGemmParams& p, uint16_t (*As)[GEMM_BM * GEMM_PAD
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
-  // Global loads of one K step into register set (A, W, SB). Steps past the
-  // end re-read the last one, so the loads stay unconditional. Two sets: even
-  // steps and odd steps.
 #define GEMM_GLOAD(A, W, SB, STEP)                                                        \
   {                                                                                       \
     const uint32_t st_ = min((uint32_t)(STEP), nk - 1);                                   \
-    _Pragma("unroll") for (int i = 0; i < GEMM_RA; ++i) A[i] = asrc[i][st_ * 8];          \
+    _Pragma("unroll") for (int i = 0; i < G::RA; ++i) A[i] = asrc[i][st_ * 8];            \
     _Pragma("unroll") for (int r = 0; r < G::RW; ++r) W[r] = wsrc[st_ * 2 + r];           \
     SB = sbsrc[st_];                                                                      \
   }
-  lisa_u32x4 a0[GEMM_RA], a1[GEMM_RA], w0[G::RW], w1[G::RW];
+  lisa_u32x4 a0[G::RA], a1[G::RA], w0[G::RW], w1[G::RW];
   uint32_t sb0, sb1;
   GEMM_GLOAD(a0, w0, sb0, 0);
   GEMM_GLOAD(a1, w1, sb1, 1);
-  gemm_lstore<BN>(As[0], Ws[0], tid, a0, w0, sb0);
+  gemm_lstore<BN, NT>(As[0], Ws[0], tid, a0, w0, sb0);
   __syncthreads();
-  // nk is even (k is a multiple of 128): steps go in pairs, one exit
   for (uint32_t step = 0; step < nk; step += 2) {
-    // even step: MFMAs on stage 0 while step+1 goes to stage 1 and step+2 loads
     GEMM_GLOAD(a0, w0, sb0, step + 2);
-    gemm_step<BN>(As[0], Ws[0], As[1], Ws[1], tid, wm, wn, lane, a1, w1, sb1, acc);
+    gemm_step<BN, NT>(As[0], Ws[0], As[1], Ws[1], tid, wm, wn, lane, a1, w1, sb1, acc);
     __syncthreads();
-    // odd step: MFMAs on stage 1 while step+2 goes to stage 0 and step+3 loads
-    // (past the last step the stores write data nobody reads)
     GEMM_GLOAD(a1, w1, sb1, step + 3);
-    gemm_step<BN>(As[1], Ws[1], As[0], Ws[0], tid, wm, wn, lane, a0, w0, sb0, acc);
+    gemm_step<BN, NT>(As[1], Ws[1], As[0], Ws[0], tid, wm, wn, lane, a0, w0, sb0, acc);
     __syncthreads();
   }
 #undef GEMM_GLOAD
-  // C layout of a 32x32 block: element r of lane l is row 8(r/4) + 4(l/32) + r%4, column l%32
 #pragma unroll
   for (int i = 0; i < 4; ++i)
 #pragma unroll
     for (int j = 0; j < G::NB; ++j) {
-      const uint32_t col = n0 + wn * (BN / 2) + j * 32 + (lane & 31);
+      const uint32_t col = n0 + wn * (BN / G::WN) + j * 32 + (lane & 31);
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const uint32_t row = m0 + wm * 128 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
@@ -1710,19 +1699,21 @@ DEV void q4_gemm_body(const LisaGemmParams& p, uint16_t (*As)[GEMM_BM * GEMM_PAD
     }
 }
 
-// One workgroup per CU (the LDS stages take 108 or 144 KB), so the whole
-// register file is available to its four waves.
+// lisa_q4_gemm: one 4-wave workgroup per CU (the LDS stages take 108 KB), so the
+// whole register file is available to its waves. lisa_q4_gemm_wide: eight
+// waves, two per SIMD (252 registers each), so one wave's MFMAs run while the
+// other waits on a barrier, an LDS read or its dequant.
 extern "C" __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void lisa_q4_gemm(
     LisaGemmParams p) {
   __shared__ __attribute__((aligned(16))) uint16_t As[2][GEMM_BM * GEMM_PAD];
   __shared__ __attribute__((aligned(16))) uint16_t Ws[2][LISA_GEMM_TILE_N * GEMM_PAD];
-  q4_gemm_body<LISA_GEMM_TILE_N>(p, As, Ws);
+  q4_gemm_body<LISA_GEMM_TILE_N, 256>(p, As, Ws);
 }
-extern "C" __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void lisa_q4_gemm_wide(
+extern "C" __global__ __launch_bounds__(LISA_GEMM_THREADS_WIDE) __attribute__((amdgpu_waves_per_eu(2, 2))) void lisa_q4_gemm_wide(
     LisaGemmParams p) {
   __shared__ __attribute__((aligned(16))) uint16_t As[2][GEMM_BM * GEMM_PAD];
   __shared__ __attribute__((aligned(16))) uint16_t Ws[2][LISA_GEMM_TILE_N_WIDE * GEMM_PAD];
-  q4_gemm_body<LISA_GEMM_TILE_N_WIDE>(p, As, Ws);
+  q4_gemm_body<LISA_GEMM_TILE_N_WIDE, LISA_GEMM_THREADS_WIDE>(p, As, Ws);
 }
 
 // Per-row kernels. NORM/RESNORM follow the q4 prologue's arithmetic exactly

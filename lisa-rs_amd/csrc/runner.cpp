@@ -1119,14 +1119,14 @@ int launch_gemm(LisaRunner* r, const uint16_t* a, uint32_t m, const Q4Dev& w, fl
   g.k = w.k;
   g.ldc = w.n;
   // One workgroup per CU: a launch runs in rounds of `cus` tiles. A 256-wide
-  // tile takes about 1.6x a 128-wide one (it reads half the LDS bytes per
-  // MFMA); take it unless its rounds cost more.
+  // tile (eight waves) takes about 1.5x a 128-wide one; take it unless its
+  // rounds cost more.
   const uint32_t gm = (m + LISA_GEMM_TILE_M - 1) / LISA_GEMM_TILE_M;
   const uint32_t gn = (w.n + LISA_GEMM_TILE_N - 1) / LISA_GEMM_TILE_N;
   const uint32_t gw = (w.n + LISA_GEMM_TILE_N_WIDE - 1) / LISA_GEMM_TILE_N_WIDE;
   const uint32_t cus = r->dev->cu_count > 0 ? (uint32_t)r->dev->cu_count : 256;
   const uint32_t rn = (gn * gm + cus - 1) / cus, rw = (gw * gm + cus - 1) / cus;
-  if (rw * 16 <= rn * 10) return lisa_launch(r->dev, r->gemm_wide, &g, sizeof g, gw, gm, 1, 256, 1, 1);
+  if (rw * 3 <= rn * 2) return lisa_launch(r->dev, r->gemm_wide, &g, sizeof g, gw, gm, 1, LISA_GEMM_THREADS_WIDE, 1, 1);
   return lisa_launch(r->dev, r->gemm, &g, sizeof g, gn, gm, 1, 256, 1, 1);
 }
 

@@ -38,8 +38,9 @@ def gemm(pkg, dev, a_bf16, q, m, kernel="lisa_q4_gemm"):
     ab = dev.upload(a_bf16)
     p = pkg.GemmParams(ab.ptr, q.wbuf.ptr, q.sbbuf.ptr, out.ptr, m, q.n, q.k, q.n)
     tm = pkg.GEMM_TILE_M
-    tn = pkg.GEMM_TILE_N_WIDE if kernel.endswith("_wide") else pkg.GEMM_TILE_N
-    dev.dispatch(kernel, p, ((q.n + tn - 1) // tn, (m + tm - 1) // tm), (256,))
+    wide = kernel.endswith("_wide")
+    tn = pkg.GEMM_TILE_N_WIDE if wide else pkg.GEMM_TILE_N
+    dev.dispatch(kernel, p, ((q.n + tn - 1) // tn, (m + tm - 1) // tm), (pkg.GEMM_THREADS_WIDE if wide else 256,))
     return out.read(np.float32, m * q.n).reshape(m, q.n)
 
 
