@@ -688,6 +688,15 @@ DEV void qmv_body(const LisaQmvParams& p, unsigned char* lds) {
   // wv is wave-uniform: keeping it scalar keeps the matrix lookup on scalar loads
   const int tid = threadIdx.x, lane = tid & 63, wv = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int li = lane & 15, rp = lane >> 4;
+  // One word of every 64-byte line of the kernel arguments, read in one batch
+  // and consumed: the lookups below read further words of these lines in a
+  // chain of dependent scalar loads, and the first touch of a line misses the
+  // scalar cache, so without this every link of the chain waits for memory.
+  {
+    const uint32_t* kw = reinterpret_cast<const uint32_t*>(&p);
+    static_assert(sizeof(LisaQmvParams) > 320 && sizeof(LisaQmvParams) <= 384, "six argument lines");
+    asm volatile("" : : "s"(kw[0]), "s"(kw[16]), "s"(kw[32]), "s"(kw[48]), "s"(kw[64]), "s"(kw[80]));
+  }
   const uint32_t tiles = qmv_tiles(p);
   const uint32_t tile = C::SPLIT ? blockIdx.x : blockIdx.x * 4 + wv;
   const bool tile_ok = tile < tiles;
