@@ -84,6 +84,15 @@ typedef struct LisaQmvParams {
   uint32_t pro_mode;
   uint32_t capture;
   uint32_t ksplit; /* 1 or 4: waves of a workgroup split K of one tile */
+  /* GDN in-projection (K = 5120, normalizing prologue): when gate_ab is set,
+   * workgroup w < 48 also forms the 80 per-group contributions of rows w of the
+   * q4 a and b matrices [48][5120] against its staged x, stored f32
+   * gate_ab[m][w][a, b][80]; the recurrence adds them in a q4 launch's order. */
+  const uint32_t* gate_a_w;
+  const uint32_t* gate_a_sb;
+  const uint32_t* gate_b_w;
+  const uint32_t* gate_b_sb;
+  float* gate_ab;
 } LisaQmvParams;
 
 /* ---- GDN recurrence + gated RMSNorm --------------------------------------
@@ -109,6 +118,10 @@ typedef struct LisaGdnParams {
   uint32_t m_rows; /* prefill kernels: number of rows (time steps) */
   float* qk;       /* prefill: normalized q, k per row [m][2][2048] */
   float* gates;    /* prefill: (beta, decay) per row and value head [m][48][2] */
+  /* Decode: when set, a and b of head h come from the in-projection's group
+   * contributions gate_ab[m][h][a, b][80] (see LisaQmvParams.gate_ab) and the
+   * a, b fields are unused. */
+  const float* gate_ab;
 } LisaGdnParams;
 
 /* ---- split-K decode attention --------------------------------------------

@@ -70,7 +70,9 @@ class QmvParams(C.Structure):
                 ("conv_slot_stride", C.c_uint64),
                 ("am_val", C.c_uint64), ("am_idx", C.c_uint64),
                 ("mats", Q4Mat * 4), ("tile_start", C.c_uint32 * 5),
-                ("n_mats", C.c_uint32), ("pro_mode", C.c_uint32), ("capture", C.c_uint32), ("ksplit", C.c_uint32)]
+                ("n_mats", C.c_uint32), ("pro_mode", C.c_uint32), ("capture", C.c_uint32), ("ksplit", C.c_uint32),
+                ("gate_a_w", C.c_uint64), ("gate_a_sb", C.c_uint64), ("gate_b_w", C.c_uint64),
+                ("gate_b_sb", C.c_uint64), ("gate_ab", C.c_uint64)]
 
 
 class GdnParams(C.Structure):
@@ -78,7 +80,8 @@ class GdnParams(C.Structure):
                 ("a_log", C.c_uint64), ("dt_bias", C.c_uint64), ("norm_w", C.c_uint64),
                 ("state", C.c_uint64), ("slots", C.c_uint64), ("slot_stride", C.c_uint64),
                 ("gated", C.c_uint64), ("y_out", C.c_uint64), ("q_scale", C.c_float), ("k_scale", C.c_float),
-                ("capture", C.c_uint32), ("m_rows", C.c_uint32), ("qk", C.c_uint64), ("gates", C.c_uint64)]
+                ("capture", C.c_uint32), ("m_rows", C.c_uint32), ("qk", C.c_uint64), ("gates", C.c_uint64),
+                ("gate_ab", C.c_uint64)]
 
 
 class AttnParams(C.Structure):

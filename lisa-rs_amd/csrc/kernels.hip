@@ -694,8 +694,8 @@ DEV void qmv_body(const LisaQmvParams& p, unsigned char* lds) {
   // scalar cache, so without this every link of the chain waits for memory.
   {
     const uint32_t* kw = reinterpret_cast<const uint32_t*>(&p);
-    static_assert(sizeof(LisaQmvParams) > 320 && sizeof(LisaQmvParams) <= 384, "six argument lines");
-    asm volatile("" : : "s"(kw[0]), "s"(kw[16]), "s"(kw[32]), "s"(kw[48]), "s"(kw[64]), "s"(kw[80]));
+    static_assert(sizeof(LisaQmvParams) > 384 && sizeof(LisaQmvParams) <= 448, "seven argument lines");
+    asm volatile("" : : "s"(kw[0]), "s"(kw[16]), "s"(kw[32]), "s"(kw[48]), "s"(kw[64]), "s"(kw[80]), "s"(kw[96]));
   }
   const uint32_t tiles = qmv_tiles(p);
   const uint32_t tile = C::SPLIT ? blockIdx.x : blockIdx.x * 4 + wv;
@@ -887,6 +887,31 @@ DEV void qmv_body(const LisaQmvParams& p, unsigned char* lds) {
       __syncthreads();
     }
   }
+  if constexpr (K == LISA_HIDDEN && !C::SPLIT && !WAVEX && MODE != LISA_PRO_LOADX) {
+    // GDN in-projection: workgroup w < 48 forms the per-group contributions of
+    // rows w of the a and b matrices against the staged x (thread g < 80 forms
+    // group g as a q4 tile's lane forms each of its groups, from a running sum
+    // of 0), last, when the tile's registers are free. The launch then carries
+    // no a/b tiles: their 12 tiles would make 515 workgroups, three past two
+    // per CU.
+    if (p.gate_ab != nullptr && blockIdx.x < LISA_GDN_VH && tid < C::G) {
+      const uint32_t hh = blockIdx.x;
+      const uint4* aw = reinterpret_cast<const uint4*>(p.gate_a_w + (size_t)hh * (K / 8));
+      const uint4* bw = reinterpret_cast<const uint4*>(p.gate_b_w + (size_t)hh * (K / 8));
+      const uint4 a0 = aw[2 * tid], b0 = aw[2 * tid + 1], a1 = bw[2 * tid], b1 = bw[2 * tid + 1];
+      const uint32_t s0 = p.gate_a_sb[(size_t)hh * C::G + tid], s1 = p.gate_b_sb[(size_t)hh * C::G + tid];
+      float G0[M], G1[M];
+#pragma unroll
+      for (int m = 0; m < M; ++m) { G0[m] = 0.0f; G1[m] = 0.0f; }
+      group_dot2<C::ROWBYTES, C::G, M>(lds, tid, a0, b0, a1, b1, s0, s1, gsum, G0, G1);
+#pragma unroll
+      for (int m = 0; m < M; ++m) {
+        float* dst = p.gate_ab + (((size_t)m * LISA_GDN_VH + hh) * 2) * C::G + tid;
+        dst[0] = G0[m];
+        dst[C::G] = G1[m];
+      }
+    }
+  }
 }
 
 // One kernel per (K, M, prologue): lisa_qmv_k<K>_m<M>_<x|resnorm|embed|cast|norm|mtpfc|prenorm>,
@@ -1014,6 +1039,8 @@ DEV void gdn_body(const LisaGdnParams& p) {
   // the 128 B of state this thread owns, so the norms and gates are formed
   // while the state arrives.
   float c0[M], c1[M], vval[M], zraw[M], braw[M], araw[M];
+  float gav[M][5], gbv[M][5];
+  const bool gsrc = p.gate_ab != nullptr;
   float nwt = 0.0f;
 #pragma unroll
   for (int t = 0; t < M; ++t) {
@@ -1025,8 +1052,21 @@ DEV void gdn_body(const LisaGdnParams& p) {
     vval[t] = co[2 * LISA_GDN_KEY_DIM + h * 128 + v];
     zraw[t] = 0.0f;
     if (tid < 128) zraw[t] = p.z[(size_t)t * LISA_GDN_VALUE_DIM + h * 128 + tid];
-    braw[t] = p.b[(size_t)t * LISA_GDN_VH + h];
-    araw[t] = p.a[(size_t)t * LISA_GDN_VH + h];
+    braw[t] = 0.0f;
+    araw[t] = 0.0f;
+    if (!gsrc) {
+      braw[t] = p.b[(size_t)t * LISA_GDN_VH + h];
+      araw[t] = p.a[(size_t)t * LISA_GDN_VH + h];
+    } else {
+      // the in-projection's group contributions for lane li's groups
+      // li, 16 + li, .., 64 + li (summed below, once the state loads are out)
+      const float* ga = p.gate_ab + (((size_t)t * LISA_GDN_VH + h) * 2) * (LISA_HIDDEN / 64) + (lane & 15);
+#pragma unroll
+      for (int i = 0; i < 5; ++i) {
+        gav[t][i] = ga[16 * i];
+        gbv[t][i] = ga[LISA_HIDDEN / 64 + 16 * i];
+      }
+    }
   }
   if (tid < 128) nwt = bf2f(p.norm_w[tid]);
   __builtin_amdgcn_sched_barrier(0);
@@ -1038,6 +1078,22 @@ DEV void gdn_body(const LisaGdnParams& p) {
     S[4 * i] = f.x; S[4 * i + 1] = f.y; S[4 * i + 2] = f.z; S[4 * i + 3] = f.w;
   }
   __builtin_amdgcn_sched_barrier(0);
+  if (gsrc) {
+    // a and b as a q4 launch forms a row: lane li adds its five group
+    // contributions to a running sum from 0 in order, then tree16 (thread 128,
+    // lane 0 of wave 2, forms the gates from them)
+#pragma unroll
+    for (int t = 0; t < M; ++t) {
+      float ta = 0.0f, tb = 0.0f;
+#pragma unroll
+      for (int i = 0; i < 5; ++i) {
+        ta = ta + gav[t][i];
+        tb = tb + gbv[t][i];
+      }
+      araw[t] = tree16(ta);
+      braw[t] = tree16(tb);
+    }
+  }
 #pragma unroll
   for (int t = 0; t < rows; ++t) {
     const size_t o = (size_t)t * LISA_GDN_VALUE_DIM + h * 128 + tid;

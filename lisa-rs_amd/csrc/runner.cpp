@@ -62,7 +62,7 @@ struct MtpDev {
 struct Ctx {
   int rows = 1;
   uint16_t *H, *gated, *act, *xnorm, *cond;  // H: residual rows, updated in place
-  float *B, *conv_out, *z, *a, *b, *q_proj, *k_raw, *v_raw, *part_o, *part_ml, *logits, *am_val;
+  float *B, *conv_out, *z, *a, *b, *gate_ab, *q_proj, *k_raw, *v_raw, *part_o, *part_ml, *logits, *am_val;
   uint32_t *am_idx, *tokens, *argmax, *pos, *step, *history;
 };
 
@@ -341,6 +341,7 @@ void plan_ctx(LisaRunner* r, Arena& A, Ctx& c, int rows) {
   c.z = A.take<float>((size_t)rows * LISA_GDN_VALUE_DIM);
   c.a = A.take<float>((size_t)rows * LISA_GDN_VH);
   c.b = A.take<float>((size_t)rows * LISA_GDN_VH);
+  c.gate_ab = A.take<float>((size_t)rows * LISA_GDN_VH * 2 * (LISA_HIDDEN / 64));
   c.gated = A.take<uint16_t>((size_t)rows * LISA_ATT_OUT);
   c.act = A.take<uint16_t>((size_t)rows * LISA_INTER);
   c.q_proj = A.take<float>((size_t)rows * LISA_ATT_Q_OUT);
@@ -374,6 +375,10 @@ int launch_qmv(LisaRunner* r, int m_rows, uint32_t K, LisaQmvParams& p, const st
   if (ki < 0) return lisa_fail(LISA_E_ARG, "no q4 kernel for K=%u", K);
   if (mats.empty() || mats.size() > LISA_QMV_MAX_MATS) return lisa_fail(LISA_E_ARG, "q4 launch of %zu matrices", mats.size());
   if (p.pro_mode > LISA_PRO_PRENORM) return lisa_fail(LISA_E_ARG, "bad q4 prologue mode %u", p.pro_mode);
+  if (p.gate_ab && (K != LISA_HIDDEN || p.pro_mode == LISA_PRO_LOADX || !p.gate_a_w || !p.gate_a_sb ||
+                    !p.gate_b_w || !p.gate_b_sb))
+    return lisa_fail(LISA_E_ARG, "gate contributions need K=%u, a normalizing prologue and both gate matrices",
+                     (unsigned)LISA_HIDDEN);
   LisaFunction* fn = r->qmv[m_rows == 3 ? 1 : 0][ki][p.pro_mode];
   // a launch whose matrices all share one epilogue uses the specialized kernel when there is one
   bool same_kind = !mats.empty();
@@ -511,17 +516,20 @@ int encode_target(LisaRunner* r, int m, bool capture, bool feedback) {
       p.conv_slots = capture ? r->conv_slots + (size_t)si * 3 * LISA_GDN_CONV_DIM : nullptr;
       p.conv_slot_stride = (uint64_t)r->gdn_layers * 3 * LISA_GDN_CONV_DIM;
       p.capture = capture ? 1 : 0;
+      // a and b leave the tile list: the first 48 workgroups form their group
+      // contributions, which the recurrence sums (512 workgroups, not 515)
+      p.gate_a_w = l.a.w;
+      p.gate_a_sb = l.a.sb;
+      p.gate_b_w = l.b.w;
+      p.gate_b_sb = l.b.sb;
+      p.gate_ab = c.gate_ab;
       LISA_TRY(prof_mark(r, LISA_KIND_GDN_IN));
       LISA_TRY(launch_qmv(r, m, LISA_HIDDEN, p,
-                          {{&l.qkv, nullptr, c.conv_out, LISA_EPI_CONV},
-                           {&l.z, nullptr, c.z, LISA_EPI_STORE},
-                           {&l.a, nullptr, c.a, LISA_EPI_STORE},
-                           {&l.b, nullptr, c.b, LISA_EPI_STORE}}));
+                          {{&l.qkv, nullptr, c.conv_out, LISA_EPI_CONV}, {&l.z, nullptr, c.z, LISA_EPI_STORE}}));
       LisaGdnParams g{};
       g.conv_out = c.conv_out;
       g.z = c.z;
-      g.a = c.a;
-      g.b = c.b;
+      g.gate_ab = c.gate_ab;
       g.a_log = l.a_log;
       g.dt_bias = l.dt_bias;
       g.norm_w = l.gnorm;

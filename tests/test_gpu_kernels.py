@@ -229,26 +229,42 @@ def test_gdn_layer_config1(pkg, orc, dev, M):
     p.h_in, p.norm_w = hb.ptr, nb.ptr
     p.conv_w, p.conv_state, p.conv_slots, p.conv_slot_stride = cwb.ptr, csb.ptr, cslot.ptr, 3 * 10240
     p.capture = 1 if M == 3 else 0
-    launch_qmv(pkg, dev, K, M, p, [(qd["qkv"], None, co.ptr, pkg.EPI_CONV), (qd["z"], None, zb.ptr, pkg.EPI_STORE),
-                                  (qd["a"], None, ab.ptr, pkg.EPI_STORE), (qd["b"], None, bb.ptr, pkg.EPI_STORE)])
+    # the decoder's in-projection: qkv and z tiles; a and b as per-group
+    # contributions formed by the first 48 workgroups
+    gab = dev.buffer(M * 48 * 2 * 80 * 4)
+    p.gate_a_w, p.gate_a_sb, p.gate_b_w, p.gate_b_sb = qd["a"].wbuf.ptr, qd["a"].sbbuf.ptr, qd["b"].wbuf.ptr, qd["b"].sbbuf.ptr
+    p.gate_ab = gab.ptr
+    launch_qmv(pkg, dev, K, M, p, [(qd["qkv"], None, co.ptr, pkg.EPI_CONV), (qd["z"], None, zb.ptr, pkg.EPI_STORE)])
     assert same_bits(co.read(np.float32, M * 10240).reshape(M, 10240), conv_out)
     assert same_bits(zb.read(np.float32, M * 6144).reshape(M, 6144), proj["z"])
     assert np.array_equal(csb.read(np.uint16, 3 * 10240), cs_want)
+    # a and b as q4 tiles (the recurrence's raw a/b inputs)
+    pab = pkg.QmvParams()
+    pab.pro_mode = pkg.PRO_NORM
+    pab.h_in, pab.norm_w = hb.ptr, nb.ptr
+    launch_qmv(pkg, dev, K, M, pab, [(qd["a"], None, ab.ptr, pkg.EPI_STORE), (qd["b"], None, bb.ptr, pkg.EPI_STORE)])
+    assert same_bits(ab.read(np.float32, M * 48).reshape(M, 48), proj["a"])
+    assert same_bits(bb.read(np.float32, M * 48).reshape(M, 48), proj["b"])
 
-    stb = dev.upload(state)
-    gslot = dev.buffer(2 * 48 * 128 * 128 * 4)
-    gb = dev.buffer(M * 6144 * 2)
-    g = pkg.GdnParams()
-    g.conv_out, g.z, g.a, g.b = co.ptr, zb.ptr, ab.ptr, bb.ptr
     al, dtb, gn = dev.upload(a_log), dev.upload(dt_bias), dev.upload(gnorm)
-    g.a_log, g.dt_bias, g.norm_w = al.ptr, dtb.ptr, gn.ptr
-    g.state, g.slots, g.slot_stride, g.gated = stb.ptr, gslot.ptr, 48 * 128 * 128, gb.ptr
     inv = np.float32(1.0) / np.sqrt(np.float32(128.0))
-    g.q_scale, g.k_scale = float(inv * inv), float(inv)
-    g.capture = 1 if M == 3 else 0
-    dev.dispatch(f"lisa_gdn_recurrence_m{M}", g, (48,), (512,))
-    assert np.array_equal(gb.read(np.uint16, M * 6144).reshape(M, 6144), gated)
-    assert same_bits(stb.read(np.float32, 48 * 128 * 128), st_want)
+    for source in ("contributions", "tiles"):
+        stb = dev.upload(state)
+        gslot = dev.buffer(2 * 48 * 128 * 128 * 4)
+        gb = dev.buffer(M * 6144 * 2)
+        g = pkg.GdnParams()
+        g.conv_out, g.z = co.ptr, zb.ptr
+        if source == "contributions":
+            g.gate_ab = gab.ptr
+        else:
+            g.a, g.b = ab.ptr, bb.ptr
+        g.a_log, g.dt_bias, g.norm_w = al.ptr, dtb.ptr, gn.ptr
+        g.state, g.slots, g.slot_stride, g.gated = stb.ptr, gslot.ptr, 48 * 128 * 128, gb.ptr
+        g.q_scale, g.k_scale = float(inv * inv), float(inv)
+        g.capture = 1 if M == 3 else 0
+        dev.dispatch(f"lisa_gdn_recurrence_m{M}", g, (48,), (512,))
+        assert np.array_equal(gb.read(np.uint16, M * 6144).reshape(M, 6144), gated), source
+        assert same_bits(stb.read(np.float32, 48 * 128 * 128), st_want), source
     if M == 3:
         for t in range(2):
             assert same_bits(gslot.read(np.float32, 48 * 128 * 128, offset=t * 48 * 128 * 128 * 4),
