@@ -57,6 +57,9 @@ typedef struct LisaQ4Mat {
   uint32_t kind;
 } LisaQ4Mat;
 
+/* floats per (row, value head) of the in-projection's gate contributions */
+#define LISA_GDN_GATE_FLOATS 192
+
 typedef struct LisaQmvParams {
   /* prologue */
   const uint16_t* x_in;
@@ -87,7 +90,9 @@ typedef struct LisaQmvParams {
   /* GDN in-projection (K = 5120, normalizing prologue): when gate_ab is set,
    * workgroup w < 48 also forms the 80 per-group contributions of rows w of the
    * q4 a and b matrices [48][5120] against its staged x, stored f32
-   * gate_ab[m][w][a, b][80]; the recurrence adds them in a q4 launch's order. */
+   * gate_ab[m][w][LISA_GDN_GATE_FLOATS]: for lane li < 16 of a q4 tile, 12
+   * floats at 12 li holding a's groups li, 16 + li, .., 64 + li, then b's, then
+   * two unused; the recurrence adds them in a q4 launch's order. */
   const uint32_t* gate_a_w;
   const uint32_t* gate_a_sb;
   const uint32_t* gate_b_w;
@@ -119,8 +124,8 @@ typedef struct LisaGdnParams {
   float* qk;       /* prefill: normalized q, k per row [m][2][2048] */
   float* gates;    /* prefill: (beta, decay) per row and value head [m][48][2] */
   /* Decode: when set, a and b of head h come from the in-projection's group
-   * contributions gate_ab[m][h][a, b][80] (see LisaQmvParams.gate_ab) and the
-   * a, b fields are unused. */
+   * contributions gate_ab[m][h][LISA_GDN_GATE_FLOATS] (see LisaQmvParams.gate_ab)
+   * and the a, b fields are unused. */
   const float* gate_ab;
 } LisaGdnParams;
 

@@ -904,11 +904,12 @@ DEV void qmv_body(const LisaQmvParams& p, unsigned char* lds) {
 #pragma unroll
       for (int m = 0; m < M; ++m) { G0[m] = 0.0f; G1[m] = 0.0f; }
       group_dot2<C::ROWBYTES, C::G, M>(lds, tid, a0, b0, a1, b1, s0, s1, gsum, G0, G1);
+      // lane (tid & 15)'s slot: a's five groups, then b's
 #pragma unroll
       for (int m = 0; m < M; ++m) {
-        float* dst = p.gate_ab + (((size_t)m * LISA_GDN_VH + hh) * 2) * C::G + tid;
+        float* dst = p.gate_ab + ((size_t)m * LISA_GDN_VH + hh) * LISA_GDN_GATE_FLOATS + 12 * (tid & 15) + (tid >> 4);
         dst[0] = G0[m];
-        dst[C::G] = G1[m];
+        dst[5] = G1[m];
       }
     }
   }
@@ -1057,15 +1058,15 @@ DEV void gdn_body(const LisaGdnParams& p) {
     if (!gsrc) {
       braw[t] = p.b[(size_t)t * LISA_GDN_VH + h];
       araw[t] = p.a[(size_t)t * LISA_GDN_VH + h];
-    } else {
+    } else if (wave == 2) {
       // the in-projection's group contributions for lane li's groups
-      // li, 16 + li, .., 64 + li (summed below, once the state loads are out)
-      const float* ga = p.gate_ab + (((size_t)t * LISA_GDN_VH + h) * 2) * (LISA_HIDDEN / 64) + (lane & 15);
-#pragma unroll
-      for (int i = 0; i < 5; ++i) {
-        gav[t][i] = ga[16 * i];
-        gbv[t][i] = ga[LISA_HIDDEN / 64 + 16 * i];
-      }
+      // li, 16 + li, .., 64 + li (summed below, once the state loads are out);
+      // only wave 2 forms the gates
+      const float4* ga = reinterpret_cast<const float4*>(
+          p.gate_ab + ((size_t)t * LISA_GDN_VH + h) * LISA_GDN_GATE_FLOATS + 12 * (lane & 15));
+      const float4 g0 = ga[0], g1 = ga[1], g2 = ga[2];
+      gav[t][0] = g0.x; gav[t][1] = g0.y; gav[t][2] = g0.z; gav[t][3] = g0.w; gav[t][4] = g1.x;
+      gbv[t][0] = g1.y; gbv[t][1] = g1.z; gbv[t][2] = g1.w; gbv[t][3] = g2.x; gbv[t][4] = g2.y;
     }
   }
   if (tid < 128) nwt = bf2f(p.norm_w[tid]);
@@ -1078,7 +1079,7 @@ DEV void gdn_body(const LisaGdnParams& p) {
     S[4 * i] = f.x; S[4 * i + 1] = f.y; S[4 * i + 2] = f.z; S[4 * i + 3] = f.w;
   }
   __builtin_amdgcn_sched_barrier(0);
-  if (gsrc) {
+  if (gsrc && wave == 2) {
     // a and b as a q4 launch forms a row: lane li adds its five group
     // contributions to a running sum from 0 in order, then tree16 (thread 128,
     // lane 0 of wave 2, forms the gates from them)

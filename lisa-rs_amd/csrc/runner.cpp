@@ -341,7 +341,7 @@ void plan_ctx(LisaRunner* r, Arena& A, Ctx& c, int rows) {
   c.z = A.take<float>((size_t)rows * LISA_GDN_VALUE_DIM);
   c.a = A.take<float>((size_t)rows * LISA_GDN_VH);
   c.b = A.take<float>((size_t)rows * LISA_GDN_VH);
-  c.gate_ab = A.take<float>((size_t)rows * LISA_GDN_VH * 2 * (LISA_HIDDEN / 64));
+  c.gate_ab = A.take<float>((size_t)rows * LISA_GDN_VH * LISA_GDN_GATE_FLOATS);
   c.gated = A.take<uint16_t>((size_t)rows * LISA_ATT_OUT);
   c.act = A.take<uint16_t>((size_t)rows * LISA_INTER);
   c.q_proj = A.take<float>((size_t)rows * LISA_ATT_Q_OUT);

@@ -231,7 +231,7 @@ def test_gdn_layer_config1(pkg, orc, dev, M):
     p.capture = 1 if M == 3 else 0
     # the decoder's in-projection: qkv and z tiles; a and b as per-group
     # contributions formed by the first 48 workgroups
-    gab = dev.buffer(M * 48 * 2 * 80 * 4)
+    gab = dev.buffer(M * 48 * 192 * 4)  # LISA_GDN_GATE_FLOATS per (row, head)
     p.gate_a_w, p.gate_a_sb, p.gate_b_w, p.gate_b_sb = qd["a"].wbuf.ptr, qd["a"].sbbuf.ptr, qd["b"].wbuf.ptr, qd["b"].sbbuf.ptr
     p.gate_ab = gab.ptr
     launch_qmv(pkg, dev, K, M, p, [(qd["qkv"], None, co.ptr, pkg.EPI_CONV), (qd["z"], None, zb.ptr, pkg.EPI_STORE)])
