@@ -127,6 +127,21 @@ typedef struct LisaGdnParams {
    * contributions gate_ab[m][h][LISA_GDN_GATE_FLOATS] (see LisaQmvParams.gate_ab)
    * and the a, b fields are unused. */
   const float* gate_ab;
+  /* Decode: workgroups past the 48 heads (a grid of 48 + 8 n, n >= 1) only
+   * load the 8-row q4 tiles of the next launch's matrix (W u32[rows][pf_k/8],
+   * SB u32[rows][pf_k/64]; pf_tiles tiles, at most 32 n; pf_k a multiple of 64,
+   * at most 7168), tile t by a workgroup on XCD t mod 8, the XCD whose L2 serves
+   * that launch's workgroup t. pf_sink (4 bytes) receives a checksum of the
+   * loaded words only if it equals a fixed value. The prefetch workgroups
+   * first sleep pf_delay x 512 cycles (at most 64), so that the heads' state
+   * loads go out first. */
+  const uint32_t* pf_w;
+  const uint32_t* pf_sb;
+  uint32_t* pf_sink;
+  uint32_t pf_tiles;
+  uint32_t pf_k;
+  uint32_t pf_delay;
+  uint32_t pad0;
 } LisaGdnParams;
 
 /* ---- split-K decode attention --------------------------------------------

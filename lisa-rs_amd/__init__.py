@@ -81,7 +81,8 @@ class GdnParams(C.Structure):
                 ("state", C.c_uint64), ("slots", C.c_uint64), ("slot_stride", C.c_uint64),
                 ("gated", C.c_uint64), ("y_out", C.c_uint64), ("q_scale", C.c_float), ("k_scale", C.c_float),
                 ("capture", C.c_uint32), ("m_rows", C.c_uint32), ("qk", C.c_uint64), ("gates", C.c_uint64),
-                ("gate_ab", C.c_uint64)]
+                ("gate_ab", C.c_uint64), ("pf_w", C.c_uint64), ("pf_sb", C.c_uint64), ("pf_sink", C.c_uint64),
+                ("pf_tiles", C.c_uint32), ("pf_k", C.c_uint32), ("pf_delay", C.c_uint32), ("pad0", C.c_uint32)]
 
 
 class AttnParams(C.Structure):

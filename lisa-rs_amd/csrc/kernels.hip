@@ -1028,7 +1028,41 @@ DEV uint16_t gdn_gated(float y, float rinv, float nw, float zraw) {
   return lisa_f32_to_bf16(n * lisa_silu_exp(z));
 }
 
-template <int M>
+// Workgroups past the heads: the next q4 launch's 8-row tiles into the L2 of
+// the XCD that launch's workgroup t runs on (workgroups go to the 8 XCDs
+// round-robin by id, and the recurrence leaves the memory system mostly idle).
+// Every load is issued before any is used; a tile is its pf_k / 4 W chunks
+// and pf_k / 32 SB chunks of 16 bytes, at most 4 x 512.
+typedef uint32_t lisa_u32x4 __attribute__((ext_vector_type(4)));
+DEV void gdn_l2_prefetch(const LisaGdnParams& p) {
+  constexpr int MAXT = 4;
+  const uint32_t j = blockIdx.x - LISA_GDN_VH, x = j & 7, k = j >> 3, per = (gridDim.x - LISA_GDN_VH) >> 3;
+  const uint32_t wq = p.pf_k / 4, sq = p.pf_k / 32;
+  const uint4* w = reinterpret_cast<const uint4*>(p.pf_w);
+  const uint4* sb = reinterpret_cast<const uint4*>(p.pf_sb);
+  for (uint32_t i = 0; i < min(p.pf_delay, 64u); ++i) __builtin_amdgcn_s_sleep(8);
+  lisa_u32x4 v[MAXT][4];
+#pragma unroll
+  for (int n = 0; n < MAXT; ++n) {
+    const uint32_t t = x + 8 * (k + n * per);
+    const bool ok = t < p.pf_tiles;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const uint32_t i = min(threadIdx.x + 512u * r, wq + sq - 1);
+      const uint4* src = i < wq ? w + (size_t)t * wq + i : sb + (size_t)t * sq + (i - wq);
+      v[n][r] = ok ? *reinterpret_cast<const lisa_u32x4*>(src) : lisa_u32x4{0, 0, 0, 0};
+    }
+  }
+  uint32_t acc = 0;
+#pragma unroll
+  for (int n = 0; n < MAXT; ++n)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) acc ^= v[n][r].x ^ v[n][r].y ^ v[n][r].z ^ v[n][r].w;
+  if (acc == 0x2545f491u) p.pf_sink[0] = acc;
+}
+
+// GSRC: a and b come from the in-projection's group contributions (gate_ab).
+template <int M, bool GSRC>
 DEV void gdn_body(const LisaGdnParams& p) {
   const int rows = M;
   const int h = blockIdx.x, kh = h / (LISA_GDN_VH / LISA_GDN_KH);
@@ -1038,30 +1072,29 @@ DEV void gdn_body(const LisaGdnParams& p) {
   // first (q on wave 0 / k on wave 1 of the key head, the state row's v value,
   // z and the norm weight; the gate inputs are uniform, scalar loads), then
   // the 128 B of state this thread owns, so the norms and gates are formed
-  // while the state arrives.
+  // while the state arrives. None of these loads sits behind a branch: where
+  // a branch merges loaded registers, the compiler waits for the loads, which
+  // put a whole memory round trip in front of the state loads. Threads that
+  // do not use a value load an in-bounds copy of it instead.
   float c0[M], c1[M], vval[M], zraw[M], braw[M], araw[M];
   float gav[M][5], gbv[M][5];
-  const bool gsrc = p.gate_ab != nullptr;
-  float nwt = 0.0f;
 #pragma unroll
   for (int t = 0; t < M; ++t) {
     const float* co = p.conv_out + (size_t)t * LISA_GDN_CONV_DIM;
-    const float* src = co + (wave == 0 ? 0 : LISA_GDN_KEY_DIM) + kh * 128;
-    c0[t] = 0.0f;
-    c1[t] = 0.0f;
-    if (wave < 2) { c0[t] = src[lane]; c1[t] = src[lane + 64]; }
+    const float* src = co + ((wave & 1) ? LISA_GDN_KEY_DIM : 0) + kh * 128;
+    c0[t] = src[lane];
+    c1[t] = src[lane + 64];
     vval[t] = co[2 * LISA_GDN_KEY_DIM + h * 128 + v];
-    zraw[t] = 0.0f;
-    if (tid < 128) zraw[t] = p.z[(size_t)t * LISA_GDN_VALUE_DIM + h * 128 + tid];
+    zraw[t] = p.z[(size_t)t * LISA_GDN_VALUE_DIM + h * 128 + (tid & 127)];
     braw[t] = 0.0f;
     araw[t] = 0.0f;
-    if (!gsrc) {
+    if constexpr (!GSRC) {
       braw[t] = p.b[(size_t)t * LISA_GDN_VH + h];
       araw[t] = p.a[(size_t)t * LISA_GDN_VH + h];
-    } else if (wave == 2) {
+    } else {
       // the in-projection's group contributions for lane li's groups
-      // li, 16 + li, .., 64 + li (summed below, once the state loads are out);
-      // only wave 2 forms the gates
+      // li, 16 + li, .., 64 + li (summed below by wave 2, once the state loads
+      // are out)
       const float4* ga = reinterpret_cast<const float4*>(
           p.gate_ab + ((size_t)t * LISA_GDN_VH + h) * LISA_GDN_GATE_FLOATS + 12 * (lane & 15));
       const float4 g0 = ga[0], g1 = ga[1], g2 = ga[2];
@@ -1069,7 +1102,7 @@ DEV void gdn_body(const LisaGdnParams& p) {
       gbv[t][0] = g1.y; gbv[t][1] = g1.z; gbv[t][2] = g1.w; gbv[t][3] = g2.x; gbv[t][4] = g2.y;
     }
   }
-  if (tid < 128) nwt = bf2f(p.norm_w[tid]);
+  const float nwt = bf2f(p.norm_w[tid & 127]);
   __builtin_amdgcn_sched_barrier(0);
   float* srow = p.state + (size_t)h * 128 * 128 + (size_t)v * 128;
   float S[32];
@@ -1079,7 +1112,7 @@ DEV void gdn_body(const LisaGdnParams& p) {
     S[4 * i] = f.x; S[4 * i + 1] = f.y; S[4 * i + 2] = f.z; S[4 * i + 3] = f.w;
   }
   __builtin_amdgcn_sched_barrier(0);
-  if (gsrc && wave == 2) {
+  if (GSRC && wave == 2) {
     // a and b as a q4 launch forms a row: lane li adds its five group
     // contributions to a running sum from 0 in order, then tree16 (thread 128,
     // lane 0 of wave 2, forms the gates from them)
@@ -1278,8 +1311,19 @@ extern "C" __global__ __launch_bounds__(128) void lisa_gdn_out_rows(LisaGdnParam
   p.gated[o + tid] = gdn_gated(y, rinv, nwt, zraw);
 }
 
-extern "C" __global__ __launch_bounds__(512) void lisa_gdn_recurrence_m1(LisaGdnParams p) { gdn_body<1>(p); }
-extern "C" __global__ __launch_bounds__(512) void lisa_gdn_recurrence_m3(LisaGdnParams p) { gdn_body<3>(p); }
+// Workgroups 0..47: one value head each; past them, L2 prefetch of the next
+// launch's weights.
+template <int M>
+DEV void gdn_entry(const LisaGdnParams& p) {
+  if (blockIdx.x >= LISA_GDN_VH) {
+    if (p.pf_w) gdn_l2_prefetch(p);
+    return;
+  }
+  if (p.gate_ab) gdn_body<M, true>(p);
+  else gdn_body<M, false>(p);
+}
+extern "C" __global__ __launch_bounds__(512) void lisa_gdn_recurrence_m1(LisaGdnParams p) { gdn_entry<1>(p); }
+extern "C" __global__ __launch_bounds__(512) void lisa_gdn_recurrence_m3(LisaGdnParams p) { gdn_entry<3>(p); }
 
 // ===========================================================================
 // split-K decode attention

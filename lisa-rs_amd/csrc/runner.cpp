@@ -63,7 +63,7 @@ struct Ctx {
   int rows = 1;
   uint16_t *H, *gated, *act, *xnorm, *cond;  // H: residual rows, updated in place
   float *B, *conv_out, *z, *a, *b, *gate_ab, *q_proj, *k_raw, *v_raw, *part_o, *part_ml, *logits, *am_val;
-  uint32_t *am_idx, *tokens, *argmax, *pos, *step, *history;
+  uint32_t *am_idx, *tokens, *argmax, *pos, *step, *history, *pf_sink;
 };
 
 size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
@@ -93,6 +93,12 @@ struct LisaCheckpoint {
 struct LisaRunner {
   LisaRunnerConfig cfg{};
   LisaDevice* dev = nullptr;
+  // GDN recurrence launches carry L2 prefetch workgroups for the out_proj
+  // weights, l2_prefetch per XCD (environment LISA_L2_PREFETCH, 0 = none,
+  // else 20..26), after a sleep of l2_prefetch_delay x 512 cycles
+  // (LISA_L2_PREFETCH_DELAY)
+  uint32_t l2_prefetch = 20;
+  uint32_t l2_prefetch_delay = 0;
   LisaModule* mod = nullptr;
   // kernels
   LisaFunction *qmv[2][5][7] = {};  // [m3][K index][prologue mode]
@@ -359,6 +365,7 @@ void plan_ctx(LisaRunner* r, Arena& A, Ctx& c, int rows) {
   c.pos = A.take<uint32_t>(4);
   c.step = A.take<uint32_t>(4);
   c.history = A.take<uint32_t>(kHistoryCap);
+  c.pf_sink = A.take<uint32_t>(64);
 }
 
 // ---- launch helpers --------------------------------------------------------------
@@ -540,8 +547,22 @@ int encode_target(LisaRunner* r, int m, bool capture, bool feedback) {
       g.q_scale = inv * inv;
       g.k_scale = inv;
       g.capture = capture ? 1 : 0;
+      // more workgroups per XCD load the out_proj's 640 tiles (4 each at most)
+      // into the L2 that its workgroups will read them from
+      uint32_t grid = LISA_GDN_VH;
+      if (r->l2_prefetch) {
+        g.pf_w = l.out.w;
+        g.pf_sb = l.out.sb;
+        g.pf_sink = c.pf_sink;
+        g.pf_tiles = l.out.n / 8;
+        g.pf_k = l.out.k;
+        g.pf_delay = r->l2_prefetch_delay;
+        grid += 8 * r->l2_prefetch;
+        if (g.pf_tiles > 32 * r->l2_prefetch || l.out.k % 64 != 0 || l.out.k > 7168)
+          return lisa_fail(LISA_E_ARG, "out_proj of %u x %u does not fit the prefetch workgroups", l.out.n, l.out.k);
+      }
       LISA_TRY(prof_mark(r, LISA_KIND_GDN_RECURRENCE));
-      LISA_TRY(lisa_launch(r->dev, r->gdn[m == 3 ? 1 : 0], &g, sizeof g, LISA_GDN_VH, 1, 1, 512, 1, 1));
+      LISA_TRY(lisa_launch(r->dev, r->gdn[m == 3 ? 1 : 0], &g, sizeof g, grid, 1, 1, 512, 1, 1));
       LISA_TRY(prof_mark(r, LISA_KIND_GDN_OUT));
       LISA_TRY(launch_resid(r, c, m, LISA_GDN_VALUE_DIM, c.gated, l.out));
     } else {
@@ -671,6 +692,11 @@ extern "C" int lisa_runner_create(const LisaRunnerConfig* cfg, LisaRunner** out)
   if (cfg->capacity > 64 * 1024) return lisa_fail(LISA_E_ARG, "KV capacity above 65536 is not supported");
   std::unique_ptr<LisaRunner> r(new LisaRunner());
   r->cfg = *cfg;
+  if (const char* e = std::getenv("LISA_L2_PREFETCH")) {
+    const int n = std::atoi(e);
+    r->l2_prefetch = n <= 0 ? 0 : (uint32_t)std::min(std::max(n, 20), 26);
+  }
+  if (const char* e = std::getenv("LISA_L2_PREFETCH_DELAY")) r->l2_prefetch_delay = (uint32_t)std::min(std::max(std::atoi(e), 0), 64);
   LISA_TRY(lisa_device_create(cfg->device, &r->dev));
   LISA_TRY(lisa_module_load_default(r->dev, &r->mod));
   // lisa_qmv_k<K>_m<M>_<prologue>; combinations the module does not hold stay null
