@@ -248,21 +248,27 @@ def test_gdn_layer_config1(pkg, orc, dev, M):
 
     al, dtb, gn = dev.upload(a_log), dev.upload(dt_bias), dev.upload(gnorm)
     inv = np.float32(1.0) / np.sqrt(np.float32(128.0))
+    oq, sink = DevQ4(dev, ow, osc, ob), dev.buffer(256)
     for source in ("contributions", "tiles"):
         stb = dev.upload(state)
         gslot = dev.buffer(2 * 48 * 128 * 128 * 4)
         gb = dev.buffer(M * 6144 * 2)
         g = pkg.GdnParams()
         g.conv_out, g.z = co.ptr, zb.ptr
+        grid = 48
         if source == "contributions":
             g.gate_ab = gab.ptr
+            # as the decoder launches it: 20 workgroups per XCD past the heads
+            # prefetch the out_proj tiles (they compute nothing)
+            g.pf_w, g.pf_sb, g.pf_sink = oq.wbuf.ptr, oq.sbbuf.ptr, sink.ptr
+            g.pf_tiles, g.pf_k, grid = 5120 // 8, 6144, 48 + 8 * 20
         else:
             g.a, g.b = ab.ptr, bb.ptr
         g.a_log, g.dt_bias, g.norm_w = al.ptr, dtb.ptr, gn.ptr
         g.state, g.slots, g.slot_stride, g.gated = stb.ptr, gslot.ptr, 48 * 128 * 128, gb.ptr
         g.q_scale, g.k_scale = float(inv * inv), float(inv)
         g.capture = 1 if M == 3 else 0
-        dev.dispatch(f"lisa_gdn_recurrence_m{M}", g, (48,), (512,))
+        dev.dispatch(f"lisa_gdn_recurrence_m{M}", g, (grid,), (512,))
         assert np.array_equal(gb.read(np.uint16, M * 6144).reshape(M, 6144), gated), source
         assert same_bits(stb.read(np.float32, 48 * 128 * 128), st_want), source
     if M == 3:
@@ -276,7 +282,7 @@ def test_gdn_layer_config1(pkg, orc, dev, M):
     po = pkg.QmvParams()
     po.pro_mode = pkg.PRO_LOADX
     po.x_in = gb.ptr
-    launch_qmv(pkg, dev, 6144, M, po, [(DevQ4(dev, ow, osc, ob), None, outb.ptr, pkg.EPI_STORE)])
+    launch_qmv(pkg, dev, 6144, M, po, [(oq, None, outb.ptr, pkg.EPI_STORE)])
     assert same_bits(outb.read(np.float32, M * 5120).reshape(M, 5120), branch)
 
 
