@@ -21,9 +21,11 @@
  * One launch covers up to 4 matrices that share the input x; the virtual row
  * space is split into 8-row tiles, each matrix owning a contiguous tile range
  * [tile_start[e], tile_start[e+1]), tile_start[n_mats] the total.
- * ksplit is 4 when the launch has at most
- * 8192 virtual rows (the N=5120 projections), else 1: a fixed rule, so the
- * summation order of every output is a function of the launch shape. */
+ * ksplit is 4 for K != 5120 (the kernels lisa_qmv_k{6144,10240,17408}_*: one
+ * tile per workgroup, its group iterations split over the 4 waves; these are
+ * the projections back to the 5120-row residual) and 1 for K = 5120 (one tile
+ * per wave): a fixed rule, so the summation order of every output is a
+ * function of K. */
 #define LISA_QMV_MAX_MATS 4
 
 enum {

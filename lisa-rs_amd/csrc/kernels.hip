@@ -964,7 +964,6 @@ QMV_KERNEL_EPI(5120, 3, LISA_PRO_PRENORM, prenorm, LISA_EPI_ARGMAX, argmax)
 // thread (v, q) = (tid/4, tid%4) owns the runs q, q+4, q+8, q+12 of 8 of state
 // row v (gdn_row_step_il).
 // ===========================================================================
-// M = 0: the row count comes from p.m_rows (prefill).
 // q or k of one key head (gdn.metal q/k norm): RMS over 128 values as tree64 of
 // c0^2 + c1^2 (lane l holds c[l], c[l+64]), scaled, rounded to bf16.
 DEV void gdn_qk_norm(float c0, float c1, float scale, float& n0, float& n1) {
