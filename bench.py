@@ -251,7 +251,8 @@ def speculative_phase(pkg, steps=128, p_accept=0.6, seed=0x5EED):
     return {"speculative_decode_tok_s": round(steps / (ms.value / 1e3), 2),
             "acceptance": round(st["accepted_drafts"] / max(1, st["drafted_tokens"]), 4),
             "tokens": steps, "rounds": st["rounds"], "target_forwards": st["target_forwards"],
-            "exact_match": bool(list(toks) == truth), "p_accept_forced": p_accept}
+            "exact_match": bool(list(toks) == truth), "p_accept_forced": p_accept,
+            "_tokens": [int(t) for t in toks]}
 
 
 GEMM_SHAPES = [(2048, INTER, HIDDEN, "mlp gate (and up)"), (2048, HIDDEN, INTER, "mlp down"),
@@ -480,10 +481,27 @@ def main():
             "kind": "port",
             "sample": f"{args.cpu_steps} M=1 decode steps of the full 64-layer model at ctx {CTX} "
                       f"(same weights, context and first token as the GPU run)"}
-        result["exact_match"] = bool(list(tokens[: args.cpu_steps]) == cpu_tokens)
-        print(f"[bench] cpu {cpu_tok_s:.3f} tok/s; tokens gpu {list(tokens[:args.cpu_steps])} "
-              f"cpu {cpu_tokens}", file=sys.stderr, flush=True)
+        # argmax-exact over the tokens both sides produced (the GPU's timed
+        # region decoded K of them, the oracle cpu_steps)
+        n_cmp = min(len(tokens), len(cpu_tokens))
+        gpu_head = [int(t) for t in tokens[:n_cmp]]
+        result["exact_match"] = bool(n_cmp > 0 and gpu_head == cpu_tokens[:n_cmp])
+        result["exact_match_tokens"] = n_cmp
+        if "speculative" in result:
+            # the speculative stream starts from the same state and first token
+            spec_head = result["speculative"].pop("_tokens")[:n_cmp]
+            result["speculative"]["exact_match_oracle"] = bool(spec_head == cpu_tokens[:len(spec_head)])
+        print(f"[bench] cpu {cpu_tok_s:.3f} tok/s; first {n_cmp} tokens gpu {gpu_head} cpu {cpu_tokens[:n_cmp]}",
+              file=sys.stderr, flush=True)
+    if "speculative" in result:
+        result["speculative"].pop("_tokens", None)
     print(json.dumps(result), flush=True)
+    mismatch = [k for k in ("exact_match",) if result.get(k) is False]
+    if "speculative" in result:
+        mismatch += [k for k in ("exact_match", "exact_match_oracle") if result["speculative"].get(k) is False]
+    if mismatch:
+        print(f"bench.py: token mismatch ({', '.join(mismatch)})", file=sys.stderr, flush=True)
+        sys.exit(1)
 
 
 if __name__ == "__main__":

@@ -183,7 +183,9 @@ int lisa_runner_verify_block3(LisaRunner* r, const uint32_t tokens[3], uint32_t 
 /* commit_verified_prefix (runner.rs:911-944): rows in 1..3. */
 int lisa_runner_commit_verified_prefix(LisaRunner* r, int32_t rows);
 
-/* checkpoint_state / restore_state (runner.rs:447-503). */
+/* checkpoint_state / restore_state (runner.rs:447-503). Restore rejects a
+ * position past the KV capacity (LISA_E_CAPACITY) and a checkpoint taken on a
+ * runner with another number of GDN layers (LISA_E_ARG). */
 typedef struct LisaCheckpoint LisaCheckpoint;
 int lisa_runner_checkpoint_state(LisaRunner* r, LisaCheckpoint** out);
 int lisa_runner_restore_state(LisaRunner* r, const LisaCheckpoint* ck);
@@ -213,6 +215,15 @@ int lisa_mtp_upload_cond(LisaRunner* r, const uint16_t* hidden);
 int lisa_mtp_read_normalized(LisaRunner* r, uint16_t* out);
 uint32_t lisa_mtp_position(LisaRunner* r);
 int lisa_mtp_trim_state(LisaRunner* r, int32_t count);
+
+/* MtpRunner::checkpoint_state / restore_state (runner.rs:2382-2420): device
+ * copies of the drafter's KV caches and its position. Restore rejects a
+ * checkpoint position past the capacity (LISA_E_CAPACITY, as the reference
+ * does) and a checkpoint of another capacity (LISA_E_ARG). */
+typedef struct LisaMtpCheckpoint LisaMtpCheckpoint;
+int lisa_mtp_checkpoint_state(LisaRunner* r, LisaMtpCheckpoint** out);
+int lisa_mtp_restore_state(LisaRunner* r, const LisaMtpCheckpoint* ck);
+void lisa_mtp_checkpoint_free(LisaMtpCheckpoint* ck);
 
 /* ========================= speculative (speculative/mod.rs) ============== */
 typedef struct LisaAcceptance {

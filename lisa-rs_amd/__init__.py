@@ -214,6 +214,9 @@ _SIGS = {
     "lisa_mtp_read_normalized": (C.c_int, [_P, _P]),
     "lisa_mtp_position": (C.c_uint32, [_P]),
     "lisa_mtp_trim_state": (C.c_int, [_P, C.c_int32]),
+    "lisa_mtp_checkpoint_state": (C.c_int, [_P, C.POINTER(_P)]),
+    "lisa_mtp_restore_state": (C.c_int, [_P, _P]),
+    "lisa_mtp_checkpoint_free": (None, [_P]),
     "lisa_accept_greedy": (C.c_int, [_P, C.c_int32, _P, C.POINTER(Acceptance)]),
     "lisa_mtp_reconcile_plan": (C.c_int, [C.c_int32, C.c_int32, C.c_int32, C.POINTER(ReconcilePlan)]),
     "lisa_generate_greedy_block3": (C.c_int, [_P, C.c_uint32, _P, C.c_uint32, _P, C.c_int32, _P, C.c_int32,
@@ -503,6 +506,19 @@ class Runner:
 
     def mtp_trim_state(self, count: int) -> None:
         _check(lib().lisa_mtp_trim_state(self.h, count))
+
+    def mtp_checkpoint_state(self):
+        """MtpRunner::checkpoint_state (runner.rs:2382-2398)."""
+        ck = C.c_void_p()
+        _check(lib().lisa_mtp_checkpoint_state(self.h, C.byref(ck)))
+        return ck
+
+    def mtp_restore_state(self, ck) -> None:
+        """MtpRunner::restore_state (runner.rs:2400-2420)."""
+        _check(lib().lisa_mtp_restore_state(self.h, ck))
+
+    def free_mtp_checkpoint(self, ck) -> None:
+        lib().lisa_mtp_checkpoint_free(ck)
 
     def generate_greedy_block3(self, bonus: int, target_hidden: np.ndarray, mtp_seed_token: int,
                                mtp_seed_hidden: np.ndarray, max_tokens: int, force_truth=None,

@@ -1790,6 +1790,7 @@ DEV void q4_gemm_body(const LisaGemmParams& p, uint16_t (*As)[GEMM_BM * GEMM_PAD
     GEMM_GLOAD(a0, w0, sb0, step + 2);
     gemm_step<BN, NT>(As[0], Ws[0], As[1], Ws[1], tid, wm, wn, lane, a1, w1, sb1, acc);
     __syncthreads();
+    if (step + 1 >= nk) break;  // odd number of K steps: the last one is done
     GEMM_GLOAD(a1, w1, sb1, step + 3);
     gemm_step<BN, NT>(As[1], Ws[1], As[0], Ws[0], tid, wm, wn, lane, a0, w0, sb0, acc);
     __syncthreads();

@@ -88,6 +88,17 @@ struct LisaCheckpoint {
   LisaBuffer* gdn = nullptr;
   LisaBuffer* conv = nullptr;
   uint32_t position = 0;
+  // geometry of the runner that took it: a restore into a runner of another
+  // depth would copy past its state arenas
+  int32_t gdn_layers = 0;
+};
+
+// MtpCheckpoint (runner.rs:2375-2380): the drafter's KV caches and position.
+struct LisaMtpCheckpoint {
+  LisaBuffer* key = nullptr;
+  LisaBuffer* value = nullptr;
+  uint32_t position = 0;
+  int32_t capacity = 0;
 };
 
 struct LisaRunner {
@@ -973,6 +984,7 @@ extern "C" int lisa_runner_checkpoint_state(LisaRunner* r, LisaCheckpoint** out)
   LISA_TRY(lisa_hip_check(hipMemcpyAsync(ck->conv->ptr, r->conv_state, cs, hipMemcpyDeviceToDevice, r->dev->stream), "D2D"));
   LISA_TRY(sync(r));
   ck->position = r->position;
+  ck->gdn_layers = r->gdn_layers;
   *out = ck.release();
   return LISA_OK;
 }
@@ -981,6 +993,10 @@ extern "C" int lisa_runner_restore_state(LisaRunner* r, const LisaCheckpoint* ck
   if (!r || !ck) return lisa_fail(LISA_E_ARG, "lisa_runner_restore_state: bad argument");
   if (ck->position > (uint32_t)r->cfg.capacity)
     return lisa_fail(LISA_E_CAPACITY, "checkpoint position %u exceeds KV capacity %d", ck->position, r->cfg.capacity);
+  const size_t gs = (size_t)r->gdn_layers * LISA_GDN_STATE * 4, cs = (size_t)r->gdn_layers * 3 * LISA_GDN_CONV_DIM * 2;
+  if (ck->gdn_layers != r->gdn_layers || !ck->gdn || !ck->conv || ck->gdn->len != gs || ck->conv->len != cs)
+    return lisa_fail(LISA_E_ARG, "checkpoint of %d GDN layers does not fit a runner of %d", ck->gdn_layers,
+                     r->gdn_layers);
   LISA_TRY(lisa_hip_check(hipMemcpyAsync(r->gdn_state, ck->gdn->ptr, ck->gdn->len, hipMemcpyDeviceToDevice, r->dev->stream), "D2D"));
   LISA_TRY(lisa_hip_check(hipMemcpyAsync(r->conv_state, ck->conv->ptr, ck->conv->len, hipMemcpyDeviceToDevice, r->dev->stream), "D2D"));
   r->position = ck->position;
@@ -1081,6 +1097,58 @@ extern "C" int lisa_mtp_trim_state(LisaRunner* r, int32_t count) {
   r->mtp_position -= (uint32_t)count;
   LISA_TRY(write_pos(r, r->drf, r->mtp_position));
   return sync(r);
+}
+
+// MtpRunner::checkpoint_state / restore_state (runner.rs:2382-2420): the
+// drafter's KV caches (device-to-device copies of the whole capacity) and its
+// logical position.
+extern "C" int lisa_mtp_checkpoint_state(LisaRunner* r, LisaMtpCheckpoint** out) {
+  if (!r || !out) return lisa_fail(LISA_E_ARG, "lisa_mtp_checkpoint_state: bad argument");
+  if (!r->cfg.with_mtp) return lisa_fail(LISA_E_STATE, "runner was created without the MTP drafter");
+  const size_t len = (size_t)LISA_ATT_KVH * r->cfg.capacity * LISA_ATT_HD * 2;
+  std::unique_ptr<LisaMtpCheckpoint> ck(new LisaMtpCheckpoint());
+  auto release = [](LisaMtpCheckpoint* c) {
+    lisa_buffer_free(c->key);
+    lisa_buffer_free(c->value);
+    c->key = c->value = nullptr;
+  };
+  int rc = lisa_buffer_alloc(r->dev, len, &ck->key);
+  if (!rc) rc = lisa_buffer_alloc(r->dev, len, &ck->value);
+  if (!rc) rc = lisa_hip_check(hipMemcpyAsync(ck->key->ptr, r->mtp_key, len, hipMemcpyDeviceToDevice, r->dev->stream), "D2D");
+  if (!rc)
+    rc = lisa_hip_check(hipMemcpyAsync(ck->value->ptr, r->mtp_value, len, hipMemcpyDeviceToDevice, r->dev->stream), "D2D");
+  if (!rc) rc = sync(r);
+  if (rc) {
+    release(ck.get());
+    return rc;
+  }
+  ck->position = r->mtp_position;
+  ck->capacity = r->cfg.capacity;
+  *out = ck.release();
+  return LISA_OK;
+}
+
+extern "C" int lisa_mtp_restore_state(LisaRunner* r, const LisaMtpCheckpoint* ck) {
+  if (!r || !ck) return lisa_fail(LISA_E_ARG, "lisa_mtp_restore_state: bad argument");
+  if (!r->cfg.with_mtp) return lisa_fail(LISA_E_STATE, "runner was created without the MTP drafter");
+  if (ck->position > (uint32_t)r->cfg.capacity)
+    return lisa_fail(LISA_E_CAPACITY, "MTP checkpoint position %u exceeds capacity %d", ck->position, r->cfg.capacity);
+  const size_t len = (size_t)LISA_ATT_KVH * r->cfg.capacity * LISA_ATT_HD * 2;
+  if (ck->capacity != r->cfg.capacity || !ck->key || !ck->value || ck->key->len != len || ck->value->len != len)
+    return lisa_fail(LISA_E_ARG, "MTP checkpoint of capacity %d does not fit a runner of capacity %d", ck->capacity,
+                     r->cfg.capacity);
+  LISA_TRY(lisa_hip_check(hipMemcpyAsync(r->mtp_key, ck->key->ptr, len, hipMemcpyDeviceToDevice, r->dev->stream), "D2D"));
+  LISA_TRY(lisa_hip_check(hipMemcpyAsync(r->mtp_value, ck->value->ptr, len, hipMemcpyDeviceToDevice, r->dev->stream), "D2D"));
+  r->mtp_position = ck->position;
+  LISA_TRY(write_pos(r, r->drf, r->mtp_position));
+  return sync(r);
+}
+
+extern "C" void lisa_mtp_checkpoint_free(LisaMtpCheckpoint* ck) {
+  if (!ck) return;
+  lisa_buffer_free(ck->key);
+  lisa_buffer_free(ck->value);
+  delete ck;
 }
 
 // =============================================================================

@@ -349,28 +349,74 @@ void orc_q4_linear(const uint16_t* x, const uint32_t* w, const uint16_t* scales,
 // is the hardware's, so its results are compared with a tolerance).
 void orc_q4_gemm(const uint16_t* a, const uint32_t* w, const uint16_t* scales, const uint16_t* biases, int n_rows,
                  int k, int m_rows, float* out) {
+  // Output (m, n) is four double lanes, lane j summing a[k'] * wd[k'] over
+  // k' = j mod 4 in ascending order, then (l0 + l1) + (l2 + l3). A product of
+  // two floats is exact in double, so the fused multiply-adds below equal a
+  // multiply followed by a rounded add; blocks of 4 weight rows x 3 input rows
+  // keep the operands in registers.
   const int wpr = k / 8, groups = k / 64;
   std::vector<float> af((size_t)m_rows * k);
   for (size_t i = 0; i < af.size(); ++i) af[i] = bf(a[i]);
+  auto hsum = [](__m256d v) {
+    alignas(32) double l[4];
+    _mm256_store_pd(l, v);
+    return (float)((l[0] + l[1]) + (l[2] + l[3]));
+  };
+  const int nblocks = (n_rows + 3) / 4;
 #pragma omp parallel
   {
-    std::vector<float> wd(k);
-#pragma omp for schedule(static)
-    for (int n = 0; n < n_rows; ++n) {
-      for (int g = 0; g < groups; ++g) {
-        const float sc = bf(scales[(size_t)n * groups + g]), bi = bf(biases[(size_t)n * groups + g]);
-        for (int e = 0; e < 64; ++e) {
-          const int kk = 64 * g + e;
-          const uint32_t q = (w[(size_t)n * wpr + kk / 8] >> (4 * (kk % 8))) & 0xfu;
-          wd[kk] = bfr(lisa_fma(sc, (float)q, bi));
+    std::vector<double> wd((size_t)4 * k);
+#pragma omp for schedule(dynamic, 4)
+    for (int nb = 0; nb < nblocks; ++nb) {
+      const int n0 = 4 * nb, nn = std::min(4, n_rows - n0);
+      for (int j = 0; j < 4; ++j) {
+        const int n = n0 + std::min(j, nn - 1);
+        for (int g = 0; g < groups; ++g) {
+          const float sc = bf(scales[(size_t)n * groups + g]), bi = bf(biases[(size_t)n * groups + g]);
+          for (int e = 0; e < 64; ++e) {
+            const int kk = 64 * g + e;
+            const uint32_t q = (w[(size_t)n * wpr + kk / 8] >> (4 * (kk % 8))) & 0xfu;
+            wd[(size_t)j * k + kk] = (double)bfr(lisa_fma(sc, (float)q, bi));
+          }
         }
       }
-      for (int m = 0; m < m_rows; ++m) {
-        const float* ar = &af[(size_t)m * k];
-        double acc[4] = {0.0, 0.0, 0.0, 0.0};
-        for (int kk = 0; kk < k; kk += 4)
-          for (int j = 0; j < 4; ++j) acc[j] += (double)ar[kk + j] * (double)wd[kk + j];
-        out[(size_t)m * n_rows + n] = (float)((acc[0] + acc[1]) + (acc[2] + acc[3]));
+      const double* w0 = &wd[0];
+      const double* w1 = &wd[(size_t)k];
+      const double* w2 = &wd[(size_t)2 * k];
+      const double* w3 = &wd[(size_t)3 * k];
+      int m = 0;
+      for (; m + 3 <= m_rows; m += 3) {
+        const float* a0 = &af[(size_t)m * k];
+        const float* a1 = a0 + k;
+        const float* a2 = a1 + k;
+        __m256d c[3][4];
+        for (int i = 0; i < 3; ++i)
+          for (int j = 0; j < 4; ++j) c[i][j] = _mm256_setzero_pd();
+        for (int kk = 0; kk < k; kk += 4) {
+          const __m256d x0 = _mm256_loadu_pd(w0 + kk), x1 = _mm256_loadu_pd(w1 + kk);
+          const __m256d x2 = _mm256_loadu_pd(w2 + kk), x3 = _mm256_loadu_pd(w3 + kk);
+          const __m256d y0 = _mm256_cvtps_pd(_mm_loadu_ps(a0 + kk));
+          const __m256d y1 = _mm256_cvtps_pd(_mm_loadu_ps(a1 + kk));
+          const __m256d y2 = _mm256_cvtps_pd(_mm_loadu_ps(a2 + kk));
+          c[0][0] = _mm256_fmadd_pd(y0, x0, c[0][0]); c[0][1] = _mm256_fmadd_pd(y0, x1, c[0][1]);
+          c[0][2] = _mm256_fmadd_pd(y0, x2, c[0][2]); c[0][3] = _mm256_fmadd_pd(y0, x3, c[0][3]);
+          c[1][0] = _mm256_fmadd_pd(y1, x0, c[1][0]); c[1][1] = _mm256_fmadd_pd(y1, x1, c[1][1]);
+          c[1][2] = _mm256_fmadd_pd(y1, x2, c[1][2]); c[1][3] = _mm256_fmadd_pd(y1, x3, c[1][3]);
+          c[2][0] = _mm256_fmadd_pd(y2, x0, c[2][0]); c[2][1] = _mm256_fmadd_pd(y2, x1, c[2][1]);
+          c[2][2] = _mm256_fmadd_pd(y2, x2, c[2][2]); c[2][3] = _mm256_fmadd_pd(y2, x3, c[2][3]);
+        }
+        for (int i = 0; i < 3; ++i)
+          for (int j = 0; j < nn; ++j) out[(size_t)(m + i) * n_rows + n0 + j] = hsum(c[i][j]);
+      }
+      for (; m < m_rows; ++m) {
+        const float* a0 = &af[(size_t)m * k];
+        for (int j = 0; j < nn; ++j) {
+          const double* wj = &wd[(size_t)j * k];
+          __m256d c0 = _mm256_setzero_pd();
+          for (int kk = 0; kk < k; kk += 4)
+            c0 = _mm256_fmadd_pd(_mm256_cvtps_pd(_mm_loadu_ps(a0 + kk)), _mm256_loadu_pd(wj + kk), c0);
+          out[(size_t)m * n_rows + n0 + j] = hsum(c0);
+        }
       }
     }
   }
@@ -1106,6 +1152,91 @@ int orc_mtp_trim(OrcModel* M, int count) {
   if (count < 0 || (uint32_t)count > M->mtp.position) return -1;
   M->mtp.position -= count;
   return 0;
+}
+
+// Test hook: the storage of one model tensor, addressed like the synthetic
+// catalogue (scope = layer + 1, 0 for globals, LISA_SCOPE_MTP for the drafter;
+// part 0 = packed words or plain vector, 1 = scales, 2 = biases; the drafter's
+// KV caches under LISA_T_KEY_CACHE / LISA_T_VALUE_CACHE). Tests overwrite
+// weights through it to pin the wiring of the model functions.
+int orc_model_tensor(OrcModel* M, int scope, int kind, int part, void** ptr, size_t* bytes) {
+  auto q4 = [&](Q4& q) -> int {
+    if (part == 0) { *ptr = q.w.data(); *bytes = q.w.size() * 4; return 0; }
+    if (part == 1) { *ptr = q.s.data(); *bytes = q.s.size() * 2; return 0; }
+    if (part == 2) { *ptr = q.b.data(); *bytes = q.b.size() * 2; return 0; }
+    return -1;
+  };
+  auto vec = [&](std::vector<uint16_t>& v) -> int {
+    if (part != 0) return -1;
+    *ptr = v.data();
+    *bytes = v.size() * 2;
+    return 0;
+  };
+  if (scope == LISA_SCOPE_MTP) {
+    if (!M->has_mtp) return -2;
+    OrcMtp& t = M->mtp;
+    switch (kind) {
+      case LISA_T_MTP_PRE_FC_EMB: return vec(t.pre_fc_emb);
+      case LISA_T_MTP_PRE_FC_HID: return vec(t.pre_fc_hid);
+      case LISA_T_INPUT_NORM: return vec(t.input_norm);
+      case LISA_T_POST_NORM: return vec(t.post_norm);
+      case LISA_T_FINAL_NORM: return vec(t.final_norm);
+      case LISA_T_ATT_Q_NORM: return vec(t.q_norm);
+      case LISA_T_ATT_K_NORM: return vec(t.k_norm);
+      case LISA_T_MTP_FC: return q4(t.fc);
+      case LISA_T_ATT_Q: return q4(t.q);
+      case LISA_T_ATT_K: return q4(t.k);
+      case LISA_T_ATT_V: return q4(t.v);
+      case LISA_T_ATT_O: return q4(t.o);
+      case LISA_T_MLP_GATE: return q4(t.gate);
+      case LISA_T_MLP_UP: return q4(t.up);
+      case LISA_T_MLP_DOWN: return q4(t.down);
+      case LISA_T_KEY_CACHE: return vec(t.key_cache);
+      case LISA_T_VALUE_CACHE: return vec(t.value_cache);
+      default: return -3;
+    }
+  }
+  if (scope == 0) {
+    switch (kind) {
+      case LISA_T_EMBED: return q4(M->embed);
+      case LISA_T_LM_HEAD: return q4(M->head);
+      case LISA_T_FINAL_NORM: return vec(M->final_norm);
+      default: return -3;
+    }
+  }
+  if (scope < 1 || scope > M->layers) return -4;
+  OrcLayer& l = M->L[scope - 1];
+  switch (kind) {
+    case LISA_T_INPUT_NORM: return vec(l.input_norm);
+    case LISA_T_POST_NORM: return vec(l.post_norm);
+    case LISA_T_MLP_GATE: return q4(l.gate);
+    case LISA_T_MLP_UP: return q4(l.up);
+    case LISA_T_MLP_DOWN: return q4(l.down);
+    default: break;
+  }
+  if (l.attention) {
+    switch (kind) {
+      case LISA_T_ATT_Q: return q4(l.q);
+      case LISA_T_ATT_K: return q4(l.k);
+      case LISA_T_ATT_V: return q4(l.v);
+      case LISA_T_ATT_O: return q4(l.o);
+      case LISA_T_ATT_Q_NORM: return vec(l.q_norm);
+      case LISA_T_ATT_K_NORM: return vec(l.k_norm);
+      default: return -3;
+    }
+  }
+  switch (kind) {
+    case LISA_T_GDN_QKV: return q4(l.qkv);
+    case LISA_T_GDN_Z: return q4(l.z);
+    case LISA_T_GDN_A: return q4(l.a);
+    case LISA_T_GDN_B: return q4(l.b);
+    case LISA_T_GDN_OUT: return q4(l.out);
+    case LISA_T_GDN_CONV_W: return vec(l.conv_w);
+    case LISA_T_GDN_A_LOG: return vec(l.a_log);
+    case LISA_T_GDN_DT_BIAS: return vec(l.dt_bias);
+    case LISA_T_GDN_NORM: return vec(l.gnorm);
+    default: return -3;
+  }
 }
 
 }  // extern "C"

@@ -130,6 +130,11 @@ int orc_mtp_forward(OrcModel* m, uint32_t token, const uint16_t* cond, uint32_t*
 uint32_t orc_mtp_position(const OrcModel* m);
 int orc_mtp_trim(OrcModel* m, int count);
 
+/* Test hook: pointer to and size of one model tensor (scope = layer + 1, 0 for
+ * globals, LISA_SCOPE_MTP; kind = LISA_T_*; part 0 words/vector, 1 scales,
+ * 2 biases); 0 on success. Tests overwrite weights through it. */
+int orc_model_tensor(OrcModel* m, int scope, int kind, int part, void** ptr, size_t* bytes);
+
 /* Copy of a synthetic tensor as generated (for tests). */
 void orc_synth_bf16(uint64_t seed, uint64_t tensor_id, int dist, float a, float b, size_t n,
                     uint16_t* out);

@@ -42,11 +42,25 @@ _SIGS = {
     "orc_mtp_forward": (C.c_int, [_P, C.c_uint32, _P, _P, _P]),
     "orc_mtp_position": (C.c_uint32, [_P]),
     "orc_mtp_trim": (C.c_int, [_P, C.c_int]),
+    "orc_model_tensor": (C.c_int, [_P, C.c_int, C.c_int, C.c_int, C.POINTER(_P), C.POINTER(C.c_size_t)]),
     "orc_synth_bf16": (None, [C.c_uint64, C.c_uint64, C.c_int, C.c_float, C.c_float, C.c_size_t, _P]),
     "orc_synth_f32": (None, [C.c_uint64, C.c_uint64, C.c_int, C.c_float, C.c_float, C.c_size_t, _P]),
     "orc_synth_words": (None, [C.c_uint64, C.c_uint64, C.c_size_t, _P]),
 }
 _LIB = None
+
+def _tensor_kinds():
+    """LISA_T_* of include/lisa_model.h (the synthetic tensor catalogue), by name."""
+    import re
+    text = (ORACLE_DIR.parent / "include" / "lisa_model.h").read_text()
+    body = re.search(r"enum \{\s*(LISA_T_INPUT_NORM = 1,.*?)\};", text, re.S).group(1)
+    names = re.findall(r"(LISA_T_\w+)", body)
+    kinds = {n[len("LISA_T_"):]: i + 1 for i, n in enumerate(names)}
+    scope_mtp = int(re.search(r"#define LISA_SCOPE_MTP (\d+)", text).group(1))
+    return kinds, scope_mtp
+
+
+T, SCOPE_MTP = _tensor_kinds()
 
 MATH = {"exp": 0, "exp2": 1, "log": 2, "sin": 3, "cos": 4, "rsqrt": 5, "bf16": 6, "silu_exp": 7,
         "softplus": 8, "sigmoid_exp": 9, "silu_exp2": 10, "sigmoid_exp2": 11}
@@ -278,6 +292,17 @@ class Model:
     def mtp_trim(self, count):
         if lib().orc_mtp_trim(self.h, count):
             raise RuntimeError("bad trim")
+
+    def tensor(self, scope, kind, part, dtype):
+        """A writable numpy view of one model tensor (orc_model_tensor); the
+        view is valid while the model lives."""
+        ptr, nbytes = C.c_void_p(), C.c_size_t()
+        rc = lib().orc_model_tensor(self.h, scope, kind, part, C.byref(ptr), C.byref(nbytes))
+        if rc:
+            raise KeyError(f"no tensor scope={scope} kind={kind} part={part} ({rc})")
+        count = nbytes.value // np.dtype(dtype).itemsize
+        buf = (C.c_char * nbytes.value).from_address(ptr.value)
+        return np.frombuffer(buf, dtype=dtype, count=count)
 
 
 # ---- host-side helpers shared by tests ----------------------------------------

@@ -151,3 +151,50 @@ def test_zero_key_only_decays():
     want = s0.reshape(VH, -1).astype(np.float64) * decay[:, None]
     got = s1.reshape(VH, -1)
     assert np.all(np.abs(got - want) <= np.abs(want) * 4e-7 + 1e-30)
+
+
+def test_value_heads_read_their_key_head():
+    """gdn.metal:271: value head h reads key head h / 3 (value heads 3j, 3j+1,
+    3j+2 share key head j). Every key head gets a different one-hot key
+    column, so a wrong grouping (h % 16, or h / 3 of the wrong operand) writes
+    another column; decay 1, beta 1 and a zero state make the update exact."""
+    rng = np.random.default_rng(45)
+    vals = (rng.integers(-64, 64, size=(1, VH, HD)) / 8.0).astype(np.float32)
+    cols = [(7 * kh + 3) % HD for kh in range(16)]
+    co, z, a, b, alog, dtb, nw = delta_inputs([0], vals, query=0)
+    co[0, :2 * KEY] = 0.0
+    for kh in range(16):
+        co[0, kh * HD + cols[kh]] = 1.0            # query of key head kh
+        co[0, KEY + kh * HD + cols[kh]] = 1.0      # key of key head kh
+    s0 = np.zeros(VH * HD * HD, np.float32)
+    _, s, y, _ = orc.gdn_recurrence(co, z, a, b, alog, dtb, nw, s0, 1)
+    S = s.reshape(VH, HD, HD)
+    for h in range(VH):
+        col = cols[h // 3]
+        assert np.array_equal(S[h][:, col], vals[0, h]), h
+        assert np.count_nonzero(S[h]) == np.count_nonzero(vals[0, h]), h
+        # the readout of head h uses the same key head's query
+        ref = vals[0, h] / np.sqrt(128.0)
+        assert np.all(np.abs(y[0, h * HD:(h + 1) * HD] - ref) <= np.abs(ref) * 2.0**-7), h
+
+
+def test_beta_gate_against_double():
+    """gdn.metal:196-204: beta = bf16(sigmoid(bf16 b)) at non-saturated b.
+    From a zero state with decay 1 and a one-hot key, one step writes
+    beta * v into the key's column, so the column pins beta (and its sign:
+    sigmoid(-b) or 1 - beta would fail) against float64."""
+    rng = np.random.default_rng(46)
+    vals = (rng.integers(1, 64, size=(1, VH, HD)) / 8.0).astype(np.float32)
+    co, z, a, b, alog, dtb, nw = delta_inputs([9], vals, query=9)
+    b[0] = rng.uniform(-4.0, 4.0, VH).astype(np.float32)
+    s0 = np.zeros(VH * HD * HD, np.float32)
+    _, s, _, _ = orc.gdn_recurrence(co, z, a, b, alog, dtb, nw, s0, 1)
+    S = s.reshape(VH, HD, HD)
+    bb = fb(bf(b[0])).astype(np.float64)
+    beta = 1.0 / (1.0 + np.exp(-bb))
+    for h in range(VH):
+        want = vals[0, h].astype(np.float64) * beta[h]
+        got = S[h][:, 9].astype(np.float64)
+        # beta is rounded to bf16 (relative 2^-9) and the product to f32
+        assert np.all(np.abs(got - want) <= np.abs(want) * 2.0**-8), (h, b[0, h])
+    assert np.unique(np.round(beta, 3)).size > 20  # the gates really span (0, 1)

@@ -137,3 +137,49 @@ def test_speculative_equals_sequential(pair):
     assert list(toks) == truth
     assert stats["rounds"] > 3
     assert 0 < stats["accepted_drafts"] < stats["drafted_tokens"]
+
+
+def test_restore_rejects_checkpoint_of_other_depth(pair):
+    """A checkpoint holds the GDN/conv state of its runner's layers; restoring
+    it into a runner of another depth must fail, not copy past the arenas."""
+    pkg, orc, r, m = pair
+    other = pkg.Runner(layers=2 * LAYERS, vocab=VOCAB, capacity=64, seed=SEED, use_graph=False)
+    try:
+        ck = other.checkpoint_state()
+        with pytest.raises(pkg.LisaError) as err:
+            r.restore_state(ck)
+        assert err.value.code == -1  # LISA_E_ARG
+        other.free_checkpoint(ck)
+        ck = r.checkpoint_state()
+        with pytest.raises(pkg.LisaError):
+            other.restore_state(ck)
+        r.free_checkpoint(ck)
+    finally:
+        other.close()
+
+
+def test_mtp_checkpoint_restore(pair):
+    """MtpRunner::checkpoint_state / restore_state (runner.rs:2382-2420): the
+    drafter's KV rows and position come back. After the checkpoint, rows below
+    the checkpoint position are overwritten by other steps; the same drafter
+    step after the restore must reproduce the one taken before."""
+    pkg, orc, r, m = pair
+    fresh(r, m, filled=20)
+    am = r.forward_token_decode(3)
+    d0 = r.mtp_forward(am, 0, 0)
+    ck = r.mtp_checkpoint_state()
+    pos = r.mtp_position
+    a1 = r.mtp_forward(d0, 0, 0)
+    n1 = r.mtp_normalized()
+    r.mtp_trim_state(2)            # back below the checkpoint position
+    r.mtp_upload_cond(np.full(5120, 0x3F80, np.uint16))
+    r.mtp_forward(77, 2)           # rewrites KV row pos - 1
+    r.mtp_forward(78, 2)           # and row pos
+    r.mtp_restore_state(ck)
+    assert r.mtp_position == pos
+    a2 = r.mtp_forward(d0, 0, 0)
+    assert a2 == a1
+    assert np.array_equal(r.mtp_normalized(), n1)
+    r.free_mtp_checkpoint(ck)
+    bad = r.mtp_checkpoint_state()
+    r.free_mtp_checkpoint(bad)

@@ -46,7 +46,7 @@ def gemm(pkg, dev, a_bf16, q, m, kernel="lisa_q4_gemm"):
 
 @pytest.mark.parametrize("kernel", GEMM_KERNELS)
 @pytest.mark.parametrize("M,N,K", [(37, 200, 1024), (128, 512, 5120), (300, 48, 5120), (5, 256, 17408),
-                                   (512, 384, 6144), (260, 300, 1024)])
+                                   (512, 384, 6144), (260, 300, 1024), (33, 96, 192), (9, 130, 64)])
 def test_gemm_matches_oracle(pkg, orc, dev, M, N, K, kernel):
     rng = np.random.default_rng(M * 7 + N + K)
     w, s, b = rand_q4(rng, N, K)
@@ -58,9 +58,10 @@ def test_gemm_matches_oracle(pkg, orc, dev, M, N, K, kernel):
 
 
 @pytest.mark.parametrize("kernel", GEMM_KERNELS)
-def test_gemm_exact_integer_case(pkg, orc, dev, kernel):
+@pytest.mark.parametrize("K", [2048, 192])  # an even and an odd number of 64-wide K steps
+def test_gemm_exact_integer_case(pkg, orc, dev, kernel, K):
     rng = np.random.default_rng(3)
-    M, N, K = 70, 130, 2048
+    M, N = 70, 130
     w = rng.integers(0, 2**32, size=(N, K // 8), dtype=np.uint64).astype(np.uint32)
     a = bf16(rng.integers(-4, 5, size=(M, K)).astype(np.float32))
     s = bf16(rng.choice(np.array([0.5, 1.0, 2.0], np.float32), size=(N, K // 64)))
