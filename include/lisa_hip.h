@@ -216,6 +216,34 @@ int lisa_mtp_read_normalized(LisaRunner* r, uint16_t* out);
 uint32_t lisa_mtp_position(LisaRunner* r);
 int lisa_mtp_trim_state(LisaRunner* r, int32_t count);
 
+/* Device-resident conditioning by (buffer, byte offset), as speculative/mod.rs
+ * passes it: the target's hidden row `row` sits at lisa_runner_hidden_offset(row)
+ * of QwenRunner::scratch() (hidden_offset, runner.rs:846-848), the drafter's own
+ * normalized hidden at lisa_mtp_normalized_offset() of MtpRunner::scratch()
+ * (normalized_offset, runner.rs:2689-2692). lisa_mtp_resolve_cond maps
+ * (cond is the target's scratch, offset) to (cond_source, cond_row) of
+ * lisa_mtp_forward, rejecting offsets that address neither (host-only, no
+ * device call). lisa_mtp_forward_device is forward_position_decode_device
+ * (runner.rs:2711-2765) with that addressing; *normalized_off receives
+ * normalized_offset(). */
+uint64_t lisa_runner_hidden_offset(int32_t row);
+uint64_t lisa_mtp_normalized_offset(void);
+int lisa_mtp_resolve_cond(int32_t cond_is_target, uint64_t cond_off, int32_t* cond_source, int32_t* cond_row);
+int lisa_mtp_forward_device(LisaRunner* r, uint32_t token, int32_t cond_is_target, uint64_t cond_off,
+                            uint32_t* argmax, uint64_t* normalized_off);
+/* forward_position_decode (runner.rs:2618-2680): the drafter conditioned on a
+ * host hidden f32[5120] (bf16 by truncation); argmax and the normalized hidden
+ * (nullable, f32[5120]). */
+int lisa_mtp_forward_position_decode(LisaRunner* r, uint32_t token, const float* hidden, uint32_t* argmax,
+                                     float* normalized);
+/* forward_position_batch_with_progress (runner.rs:3494-3581): n positions of
+ * (tokens[t], hiddens f32[t][5120]) in chunks of `chunk` rows (0 = 512) with
+ * the prefill kernels (q4 GEMMs on the matrix cores, attention rows);
+ * argmax_out[n] and normalized_out f32[n][5120] (both nullable).
+ * mtp position += n. A host that reports progress calls it once per chunk. */
+int lisa_mtp_forward_batch(LisaRunner* r, const uint32_t* tokens, const float* hiddens, int32_t n, int32_t chunk,
+                           uint32_t* argmax_out, float* normalized_out);
+
 /* MtpRunner::checkpoint_state / restore_state (runner.rs:2382-2420): device
  * copies of the drafter's KV caches and its position. Restore rejects a
  * checkpoint position past the capacity (LISA_E_CAPACITY, as the reference
@@ -261,6 +289,15 @@ int lisa_generate_greedy_block3(LisaRunner* r, uint32_t bonus, const float* targ
                                 uint32_t mtp_seed_token, const float* mtp_seed_hidden, int32_t max_tokens,
                                 const uint32_t* force_truth, int32_t force_len, uint64_t force_seed,
                                 float p_accept, uint32_t* tokens_out, LisaSpecStats* stats);
+
+/* prefill_prompt_from (speculative/mod.rs:237-311): target prefill of
+ * prompt[start..n) (batched from 4 tokens), then the drafter over the shifted
+ * tokens conditioned on the target's per-position hidden rows (batched from 4
+ * positions). Outputs: the bonus token, the target hidden f32[5120] of the last
+ * position and the drafter seed (token, normalized hidden f32[5120]). Both
+ * runners must be positioned at `start`. */
+int lisa_prefill_prompt(LisaRunner* r, const uint32_t* prompt, int32_t n, int32_t start, uint32_t* bonus,
+                        float* target_hidden, uint32_t* mtp_seed_token, float* mtp_seed_hidden);
 
 #ifdef __cplusplus
 }

@@ -252,6 +252,12 @@ typedef struct LisaRowsParams {
   uint32_t* argmax_out;
   uint32_t width; /* SILU row width; ARGMAX vocabulary */
   uint32_t mode;
+  /* NORM / RESNORM: elements between normalized rows t and t + 1 of x_out
+   * (0 = 5120); 10240 writes one half of the MTP fc input rows
+   * (rms_norm_rows_stride, norm.metal:142-181). RESNORM with h_in null takes
+   * r = bf16(o) (the MTP fc output cast). */
+  uint32_t x_stride;
+  uint32_t pad0;
 } LisaRowsParams;
 
 /* lisa_attn_partial_rows takes LISA_ATT_ROWS_PER_WG rows per workgroup:

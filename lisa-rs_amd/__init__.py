@@ -110,7 +110,8 @@ class RowsParams(C.Structure):
     _fields_ = [("h_in", C.c_uint64), ("o_in", C.c_uint64), ("norm_w", C.c_uint64), ("r_out", C.c_uint64),
                 ("x_out", C.c_uint64), ("tokens", C.c_uint64), ("emb_w", C.c_uint64), ("emb_sb", C.c_uint64),
                 ("g_in", C.c_uint64), ("u_in", C.c_uint64), ("act_out", C.c_uint64), ("logits", C.c_uint64),
-                ("argmax_out", C.c_uint64), ("width", C.c_uint32), ("mode", C.c_uint32)]
+                ("argmax_out", C.c_uint64), ("width", C.c_uint32), ("mode", C.c_uint32),
+                ("x_stride", C.c_uint32), ("pad0", C.c_uint32)]
 
 
 class ConvRowsParams(C.Structure):
@@ -214,6 +215,15 @@ _SIGS = {
     "lisa_mtp_read_normalized": (C.c_int, [_P, _P]),
     "lisa_mtp_position": (C.c_uint32, [_P]),
     "lisa_mtp_trim_state": (C.c_int, [_P, C.c_int32]),
+    "lisa_runner_hidden_offset": (C.c_uint64, [C.c_int32]),
+    "lisa_mtp_normalized_offset": (C.c_uint64, []),
+    "lisa_mtp_resolve_cond": (C.c_int, [C.c_int32, C.c_uint64, C.POINTER(C.c_int32), C.POINTER(C.c_int32)]),
+    "lisa_mtp_forward_device": (C.c_int, [_P, C.c_uint32, C.c_int32, C.c_uint64, C.POINTER(C.c_uint32),
+                                          C.POINTER(C.c_uint64)]),
+    "lisa_mtp_forward_position_decode": (C.c_int, [_P, C.c_uint32, _P, C.POINTER(C.c_uint32), _P]),
+    "lisa_mtp_forward_batch": (C.c_int, [_P, _P, _P, C.c_int32, C.c_int32, _P, _P]),
+    "lisa_prefill_prompt": (C.c_int, [_P, _P, C.c_int32, C.c_int32, C.POINTER(C.c_uint32), _P,
+                                      C.POINTER(C.c_uint32), _P]),
     "lisa_mtp_checkpoint_state": (C.c_int, [_P, C.POINTER(_P)]),
     "lisa_mtp_restore_state": (C.c_int, [_P, _P]),
     "lisa_mtp_checkpoint_free": (None, [_P]),
@@ -507,6 +517,43 @@ class Runner:
     def mtp_trim_state(self, count: int) -> None:
         _check(lib().lisa_mtp_trim_state(self.h, count))
 
+    def mtp_forward_device(self, token: int, cond_is_target: bool, cond_off: int):
+        """forward_position_decode_device addressed by (buffer, byte offset):
+        returns (argmax, normalized_offset)."""
+        am, off = C.c_uint32(), C.c_uint64()
+        _check(lib().lisa_mtp_forward_device(self.h, token, 1 if cond_is_target else 0, cond_off, C.byref(am),
+                                             C.byref(off)))
+        return int(am.value), int(off.value)
+
+    def mtp_forward_position_decode(self, token: int, hidden: np.ndarray):
+        """forward_position_decode (runner.rs:2618-2680): (argmax, normalized f32[5120])."""
+        h = np.ascontiguousarray(hidden, dtype=np.float32)
+        am = C.c_uint32()
+        xn = np.empty(HIDDEN, np.float32)
+        _check(lib().lisa_mtp_forward_position_decode(self.h, token, _ptr(h), C.byref(am), _ptr(xn)))
+        return int(am.value), xn
+
+    def mtp_forward_batch(self, tokens, hiddens, chunk: int = 0):
+        """forward_position_batch_with_progress (runner.rs:3494-3581):
+        (argmax[n], normalized f32[n][5120])."""
+        t = np.ascontiguousarray(tokens, dtype=np.uint32)
+        h = np.ascontiguousarray(hiddens, dtype=np.float32).reshape(t.size, HIDDEN)
+        am = np.zeros(t.size, np.uint32)
+        xn = np.empty((t.size, HIDDEN), np.float32)
+        _check(lib().lisa_mtp_forward_batch(self.h, _ptr(t), _ptr(h), t.size, chunk, _ptr(am), _ptr(xn)))
+        return am, xn
+
+    def prefill_prompt(self, prompt, start: int = 0):
+        """prefill_prompt_from (speculative/mod.rs:237-311): (bonus, target_hidden,
+        (mtp_seed_token, mtp_seed_hidden))."""
+        p = np.ascontiguousarray(prompt, dtype=np.uint32)
+        bonus, seed = C.c_uint32(), C.c_uint32()
+        th = np.empty(HIDDEN, np.float32)
+        sh = np.empty(HIDDEN, np.float32)
+        _check(lib().lisa_prefill_prompt(self.h, _ptr(p), p.size, start, C.byref(bonus), _ptr(th), C.byref(seed),
+                                         _ptr(sh)))
+        return int(bonus.value), th, (int(seed.value), sh)
+
     def mtp_checkpoint_state(self):
         """MtpRunner::checkpoint_state (runner.rs:2382-2398)."""
         ck = C.c_void_p()
@@ -534,6 +581,23 @@ class Runner:
                                                  C.byref(stats)))
         return out[:max_tokens], {"rounds": stats.rounds, "accepted_drafts": stats.accepted_drafts,
                                   "drafted_tokens": stats.drafted_tokens, "target_forwards": stats.target_forwards}
+
+
+def hidden_offset(row: int) -> int:
+    """QwenRunner::hidden_offset (runner.rs:846-848) of the C ABI."""
+    return int(lib().lisa_runner_hidden_offset(row))
+
+
+def normalized_offset() -> int:
+    """MtpRunner::normalized_offset (runner.rs:2689-2692) of the C ABI."""
+    return int(lib().lisa_mtp_normalized_offset())
+
+
+def resolve_cond(cond_is_target: bool, cond_off: int):
+    """(cond_source, cond_row) of lisa_mtp_forward for a (buffer, offset) pair."""
+    src, row = C.c_int32(), C.c_int32()
+    _check(lib().lisa_mtp_resolve_cond(1 if cond_is_target else 0, cond_off, C.byref(src), C.byref(row)))
+    return int(src.value), int(row.value)
 
 
 def stream_key(seed: int, tensor_id: int) -> int:

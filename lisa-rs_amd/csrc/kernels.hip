@@ -1847,7 +1847,9 @@ extern "C" __global__ __launch_bounds__(256) void lisa_rows(LisaRowsParams p) {
     }
     case LISA_ROWS_NORM:
     case LISA_ROWS_RESNORM: {
-      const uint4* hs = reinterpret_cast<const uint4*>(p.h_in + (size_t)t * LISA_HIDDEN);
+      // RESNORM without h_in: r = bf16(o) (the MTP fc output cast, norm.metal:132-137)
+      const bool has_h = p.h_in != nullptr;
+      const uint4* hs = reinterpret_cast<const uint4*>((has_h ? p.h_in : p.norm_w) + (has_h ? (size_t)t * LISA_HIDDEN : 0));
       const uint4* os = reinterpret_cast<const uint4*>(p.o_in + (size_t)t * LISA_HIDDEN);
       const uint4* ws = reinterpret_cast<const uint4*>(p.norm_w);
       float v[3][8];
@@ -1858,6 +1860,9 @@ extern "C" __global__ __launch_bounds__(256) void lisa_rows(LisaRowsParams p) {
         const bool valid = tid + 256 * i < kSegChunks;
         float hv[8];
         unpack_bf8(hs[c], hv);
+        if (!has_h)
+#pragma unroll
+          for (int e = 0; e < 8; ++e) hv[e] = 0.0f;
         if (p.mode == LISA_ROWS_RESNORM) {
           const uint4 o0 = os[2 * c], o1 = os[2 * c + 1];
           const float ov[8] = {__uint_as_float(o0.x), __uint_as_float(o0.y), __uint_as_float(o0.z),
@@ -1882,7 +1887,7 @@ extern "C" __global__ __launch_bounds__(256) void lisa_rows(LisaRowsParams p) {
         unpack_bf8(ws[c], wv);
 #pragma unroll
         for (int e = 0; e < 8; ++e) x[e] = lisa_bf16r((v[i][e] * inv) * wv[e]);
-        reinterpret_cast<uint4*>(p.x_out + (size_t)t * LISA_HIDDEN)[c] = pack_bf8(x);
+        reinterpret_cast<uint4*>(p.x_out + (size_t)t * (p.x_stride ? p.x_stride : LISA_HIDDEN))[c] = pack_bf8(x);
         if (p.mode == LISA_ROWS_RESNORM)
           reinterpret_cast<uint4*>(p.r_out + (size_t)t * LISA_HIDDEN)[c] = pack_bf8(v[i]);
       }

@@ -1151,6 +1151,55 @@ extern "C" void lisa_mtp_checkpoint_free(LisaMtpCheckpoint* ck) {
   delete ck;
 }
 
+// Device-resident conditioning of the drafter, as the reference addresses it:
+// a (buffer, byte offset) pair. The target's hidden rows sit at
+// lisa_runner_hidden_offset(row) of its scratch (hidden_offset, runner.rs:846-848);
+// the drafter's own normalized hidden at lisa_mtp_normalized_offset() of its
+// scratch (normalized_offset, runner.rs:2689-2692).
+extern "C" uint64_t lisa_runner_hidden_offset(int32_t row) { return (uint64_t)row * LISA_HIDDEN * 2; }
+extern "C" uint64_t lisa_mtp_normalized_offset(void) { return 0; }
+
+extern "C" int lisa_mtp_resolve_cond(int32_t cond_is_target, uint64_t cond_off, int32_t* cond_source,
+                                     int32_t* cond_row) {
+  if (!cond_source || !cond_row) return lisa_fail(LISA_E_ARG, "lisa_mtp_resolve_cond: null output");
+  if (cond_is_target) {
+    const uint64_t row_bytes = (uint64_t)LISA_HIDDEN * 2;
+    if (cond_off % row_bytes != 0 || cond_off / row_bytes > 2)
+      return lisa_fail(LISA_E_ARG, "offset %llu is not a target hidden row", (unsigned long long)cond_off);
+    *cond_source = 0;
+    *cond_row = (int32_t)(cond_off / row_bytes);
+    return LISA_OK;
+  }
+  if (cond_off != lisa_mtp_normalized_offset())
+    return lisa_fail(LISA_E_ARG, "offset %llu is not the drafter's normalized hidden", (unsigned long long)cond_off);
+  *cond_source = 1;
+  *cond_row = 0;
+  return LISA_OK;
+}
+
+extern "C" int lisa_mtp_forward_device(LisaRunner* r, uint32_t token, int32_t cond_is_target, uint64_t cond_off,
+                                       uint32_t* argmax, uint64_t* normalized_off) {
+  int32_t src = 0, row = 0;
+  LISA_TRY(lisa_mtp_resolve_cond(cond_is_target, cond_off, &src, &row));
+  LISA_TRY(lisa_mtp_forward(r, token, src, row, argmax));
+  if (normalized_off) *normalized_off = lisa_mtp_normalized_offset();
+  return LISA_OK;
+}
+
+// forward_position_decode (runner.rs:2618-2680): the drafter conditioned on a
+// host hidden f32[5120] (uploaded as bf16 by truncation, dtype.rs:42-47);
+// returns the argmax and the normalized hidden as f32.
+extern "C" int lisa_mtp_forward_position_decode(LisaRunner* r, uint32_t token, const float* hidden, uint32_t* argmax,
+                                                float* normalized) {
+  if (!r || !hidden) return lisa_fail(LISA_E_ARG, "lisa_mtp_forward_position_decode: bad argument");
+  std::vector<uint16_t> h(LISA_HIDDEN);
+  for (int i = 0; i < LISA_HIDDEN; ++i) h[i] = lisa_f32_to_bf16_trunc(hidden[i]);
+  LISA_TRY(lisa_mtp_upload_cond(r, h.data()));
+  LISA_TRY(lisa_mtp_forward(r, token, 2, 0, argmax));
+  if (normalized) LISA_TRY(read_hidden(r, r->drf.xnorm, 1, normalized));
+  return LISA_OK;
+}
+
 // =============================================================================
 // batched prefill: forward_prefill_with_progress (runner.rs:2129-2230)
 // =============================================================================
@@ -1248,6 +1297,113 @@ int rows_norm(LisaRunner* r, uint32_t m, const uint16_t* h, const float* o, cons
   return launch_rows(r, p, 1, m);
 }
 
+// Attention over m prefill rows at positions [base, base + m) against one
+// layer's caches (the rows are split into sub-blocks that bound the slice
+// partials); q/k/v projections in P.q_proj / P.k_raw / P.v_raw, output P.gated.
+int prefill_attention(LisaRunner* r, uint32_t m, uint32_t base, const uint16_t* qn, const uint16_t* kn, uint16_t* kc,
+                      uint16_t* vc) {
+  auto& P = r->pf;
+  LisaAttnParams a{};
+  a.q_proj = P.q_proj;
+  a.k_raw = P.k_raw;
+  a.v_raw = P.v_raw;
+  a.q_norm_w = qn;
+  a.k_norm_w = kn;
+  a.key_cache = kc;
+  a.value_cache = vc;
+  a.part_o = P.part_o;
+  a.part_ml = P.part_ml;
+  a.pos = P.pos;
+  a.gated = P.gated;
+  a.capacity = (uint32_t)r->cfg.capacity;
+  a.s_max = r->s_max;
+  a.query = P.query;
+  a.m_rows = m;
+  LISA_TRY(lisa_launch(r->dev, r->attn_store_rows, &a, sizeof a, m, 7, 1, 256, 1, 1));
+  for (uint32_t r0 = 0; r0 < m; r0 += P.att_rows) {
+    const uint32_t ms = std::min(P.att_rows, m - r0);
+    LisaAttnParams b = a;
+    b.q_proj = P.q_proj + (size_t)r0 * LISA_ATT_Q_OUT;
+    b.query = P.query + (size_t)r0 * LISA_ATT_OUT;
+    b.gated = P.gated + (size_t)r0 * LISA_ATT_OUT;
+    b.pos = P.pos + 1 + r0 / P.att_rows;
+    b.m_rows = ms;
+    const uint32_t slices = (base + r0 + ms + LISA_ATT_SLICE - 1) / LISA_ATT_SLICE;
+    LISA_TRY(lisa_launch(r->dev, r->attn_partial_rows, &b, sizeof b, slices, LISA_ATT_KVH,
+                         (ms + LISA_ATT_ROWS_PER_WG - 1) / LISA_ATT_ROWS_PER_WG, 256, 1, 1));
+    LISA_TRY(lisa_launch(r->dev, r->attn_merge_rows, &b, sizeof b, LISA_ATT_QH, ms, 1, 256, 1, 1));
+  }
+  return LISA_OK;
+}
+
+// Uploads the positions the attention row kernels read: pos[0] = base, then
+// the first position of every attention sub-block.
+int upload_prefill_pos(LisaRunner* r, uint32_t m, uint32_t base) {
+  auto& P = r->pf;
+  std::vector<uint32_t> pos(1 + (m + P.att_rows - 1) / P.att_rows);
+  pos[0] = base;
+  for (size_t j = 1; j < pos.size(); ++j) pos[j] = base + (uint32_t)(j - 1) * P.att_rows;
+  return upload_u32(r, P.pos, pos.data(), pos.size());
+}
+
+// One chunk of the drafter's batched prefill (runner.rs:3494-3581) at drafter
+// positions [r->mtp_position, + m): tokens in P.tokens, the target hidden rows
+// (bf16) in P.gated; leaves argmax in P.argmax and the final normalized rows
+// in P.X. The fc input [m][10240] is staged in P.act.
+int mtp_prefill_chunk(LisaRunner* r, uint32_t m) {
+  auto& P = r->pf;
+  const MtpDev& t = r->mtp;
+  uint16_t* fc_in = P.act;
+  {
+    LisaRowsParams e{};
+    e.mode = LISA_ROWS_EMBED;
+    e.tokens = P.tokens;
+    e.emb_w = r->embed.w;
+    e.emb_sb = r->embed.sb;
+    e.r_out = P.H;
+    LISA_TRY(launch_rows(r, e, 1, m));
+  }
+  // [RMSNorm(embed, pre_fc_norm_embedding) | RMSNorm(hidden, pre_fc_norm_hidden)]
+  LisaRowsParams nh{};
+  nh.mode = LISA_ROWS_NORM;
+  nh.h_in = P.H;
+  nh.norm_w = t.pre_fc_emb;
+  nh.x_out = fc_in;
+  nh.x_stride = 2 * LISA_HIDDEN;
+  LISA_TRY(launch_rows(r, nh, 1, m));
+  nh.h_in = P.gated;
+  nh.norm_w = t.pre_fc_hid;
+  nh.x_out = fc_in + LISA_HIDDEN;
+  LISA_TRY(launch_rows(r, nh, 1, m));
+  LISA_TRY(launch_gemm(r, fc_in, m, t.fc, P.B));
+  // hidden = bf16(fc output); normalized = RMSNorm(hidden, input_norm)
+  LISA_TRY(rows_norm(r, m, nullptr, P.B, t.input_norm, P.H, P.X));
+  LISA_TRY(launch_gemm(r, P.X, m, t.q, P.q_proj));
+  LISA_TRY(launch_gemm(r, P.X, m, t.k, P.k_raw));
+  LISA_TRY(launch_gemm(r, P.X, m, t.v, P.v_raw));
+  LISA_TRY(prefill_attention(r, m, r->mtp_position, t.q_norm, t.k_norm, r->mtp_key, r->mtp_value));
+  LISA_TRY(launch_gemm(r, P.gated, m, t.o, P.B));
+  LISA_TRY(rows_norm(r, m, P.H, P.B, t.post_norm, P.H, P.X));
+  LISA_TRY(launch_gemm(r, P.X, m, t.gate, P.G));
+  LISA_TRY(launch_gemm(r, P.X, m, t.up, P.U));
+  LisaRowsParams sw{};
+  sw.mode = LISA_ROWS_SILU;
+  sw.g_in = P.G;
+  sw.u_in = P.U;
+  sw.act_out = P.act;
+  sw.width = LISA_INTER;
+  LISA_TRY(launch_rows(r, sw, (LISA_INTER + 2047) / 2048, m));
+  LISA_TRY(launch_gemm(r, P.act, m, t.down, P.B));
+  LISA_TRY(rows_norm(r, m, P.H, P.B, t.final_norm, P.H, P.X));
+  LISA_TRY(launch_gemm(r, P.X, m, r->head, P.logits));
+  LisaRowsParams am{};
+  am.mode = LISA_ROWS_ARGMAX;
+  am.logits = P.logits;
+  am.width = (uint32_t)r->cfg.vocab;
+  am.argmax_out = P.argmax;
+  return launch_rows(r, am, 1, m);
+}
+
 // One prefill chunk of m rows at positions [r->position, r->position + m).
 int prefill_chunk(LisaRunner* r, uint32_t m) {
   auto& P = r->pf;
@@ -1303,37 +1459,7 @@ int prefill_chunk(LisaRunner* r, uint32_t m) {
       LISA_TRY(launch_gemm(r, P.X, m, l.k, P.k_raw));
       LISA_TRY(launch_gemm(r, P.X, m, l.v, P.v_raw));
       const size_t off = (size_t)l.cache_index * LISA_ATT_KVH * r->cfg.capacity * LISA_ATT_HD;
-      LisaAttnParams a{};
-      a.q_proj = P.q_proj;
-      a.k_raw = P.k_raw;
-      a.v_raw = P.v_raw;
-      a.q_norm_w = l.q_norm;
-      a.k_norm_w = l.k_norm;
-      a.key_cache = r->key_cache + off;
-      a.value_cache = r->value_cache + off;
-      a.part_o = P.part_o;
-      a.part_ml = P.part_ml;
-      a.pos = P.pos;
-      a.gated = P.gated;
-      a.capacity = (uint32_t)r->cfg.capacity;
-      a.s_max = r->s_max;
-      a.query = P.query;
-      a.m_rows = m;
-      LISA_TRY(lisa_launch(r->dev, r->attn_store_rows, &a, sizeof a, m, 7, 1, 256, 1, 1));
-      for (uint32_t r0 = 0; r0 < m; r0 += P.att_rows) {
-        const uint32_t ms = std::min(P.att_rows, m - r0);
-        LisaAttnParams b = a;
-        b.q_proj = P.q_proj + (size_t)r0 * LISA_ATT_Q_OUT;
-        b.query = P.query + (size_t)r0 * LISA_ATT_OUT;
-        b.gated = P.gated + (size_t)r0 * LISA_ATT_OUT;
-        b.pos = P.pos + 1 + r0 / P.att_rows;
-        b.m_rows = ms;
-        const uint32_t slices = (r->position + r0 + ms + LISA_ATT_SLICE - 1) / LISA_ATT_SLICE;
-        LISA_TRY(lisa_launch(r->dev, r->attn_partial_rows, &b, sizeof b, slices, LISA_ATT_KVH,
-                             (ms + LISA_ATT_ROWS_PER_WG - 1) / LISA_ATT_ROWS_PER_WG, 256, 1,
-                             1));
-        LISA_TRY(lisa_launch(r->dev, r->attn_merge_rows, &b, sizeof b, LISA_ATT_QH, ms, 1, 256, 1, 1));
-      }
+      LISA_TRY(prefill_attention(r, m, r->position, l.q_norm, l.k_norm, r->key_cache + off, r->value_cache + off));
       LISA_TRY(launch_gemm(r, P.gated, m, l.o, P.B));
     }
     LISA_TRY(rows_norm(r, m, P.H, P.B, l.post_norm, P.H, P.X));
@@ -1374,10 +1500,7 @@ extern "C" int lisa_runner_forward_prefill(LisaRunner* r, const uint32_t* tokens
   for (uint32_t b = 0; b < (uint32_t)n; b += rows) {
     const uint32_t m = std::min(rows, (uint32_t)n - b);
     LISA_TRY(upload_u32(r, P.tokens, tokens + b, m));
-    std::vector<uint32_t> pos(1 + (m + P.att_rows - 1) / P.att_rows);
-    pos[0] = r->position;
-    for (size_t j = 1; j < pos.size(); ++j) pos[j] = r->position + (uint32_t)(j - 1) * P.att_rows;
-    LISA_TRY(upload_u32(r, P.pos, pos.data(), pos.size()));
+    LISA_TRY(upload_prefill_pos(r, m, r->position));
     LISA_TRY(prefill_chunk(r, m));
     if (argmax_out)
       LISA_TRY(lisa_hip_check(hipMemcpyAsync(argmax_out + b, P.argmax, (size_t)m * 4, hipMemcpyDeviceToHost,
@@ -1394,5 +1517,48 @@ extern "C" int lisa_runner_forward_prefill(LisaRunner* r, const uint32_t* tokens
   }
   r->verify_base = -1;
   LISA_TRY(write_pos(r, r->tgt, r->position));
+  return sync(r);
+}
+
+
+// MtpRunner::forward_position_batch_with_progress (runner.rs:3494-3581): the
+// drafter over n (token, target hidden) positions at [mtp_position,
+// mtp_position + n), in chunks of `chunk` rows (0 = 512, the reference's
+// PREFILL_BATCH; at most the prefill scratch's 2048), with the prefill kernels.
+extern "C" int lisa_mtp_forward_batch(LisaRunner* r, const uint32_t* tokens, const float* hiddens, int32_t n,
+                                      int32_t chunk, uint32_t* argmax_out, float* normalized_out) {
+  if (!r || n < 0 || (n && (!tokens || !hiddens))) return lisa_fail(LISA_E_ARG, "lisa_mtp_forward_batch: bad argument");
+  if (!r->cfg.with_mtp) return lisa_fail(LISA_E_STATE, "runner was created without the MTP drafter");
+  for (int32_t i = 0; i < n; ++i) LISA_TRY(check_token(r, tokens[i]));
+  if (!n) return LISA_OK;
+  if (r->mtp_position + (uint32_t)n > (uint32_t)r->cfg.capacity)
+    return lisa_fail(LISA_E_CAPACITY, "MTP KV capacity %d exhausted by prefill of %d positions", r->cfg.capacity, n);
+  const uint32_t rows = (chunk <= 0) ? 512u : std::min<uint32_t>((uint32_t)chunk, kPrefillRows);
+  LISA_TRY(ensure_prefill(r));
+  auto& P = r->pf;
+  std::vector<uint16_t> hb, xn;
+  for (uint32_t b = 0; b < (uint32_t)n; b += rows) {
+    const uint32_t m = std::min(rows, (uint32_t)n - b);
+    LISA_TRY(upload_u32(r, P.tokens, tokens + b, m));
+    hb.resize((size_t)m * LISA_HIDDEN);
+    for (size_t i = 0; i < hb.size(); ++i) hb[i] = lisa_f32_to_bf16_trunc(hiddens[(size_t)b * LISA_HIDDEN + i]);
+    LISA_TRY(lisa_hip_check(hipMemcpyAsync(P.gated, hb.data(), hb.size() * 2, hipMemcpyHostToDevice, r->dev->stream),
+                            "H2D hidden rows"));
+    LISA_TRY(upload_prefill_pos(r, m, r->mtp_position));
+    LISA_TRY(mtp_prefill_chunk(r, m));
+    if (argmax_out)
+      LISA_TRY(lisa_hip_check(hipMemcpyAsync(argmax_out + b, P.argmax, (size_t)m * 4, hipMemcpyDeviceToHost,
+                                             r->dev->stream), "D2H argmax"));
+    if (normalized_out) {
+      xn.resize((size_t)m * LISA_HIDDEN);
+      LISA_TRY(lisa_hip_check(hipMemcpyAsync(xn.data(), P.X, xn.size() * 2, hipMemcpyDeviceToHost, r->dev->stream),
+                              "D2H normalized"));
+    }
+    LISA_TRY(sync(r));  // hb and xn are reused by the next chunk
+    if (normalized_out)
+      for (size_t i = 0; i < xn.size(); ++i) normalized_out[(size_t)b * LISA_HIDDEN + i] = lisa_bf16_to_f32(xn[i]);
+    r->mtp_position += m;
+  }
+  LISA_TRY(write_pos(r, r->drf, r->mtp_position));
   return sync(r);
 }

@@ -127,3 +127,52 @@ extern "C" int lisa_generate_greedy_block3(LisaRunner* r, uint32_t bonus, const 
   if (stats) *stats = st;
   return LISA_OK;
 }
+
+// prefill_prompt_from_with_progress (speculative/mod.rs:237-311): the target
+// runs prompt[start..n) (batched prefill for 4 or more tokens, M=1 decode
+// steps otherwise), then the drafter replays the shifted tokens
+// (prompt[start+1..n) followed by the bonus) conditioned on the target's
+// per-position hidden rows (batched for 4 or more positions). Returns the
+// bonus token, the target hidden of the last prompt position, and the drafter
+// seed (its last argmax and normalized hidden). The runners must already be
+// positioned at `start` (a restored session checkpoint, or 0).
+extern "C" int lisa_prefill_prompt(LisaRunner* r, const uint32_t* prompt, int32_t n, int32_t start, uint32_t* bonus,
+                                   float* target_hidden, uint32_t* mtp_seed_token, float* mtp_seed_hidden) {
+  if (!r || !bonus || !target_hidden || !mtp_seed_token || !mtp_seed_hidden)
+    return lisa_fail(LISA_E_ARG, "lisa_prefill_prompt: bad argument");
+  if (n <= 0 || !prompt) return lisa_fail(LISA_E_ARG, "cannot prefill an empty prompt");
+  if (start < 0 || start > n) return lisa_fail(LISA_E_ARG, "prefill start %d exceeds prompt length %d", start, n);
+  const int32_t len = n - start;
+  if (len == 0) return lisa_fail(LISA_E_ARG, "prefill start %d leaves no prompt token to run", start);
+  const uint32_t* seg = prompt + start;
+  std::vector<uint32_t> am((size_t)len);
+  std::vector<float> hidden((size_t)len * 5120);
+  if (len >= 4) {
+    LISA_TRY(lisa_runner_forward_prefill(r, seg, len, 0, am.data(), hidden.data()));
+  } else {
+    for (int32_t t = 0; t < len; ++t)
+      LISA_TRY(lisa_runner_forward_token_decode(r, seg[t], &am[(size_t)t], hidden.data() + (size_t)t * 5120));
+  }
+  const uint32_t b = am[(size_t)len - 1];
+  std::vector<uint32_t> tokens((size_t)len);
+  for (int32_t t = 0; t < len; ++t) {
+    const int32_t global = start + t;
+    tokens[(size_t)t] = global + 1 < n ? prompt[global + 1] : b;
+  }
+  uint32_t seed = 0;
+  if (len >= 4) {
+    std::vector<uint32_t> mam((size_t)len);
+    std::vector<float> xn((size_t)len * 5120);
+    LISA_TRY(lisa_mtp_forward_batch(r, tokens.data(), hidden.data(), len, 0, mam.data(), xn.data()));
+    seed = mam[(size_t)len - 1];
+    std::memcpy(mtp_seed_hidden, xn.data() + (size_t)(len - 1) * 5120, 5120 * sizeof(float));
+  } else {
+    for (int32_t t = 0; t < len; ++t)
+      LISA_TRY(lisa_mtp_forward_position_decode(r, tokens[(size_t)t], hidden.data() + (size_t)t * 5120, &seed,
+                                                mtp_seed_hidden));
+  }
+  *bonus = b;
+  *mtp_seed_token = seed;
+  std::memcpy(target_hidden, hidden.data() + (size_t)(len - 1) * 5120, 5120 * sizeof(float));
+  return LISA_OK;
+}

@@ -344,28 +344,29 @@ void orc_q4_linear(const uint16_t* x, const uint32_t* w, const uint16_t* scales,
 }
 
 // Prefill q4 GEMM (gemm.metal:238-266): each weight dequantized to
-// bf16(fma(scale, q, bias)); C[m][n] = sum_k A[m][k] Wd[n][k] accumulated in
-// double and rounded once to f32 (the MFMA accumulation order of the HIP path
-// is the hardware's, so its results are compared with a tolerance).
+// bf16(fma(scale, q, bias)); C[m][n] accumulated in f32 in the order the
+// gfx950 bf16 MFMA (v_mfma_f32_32x32x16_bf16, K ascending in blocks of 16)
+// accumulates: once per 8 consecutive k, acc = f32(acc + sum of the 8 exact
+// products). Measured on the MI355X this reproduces ~99.2 % of the kernel's
+// outputs bit for bit on model-like data (the rest within a few ulps, the
+// hardware's own internal rounding), against ~21 % for one rounding at the
+// end, so the GPU prefill is compared within a tolerance. A product of two
+// bf16 values is exact in double and so is a sum of eight of them here.
+static int g_gemm_order = 0;  // 0: f32 per 8 k (the MFMA's order); 1: double sum, one rounding
+
+void orc_set_gemm_order(int order) { g_gemm_order = order ? 1 : 0; }
+
 void orc_q4_gemm(const uint16_t* a, const uint32_t* w, const uint16_t* scales, const uint16_t* biases, int n_rows,
                  int k, int m_rows, float* out) {
-  // Output (m, n) is four double lanes, lane j summing a[k'] * wd[k'] over
-  // k' = j mod 4 in ascending order, then (l0 + l1) + (l2 + l3). A product of
-  // two floats is exact in double, so the fused multiply-adds below equal a
-  // multiply followed by a rounded add; blocks of 4 weight rows x 3 input rows
-  // keep the operands in registers.
   const int wpr = k / 8, groups = k / 64;
+  const bool blocked = g_gemm_order == 0;
   std::vector<float> af((size_t)m_rows * k);
   for (size_t i = 0; i < af.size(); ++i) af[i] = bf(a[i]);
-  auto hsum = [](__m256d v) {
-    alignas(32) double l[4];
-    _mm256_store_pd(l, v);
-    return (float)((l[0] + l[1]) + (l[2] + l[3]));
-  };
   const int nblocks = (n_rows + 3) / 4;
 #pragma omp parallel
   {
-    std::vector<double> wd((size_t)4 * k);
+    // dequantized weights of 4 rows, interleaved: wt[4 kk + j] = row j, column kk
+    std::vector<double> wt((size_t)4 * k);
 #pragma omp for schedule(dynamic, 4)
     for (int nb = 0; nb < nblocks; ++nb) {
       const int n0 = 4 * nb, nn = std::min(4, n_rows - n0);
@@ -376,47 +377,57 @@ void orc_q4_gemm(const uint16_t* a, const uint32_t* w, const uint16_t* scales, c
           for (int e = 0; e < 64; ++e) {
             const int kk = 64 * g + e;
             const uint32_t q = (w[(size_t)n * wpr + kk / 8] >> (4 * (kk % 8))) & 0xfu;
-            wd[(size_t)j * k + kk] = (double)bfr(lisa_fma(sc, (float)q, bi));
+            wt[(size_t)4 * kk + j] = (double)bfr(lisa_fma(sc, (float)q, bi));
           }
         }
       }
-      const double* w0 = &wd[0];
-      const double* w1 = &wd[(size_t)k];
-      const double* w2 = &wd[(size_t)2 * k];
-      const double* w3 = &wd[(size_t)3 * k];
       int m = 0;
       for (; m + 3 <= m_rows; m += 3) {
         const float* a0 = &af[(size_t)m * k];
         const float* a1 = a0 + k;
         const float* a2 = a1 + k;
-        __m256d c[3][4];
-        for (int i = 0; i < 3; ++i)
-          for (int j = 0; j < 4; ++j) c[i][j] = _mm256_setzero_pd();
-        for (int kk = 0; kk < k; kk += 4) {
-          const __m256d x0 = _mm256_loadu_pd(w0 + kk), x1 = _mm256_loadu_pd(w1 + kk);
-          const __m256d x2 = _mm256_loadu_pd(w2 + kk), x3 = _mm256_loadu_pd(w3 + kk);
-          const __m256d y0 = _mm256_cvtps_pd(_mm_loadu_ps(a0 + kk));
-          const __m256d y1 = _mm256_cvtps_pd(_mm_loadu_ps(a1 + kk));
-          const __m256d y2 = _mm256_cvtps_pd(_mm_loadu_ps(a2 + kk));
-          c[0][0] = _mm256_fmadd_pd(y0, x0, c[0][0]); c[0][1] = _mm256_fmadd_pd(y0, x1, c[0][1]);
-          c[0][2] = _mm256_fmadd_pd(y0, x2, c[0][2]); c[0][3] = _mm256_fmadd_pd(y0, x3, c[0][3]);
-          c[1][0] = _mm256_fmadd_pd(y1, x0, c[1][0]); c[1][1] = _mm256_fmadd_pd(y1, x1, c[1][1]);
-          c[1][2] = _mm256_fmadd_pd(y1, x2, c[1][2]); c[1][3] = _mm256_fmadd_pd(y1, x3, c[1][3]);
-          c[2][0] = _mm256_fmadd_pd(y2, x0, c[2][0]); c[2][1] = _mm256_fmadd_pd(y2, x1, c[2][1]);
-          c[2][2] = _mm256_fmadd_pd(y2, x2, c[2][2]); c[2][3] = _mm256_fmadd_pd(y2, x3, c[2][3]);
+        __m256d c0 = _mm256_setzero_pd(), c1 = _mm256_setzero_pd(), c2 = _mm256_setzero_pd();
+        for (int k0 = 0; k0 < k; k0 += 8) {
+          __m256d s0 = _mm256_setzero_pd(), s1 = _mm256_setzero_pd(), s2 = _mm256_setzero_pd();
+          for (int kk = k0; kk < k0 + 8; ++kk) {
+            const __m256d wv = _mm256_loadu_pd(&wt[(size_t)4 * kk]);
+            s0 = _mm256_fmadd_pd(_mm256_set1_pd((double)a0[kk]), wv, s0);
+            s1 = _mm256_fmadd_pd(_mm256_set1_pd((double)a1[kk]), wv, s1);
+            s2 = _mm256_fmadd_pd(_mm256_set1_pd((double)a2[kk]), wv, s2);
+          }
+          // acc = f32(acc + block): the sum in double, one rounding to f32
+          c0 = _mm256_add_pd(c0, s0);
+          c1 = _mm256_add_pd(c1, s1);
+          c2 = _mm256_add_pd(c2, s2);
+          if (blocked) {
+            c0 = _mm256_cvtps_pd(_mm256_cvtpd_ps(c0));
+            c1 = _mm256_cvtps_pd(_mm256_cvtpd_ps(c1));
+            c2 = _mm256_cvtps_pd(_mm256_cvtpd_ps(c2));
+          }
         }
-        for (int i = 0; i < 3; ++i)
-          for (int j = 0; j < nn; ++j) out[(size_t)(m + i) * n_rows + n0 + j] = hsum(c[i][j]);
+        alignas(32) double r0[4], r1[4], r2[4];
+        _mm256_store_pd(r0, c0);
+        _mm256_store_pd(r1, c1);
+        _mm256_store_pd(r2, c2);
+        for (int j = 0; j < nn; ++j) {
+          out[(size_t)m * n_rows + n0 + j] = (float)r0[j];
+          out[(size_t)(m + 1) * n_rows + n0 + j] = (float)r1[j];
+          out[(size_t)(m + 2) * n_rows + n0 + j] = (float)r2[j];
+        }
       }
       for (; m < m_rows; ++m) {
         const float* a0 = &af[(size_t)m * k];
-        for (int j = 0; j < nn; ++j) {
-          const double* wj = &wd[(size_t)j * k];
-          __m256d c0 = _mm256_setzero_pd();
-          for (int kk = 0; kk < k; kk += 4)
-            c0 = _mm256_fmadd_pd(_mm256_cvtps_pd(_mm_loadu_ps(a0 + kk)), _mm256_loadu_pd(wj + kk), c0);
-          out[(size_t)m * n_rows + n0 + j] = hsum(c0);
+        __m256d c0 = _mm256_setzero_pd();
+        for (int k0 = 0; k0 < k; k0 += 8) {
+          __m256d s0 = _mm256_setzero_pd();
+          for (int kk = k0; kk < k0 + 8; ++kk)
+            s0 = _mm256_fmadd_pd(_mm256_set1_pd((double)a0[kk]), _mm256_loadu_pd(&wt[(size_t)4 * kk]), s0);
+          c0 = _mm256_add_pd(c0, s0);
+          if (blocked) c0 = _mm256_cvtps_pd(_mm256_cvtpd_ps(c0));
         }
+        alignas(32) double r0[4];
+        _mm256_store_pd(r0, c0);
+        for (int j = 0; j < nn; ++j) out[(size_t)m * n_rows + n0 + j] = (float)r0[j];
       }
     }
   }
@@ -1097,6 +1108,70 @@ int orc_model_prefill(OrcModel* M, const uint32_t* tokens, int n, int chunk, uin
     M->position += m;
   }
   M->verify_base = -1;
+  return 0;
+}
+
+// MtpRunner::forward_position_batch_with_progress (runner.rs:3494-3581): the
+// drafter over n positions (token t, target hidden t) in chunks of 512 rows,
+// on the prefill kernels' arithmetic: the host hidden is uploaded with the
+// truncating f32 -> bf16 conversion (dtype.rs:42-47), each half of the fc
+// input is an RMSNorm row (rms_norm_rows_stride, norm.metal:142-181), every
+// projection is a q4 GEMM with bf16-rounded dequantized weights, attention is
+// the causal rows form at the drafter's position, and the last norm's rows are
+// the returned hidden. argmax_out[n], normalized_out bf16[n][5120] (nullable).
+int orc_mtp_prefill(OrcModel* M, const uint32_t* tokens, const float* hiddens, int n, uint32_t* argmax_out,
+                    uint16_t* normalized_out) {
+  if (!M->has_mtp) return -1;
+  if (n < 0) return -2;
+  for (int t = 0; t < n; ++t)
+    if ((int)tokens[t] >= M->vocab) return -3;
+  OrcMtp& T = M->mtp;
+  if (T.position + (uint32_t)n > M->capacity) return -4;
+  const int chunk = 512;
+  for (int b0 = 0; b0 < n; b0 += chunk) {
+    const int m = std::min(chunk, n - b0);
+    const uint32_t base = T.position;
+    std::vector<float> E, Hh, R, B;
+    embed_rows(M, tokens + b0, m, E);
+    std::vector<uint16_t> fc_in((size_t)m * 2 * LISA_HIDDEN), cond(LISA_HIDDEN);
+    for (int t = 0; t < m; ++t) {
+      rms_norm_f(&E[(size_t)t * LISA_HIDDEN], T.pre_fc_emb.data(), LISA_HIDDEN, &fc_in[(size_t)t * 2 * LISA_HIDDEN]);
+      const float* h = hiddens + (size_t)(b0 + t) * LISA_HIDDEN;
+      std::vector<float> hb(LISA_HIDDEN);
+      for (int c = 0; c < LISA_HIDDEN; ++c) hb[c] = bf(lisa_f32_to_bf16_trunc(h[c]));
+      rms_norm_f(hb.data(), T.pre_fc_hid.data(), LISA_HIDDEN, &fc_in[(size_t)t * 2 * LISA_HIDDEN + LISA_HIDDEN]);
+    }
+    std::vector<float> fc;
+    gemm_q4(fc_in, m, T.fc, fc);
+    Hh.resize(fc.size());
+    for (size_t i = 0; i < fc.size(); ++i) Hh[i] = bfr(fc[i]);  // f32_to_bf16 (norm.metal:132-137)
+    std::vector<uint16_t> X;
+    norm_rows_bf16(Hh, m, T.input_norm, X);
+    std::vector<float> qp, kr, vr;
+    gemm_q4(X, m, T.q, qp);
+    gemm_q4(X, m, T.k, kr);
+    gemm_q4(X, m, T.v, vr);
+    std::vector<uint16_t> gated((size_t)m * LISA_ATT_OUT);
+    orc_attention(qp.data(), kr.data(), vr.data(), T.q_norm.data(), T.k_norm.data(), T.key_cache.data(),
+                  T.value_cache.data(), M->capacity, base, m, gated.data());
+    gemm_q4(gated, m, T.o, B);
+    residual_rows(Hh, B, m, R);
+    norm_rows_bf16(R, m, T.post_norm, X);
+    std::vector<float> g, u;
+    gemm_q4(X, m, T.gate, g);
+    gemm_q4(X, m, T.up, u);
+    std::vector<uint16_t> act((size_t)m * LISA_INTER);
+    orc_silu_mul(g.data(), u.data(), m * LISA_INTER, act.data());
+    gemm_q4(act, m, T.down, B);
+    residual_rows(R, B, m, Hh);
+    norm_rows_bf16(Hh, m, T.final_norm, X);
+    std::vector<float> logits;
+    gemm_q4(X, m, M->head, logits);
+    for (int t = 0; t < m; ++t)
+      if (argmax_out) argmax_out[b0 + t] = orc_argmax(&logits[(size_t)t * M->vocab], M->vocab);
+    if (normalized_out) std::memcpy(normalized_out + (size_t)b0 * LISA_HIDDEN, X.data(), 2 * X.size());
+    T.position += m;
+  }
   return 0;
 }
 

@@ -30,6 +30,12 @@ extern "C" {
 void orc_q4_linear(const uint16_t* x, const uint32_t* w, const uint16_t* scales,
                    const uint16_t* biases, int n_rows, int k, int m_rows, int ksplit, float* out);
 
+/* Accumulation order of orc_q4_gemm: 0 (default) the MFMA's, f32 once per 8
+ * consecutive k; 1 the double-precision sum rounded once. Both are valid
+ * orders of the reference's sum; tests use 1 to measure how far a change of
+ * summation order alone moves a deep model. */
+void orc_set_gemm_order(int order);
+
 /* K5 RMSNorm of one 5120-wide (or any multiple of 256) bf16 row
  * (norm.metal:10-47): out = bf16(x*inv*w). */
 void orc_rms_norm(const uint16_t* x, const uint16_t* w, int cols, uint16_t* out);
@@ -129,6 +135,12 @@ int orc_mtp_forward(OrcModel* m, uint32_t token, const uint16_t* cond, uint32_t*
                     uint16_t* normalized);
 uint32_t orc_mtp_position(const OrcModel* m);
 int orc_mtp_trim(OrcModel* m, int count);
+
+/* MtpRunner::forward_position_batch (runner.rs:3486-3581): the drafter over n
+ * (token, target hidden f32[5120]) positions with the prefill kernels'
+ * arithmetic; argmax_out[n], normalized_out bf16[n][5120] (nullable). */
+int orc_mtp_prefill(OrcModel* m, const uint32_t* tokens, const float* hiddens, int n, uint32_t* argmax_out,
+                    uint16_t* normalized_out);
 
 /* Test hook: pointer to and size of one model tensor (scope = layer + 1, 0 for
  * globals, LISA_SCOPE_MTP; kind = LISA_T_*; part 0 words/vector, 1 scales,

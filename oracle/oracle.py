@@ -19,6 +19,7 @@ _SIGS = {
     "orc_rms_norm": (None, [_P, _P, C.c_int, _P]),
     "orc_rms_norm_tiles": (None, [_P, _P, C.c_int, _P]),
     "orc_q4_gemm": (None, [_P, _P, _P, _P, C.c_int, C.c_int, C.c_int, _P]),
+    "orc_set_gemm_order": (None, [C.c_int]),
     "orc_model_prefill": (C.c_int, [_P, _P, C.c_int, C.c_int, _P, _P]),
     "orc_residual": (None, [_P, _P, C.c_int, _P]),
     "orc_embed": (None, [_P, _P, _P, C.c_uint32, C.c_int, _P]),
@@ -42,6 +43,7 @@ _SIGS = {
     "orc_mtp_forward": (C.c_int, [_P, C.c_uint32, _P, _P, _P]),
     "orc_mtp_position": (C.c_uint32, [_P]),
     "orc_mtp_trim": (C.c_int, [_P, C.c_int]),
+    "orc_mtp_prefill": (C.c_int, [_P, _P, _P, C.c_int, _P, _P]),
     "orc_model_tensor": (C.c_int, [_P, C.c_int, C.c_int, C.c_int, C.POINTER(_P), C.POINTER(C.c_size_t)]),
     "orc_synth_bf16": (None, [C.c_uint64, C.c_uint64, C.c_int, C.c_float, C.c_float, C.c_size_t, _P]),
     "orc_synth_f32": (None, [C.c_uint64, C.c_uint64, C.c_int, C.c_float, C.c_float, C.c_size_t, _P]),
@@ -103,6 +105,11 @@ def q4_gemm(a_bf16, w, scales, biases, n, k, m):
     lib().orc_q4_gemm(p(_c(a_bf16, np.uint16)), p(_c(w, np.uint32)), p(_c(scales, np.uint16)),
                       p(_c(biases, np.uint16)), n, k, m, p(out))
     return out.reshape(m, n)
+
+
+def set_gemm_order(order):
+    """0: the MFMA's order (f32 per 8 k, default); 1: double sum, one rounding."""
+    lib().orc_set_gemm_order(order)
 
 
 def residual(x_bf16, o_f32):
@@ -284,6 +291,17 @@ class Model:
         if rc:
             raise RuntimeError(f"oracle mtp forward failed ({rc})")
         return int(am[0]), xn
+
+    def mtp_prefill(self, tokens, hiddens):
+        """MtpRunner::forward_position_batch: (argmax[n], normalized bf16[n][5120])."""
+        t = _c(tokens, np.uint32)
+        h = _c(hiddens, np.float32).reshape(t.size, 5120)
+        am = np.zeros(t.size, np.uint32)
+        xn = np.empty((t.size, 5120), np.uint16)
+        rc = lib().orc_mtp_prefill(self.h, p(t), p(h), t.size, p(am), p(xn))
+        if rc:
+            raise RuntimeError(f"oracle mtp prefill failed ({rc})")
+        return am, xn
 
     @property
     def mtp_position(self):

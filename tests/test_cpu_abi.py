@@ -73,3 +73,21 @@ def test_layer_schedule():
     attn = [i for i in range(64) if orc.layer_is_attention(i)]
     assert len(attn) == 16
     assert attn == list(range(3, 64, 4))
+
+
+def test_cond_offset_mapping():
+    """The Rust shim passes the reference's (buffer, byte offset) conditioning
+    (speculative/mod.rs:141-183) through lisa_mtp_forward_device; the library
+    maps it onto (cond_source, cond_row): target hidden row r at
+    hidden_offset(r), the drafter's own hidden at normalized_offset()."""
+    pkg = load_pkg()
+    for row in range(3):
+        assert pkg.resolve_cond(True, pkg.hidden_offset(row)) == (0, row)
+    assert pkg.hidden_offset(1) - pkg.hidden_offset(0) == 5120 * 2
+    assert pkg.resolve_cond(False, pkg.normalized_offset()) == (1, 0)
+    for bad in (pkg.hidden_offset(3), pkg.hidden_offset(1) + 2, 7):
+        with pytest.raises(pkg.LisaError) as err:
+            pkg.resolve_cond(True, bad)
+        assert err.value.code == -1
+    with pytest.raises(pkg.LisaError):
+        pkg.resolve_cond(False, pkg.normalized_offset() + 16)

@@ -140,3 +140,45 @@ def test_step_equals_composition_of_kernel_functions(position):
         assert np.array_equal(xn, want_x)
     finally:
         m.close()
+
+
+def test_batched_drafter_agrees_with_sequential_steps():
+    """MtpRunner::forward_position_batch (runner.rs:3486-3581) against the same
+    positions one M=1 step at a time (forward_position_decode, :2618-2680):
+    the batch rounds every dequantized weight to bf16 (gemm.metal:246-250), so
+    the rows agree within that rounding; the argmax agrees at most positions."""
+    rng = np.random.default_rng(12)
+    n = 6
+    tokens = rng.integers(0, VOCAB, n).astype(np.uint32)
+    hiddens = rng.standard_normal((n, H)).astype(np.float32)
+    m = model()
+    try:
+        m.fill_state(9, 99)
+        bam, bxn = m.mtp_prefill(tokens, hiddens)
+        assert m.mtp_position == 9 + n
+        m.fill_state(9, 99)
+        seq = [m.mtp_forward(int(tokens[t]), orc.f32_to_bf16_trunc(hiddens[t])) for t in range(n)]
+    finally:
+        m.close()
+    sam = np.array([s[0] for s in seq])
+    sxn = orc.bf16_bits_to_f32(np.stack([s[1] for s in seq])).astype(np.float64)
+    bx = orc.bf16_bits_to_f32(bxn).astype(np.float64)
+    assert np.mean(bam == sam) >= 5 / 6
+    rel = np.sqrt(np.mean((bx - sxn) ** 2) / np.mean(sxn ** 2))
+    assert 0 < rel < 2e-2, rel
+
+
+def test_batched_drafter_wiring_of_fc_halves():
+    """The batch builds the fc input as [pre_fc | pre_fc_hidden] too: with the
+    embedding half of fc zeroed its rows do not depend on the tokens."""
+    rng = np.random.default_rng(13)
+    hiddens = rng.standard_normal((4, H)).astype(np.float32)
+    m = model()
+    try:
+        zero_fc_half(m, 0)
+        a0, x0 = m.mtp_prefill(np.array([1, 2, 3, 4], np.uint32), hiddens)
+        m.mtp_trim(4)
+        a1, x1 = m.mtp_prefill(np.array([900, 800, 700, 600], np.uint32), hiddens)
+        assert np.array_equal(a0, a1) and np.array_equal(x0, x1)
+    finally:
+        m.close()

@@ -55,6 +55,9 @@ def test_gemm_matches_oracle(pkg, orc, dev, M, N, K, kernel):
     want = orc.q4_gemm(a, w, s, b, N, K, M)
     rms = np.sqrt(np.mean(want.astype(np.float64) ** 2))
     assert np.max(np.abs(got - want)) <= 1e-5 * np.sqrt(K / 64) * rms
+    # the oracle accumulates in the MFMA's order (f32, once per 8 k): most
+    # outputs are the same bits, the rest differ by the hardware's own rounding
+    assert np.mean(got.view(np.uint32) == want.view(np.uint32)) >= 0.95
 
 
 @pytest.mark.parametrize("kernel", GEMM_KERNELS)
