@@ -255,6 +255,33 @@ def speculative_phase(pkg, steps=128, p_accept=0.6, seed=0x5EED):
             "_tokens": [int(t) for t in toks]}
 
 
+def capacity_phase(pkg, steps, warmup, capacity=32768):
+    """M=1 decode at ctx 4096 on a runner whose KV capacity is the reference's
+    serving default (src/cli/serve.rs:160): the attention grid follows the
+    live context (runner.rs:1498-1500), so the step costs what it costs at a
+    capacity just above the context."""
+    r = pkg.Runner(layers=LAYERS, vocab=VOCAB, capacity=capacity, seed=SEED, use_graph=True)
+    try:
+        L = pkg.lib()
+        dev = L.lisa_runner_device(r.h)
+        r.fill_state(CTX, CTX_SEED)
+        r.decode_greedy(FIRST_TOKEN, warmup)
+        r.fill_state(CTX, CTX_SEED)
+        ev0, ev1 = pkg.C.c_void_p(), pkg.C.c_void_p()
+        pkg._check(L.lisa_event_create(pkg.C.byref(ev0)))
+        pkg._check(L.lisa_event_create(pkg.C.byref(ev1)))
+        pkg._check(L.lisa_device_synchronize(dev))
+        pkg._check(L.lisa_event_record(ev0, dev))
+        toks = r.decode_greedy(FIRST_TOKEN, steps)
+        pkg._check(L.lisa_event_record(ev1, dev))
+        ms = pkg.C.c_float()
+        pkg._check(L.lisa_event_elapsed_ms(ev0, ev1, pkg.C.byref(ms)))
+    finally:
+        r.close()
+    return {"capacity": capacity, "ctx": CTX, "steps": steps, "tok_s": round(steps / (ms.value / 1e3), 3),
+            "ms_per_step": round(ms.value / steps, 4), "_tokens": [int(t) for t in toks]}
+
+
 GEMM_SHAPES = [(2048, INTER, HIDDEN, "mlp gate (and up)"), (2048, HIDDEN, INTER, "mlp down"),
                (2048, 12288, HIDDEN, "attention q")]
 BF16_PEAK_TFLOPS = 2500.0
@@ -458,6 +485,11 @@ def main():
         result["acceptance"] = spec["acceptance"]
         result["speculative"] = spec
         print(f"[bench] configs {result['kernel_configs']}; speculative {spec}", file=sys.stderr, flush=True)
+        cap = capacity_phase(pkg, K, W)
+        cap_tokens = cap.pop("_tokens")
+        cap["same_tokens"] = bool(cap_tokens == [int(t) for t in tokens])
+        result["capacity_32768"] = cap
+        print(f"[bench] capacity 32768 at ctx {CTX}: {cap}", file=sys.stderr, flush=True)
 
     if not args.no_cpu and args.cpu_steps > 0:
         orc = load("lisa_oracle", ROOT / "oracle" / "oracle.py")
@@ -497,6 +529,8 @@ def main():
         result["speculative"].pop("_tokens", None)
     print(json.dumps(result), flush=True)
     mismatch = [k for k in ("exact_match",) if result.get(k) is False]
+    if result.get("capacity_32768", {}).get("same_tokens") is False:
+        mismatch.append("capacity_32768.same_tokens")
     if "speculative" in result:
         mismatch += [k for k in ("exact_match", "exact_match_oracle") if result["speculative"].get(k) is False]
     if mismatch:

@@ -105,6 +105,36 @@ void lisa_event_free(LisaEvent* ev);
 int lisa_event_record(LisaEvent* ev, LisaDevice* dev);
 int lisa_event_elapsed_ms(LisaEvent* start, LisaEvent* stop, float* ms);
 
+/* ==================== decode attention (one layer) ======================= */
+/* The attention core of one gated-attention decode layer (the partial/merge
+ * half of encode_attention, runner.rs:1426-1592; attention.metal:118-319,
+ * 520-641) for BASELINE config 2: q/k RMSNorm + partial RoPE, the new K/V rows
+ * appended at positions *pos .. *pos + m_rows - 1, split-K slice partials over
+ * the live context and their merge with the output gate. All pointers are
+ * device addresses. max_pos bounds the last row's position on the host (it
+ * sizes the slice grid and the partials); rows past it are not attended. */
+typedef struct LisaAttnDecodeArgs {
+  const float* q_proj;       /* [m][12288]: per head 256 query then 256 gate, raw */
+  const float* k_raw;        /* [m][1024] */
+  const float* v_raw;        /* [m][1024] */
+  const uint16_t* q_norm_w;  /* bf16[256] */
+  const uint16_t* k_norm_w;  /* bf16[256] */
+  uint16_t* key_cache;       /* bf16 [4][capacity][256] */
+  uint16_t* value_cache;     /* bf16 [4][capacity][256] */
+  const uint32_t* pos;       /* device word: position of row 0 */
+  uint16_t* gated;           /* out: bf16 [m][6144] */
+  uint32_t capacity;
+  uint32_t m_rows;           /* 1 (decode) or 3 (block-3 verify) */
+  uint32_t max_pos;          /* *pos + m_rows - 1 <= max_pos < capacity */
+  uint32_t pad0;
+} LisaAttnDecodeArgs;
+/* Bytes of slice partials one call needs: m_rows x (max_pos / 64 + 1) x 24 x 258 x 4. */
+uint64_t lisa_attention_workspace_bytes(uint32_t m_rows, uint32_t max_pos);
+/* `workspace` (nullable) holds the partials; without one the library keeps a
+ * workspace per device, allocated and grown with hipMalloc on demand. Queued
+ * on the device stream (no wait). */
+int lisa_attention_decode(LisaDevice* dev, LisaModule* mod, const LisaAttnDecodeArgs* args, LisaBuffer* workspace);
+
 /* ============================ runner (runner.rs) ========================= */
 typedef struct LisaRunner LisaRunner;
 

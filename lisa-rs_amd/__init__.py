@@ -129,6 +129,13 @@ class CopyParams(C.Structure):
     _fields_ = [("src", C.c_uint64), ("dst", C.c_uint64), ("n16", C.c_uint64)]
 
 
+class AttnDecodeArgs(C.Structure):
+    _fields_ = [("q_proj", C.c_uint64), ("k_raw", C.c_uint64), ("v_raw", C.c_uint64), ("q_norm_w", C.c_uint64),
+                ("k_norm_w", C.c_uint64), ("key_cache", C.c_uint64), ("value_cache", C.c_uint64), ("pos", C.c_uint64),
+                ("gated", C.c_uint64), ("capacity", C.c_uint32), ("m_rows", C.c_uint32), ("max_pos", C.c_uint32),
+                ("pad0", C.c_uint32)]
+
+
 class RunnerConfig(C.Structure):
     _fields_ = [("layers", C.c_int32), ("vocab", C.c_int32), ("capacity", C.c_int32), ("with_mtp", C.c_int32),
                 ("seed", C.c_uint64), ("use_graph", C.c_int32), ("device", C.c_int32)]
@@ -188,6 +195,8 @@ _SIGS = {
     "lisa_event_free": (None, [_P]),
     "lisa_event_record": (C.c_int, [_P, _P]),
     "lisa_event_elapsed_ms": (C.c_int, [_P, _P, C.POINTER(C.c_float)]),
+    "lisa_attention_workspace_bytes": (C.c_uint64, [C.c_uint32, C.c_uint32]),
+    "lisa_attention_decode": (C.c_int, [_P, _P, C.POINTER(AttnDecodeArgs), _P]),
     "lisa_runner_create": (C.c_int, [C.POINTER(RunnerConfig), C.POINTER(_P)]),
     "lisa_runner_free": (None, [_P]),
     "lisa_runner_device": (_P, [_P]),
@@ -344,6 +353,12 @@ class Device:
 
     def synchronize(self) -> None:
         _check(lib().lisa_device_synchronize(self.h))
+
+    def attention_decode(self, args: "AttnDecodeArgs", workspace: "Buffer | None" = None, wait: bool = True) -> None:
+        """lisa_attention_decode: one decode layer's attention core (config 2)."""
+        _check(lib().lisa_attention_decode(self.h, self.module, C.byref(args), workspace.h if workspace else None))
+        if wait:
+            self.synchronize()
 
 
 # ---------------------------------------------------------------------------

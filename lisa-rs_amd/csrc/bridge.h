@@ -26,6 +26,9 @@ struct LisaDevice {
   // set while a profile pass runs: every lisa_launch is timed and tagged
   std::vector<LisaProfRec>* prof = nullptr;
   int prof_kind = -1;
+  // workspace of lisa_attention_decode called without one (grown on demand)
+  void* attn_ws = nullptr;
+  size_t attn_ws_len = 0;
 };
 
 struct LisaBuffer {
@@ -65,6 +68,11 @@ std::string lisa_library_dir();
 // Launch a kernel taking one by-value argument block.
 int lisa_launch(LisaDevice* d, LisaFunction* f, const void* params, size_t len, uint32_t gx, uint32_t gy,
                 uint32_t gz, uint32_t tx, uint32_t ty, uint32_t tz);
+
+struct LisaAttnDecodeArgs;
+// Checks a decode-attention call and launches its partial and merge kernels
+// with the slice partials at `part` (attention.cpp).
+int lisa_attention_launch(LisaDevice* dev, LisaModule* mod, const LisaAttnDecodeArgs* a, void* part);
 
 #define LISA_TRY(expr)          \
   do {                          \

@@ -76,6 +76,7 @@ extern "C" void lisa_device_free(LisaDevice* d) {
   if (!d) return;
   (void)hipSetDevice(d->ordinal);
   (void)hipStreamSynchronize(d->stream);
+  if (d->attn_ws) (void)hipFree(d->attn_ws);
   (void)hipStreamDestroy(d->stream);
   delete d;
 }

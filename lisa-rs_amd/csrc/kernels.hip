@@ -1595,7 +1595,9 @@ DEV void attn_merge_body(const LisaAttnParams& p) {
   const float m0 = ml[2 * s0], d0 = ml[2 * s0 + 1];
   __builtin_amdgcn_sched_barrier(0);
   const uint32_t ctx = __builtin_amdgcn_readfirstlane(pos_v) + t + 1;
-  const int used = (int)((ctx + LISA_ATT_SLICE - 1) / LISA_ATT_SLICE);
+  // slices past the allocated s_max (a caller whose position outruns the grid
+  // it launched) are never read
+  const int used = min((int)((ctx + LISA_ATT_SLICE - 1) / LISA_ATT_SLICE), (int)p.s_max);
   float mx = tid < used ? m0 : -INFINITY;
   for (int s = tid + 256; s < used; s += 256) mx = fmaxf(mx, ml[2 * s]);
   mx = max64(mx);

@@ -20,6 +20,7 @@
 #include <cmath>
 #include <cstdlib>
 #include <cstring>
+#include <map>
 #include <memory>
 #include <string>
 #include <vector>
@@ -34,6 +35,10 @@
 namespace {
 
 constexpr uint32_t kHistoryCap = 1u << 16;
+// Captured decode steps launch attention slices in multiples of this many
+// 64-token slices (512 positions), so one graph serves 512 positions and a
+// replay dispatches at most 7 slices past the context.
+constexpr uint32_t kGraphSliceBucket = 8;
 
 struct Q4Dev {
   uint32_t* w = nullptr;
@@ -150,7 +155,9 @@ struct LisaRunner {
   uint32_t position = 0;
   int64_t verify_base = -1;
   uint32_t mtp_position = 0;
-  LisaGraph* step_graph = nullptr;
+  // captured M=1 steps keyed by the attention slices they launch (a multiple
+  // of kGraphSliceBucket): a replay covers every position whose context fits
+  std::map<uint32_t, LisaGraph*> step_graphs;
   // per-launch timing of eager steps (lisa_runner_profile_step)
   std::vector<LisaProfRec> prof;
 };
@@ -174,6 +181,15 @@ int k_index(uint32_t k) {
 bool qmv_split(uint32_t k) { return k != LISA_HIDDEN; }
 
 uint32_t qmv_grid(uint32_t k, uint32_t tiles) { return qmv_split(k) ? tiles : (tiles + 3) / 4; }
+
+// Attention slices a launch covers: every 64-token slice up to the position
+// of its last row (the reference sizes its slice grid to the live context,
+// runner.rs:1498-1500); a captured step rounds up to kGraphSliceBucket.
+uint32_t att_slices(const LisaRunner* r, uint32_t last_pos, bool bucket) {
+  uint32_t s = last_pos / LISA_ATT_SLICE + 1;
+  if (bucket) s = (s + kGraphSliceBucket - 1) / kGraphSliceBucket * kGraphSliceBucket;
+  return std::min(s, r->s_max);
+}
 
 // workgroups of the lm_head launch = number of argmax partials per row
 int lm_head_grid(const LisaRunner* r) {
@@ -450,8 +466,9 @@ int launch_resid(LisaRunner* r, Ctx& c, int m, uint32_t K, const uint16_t* x, co
   return launch_qmv(r, m, K, p, {{&w, nullptr, nullptr, LISA_EPI_RESID}});
 }
 
-int launch_attention(LisaRunner* r, Ctx& c, int m, const uint16_t* qn, const uint16_t* kn, uint16_t* kc,
-                     uint16_t* vc) {
+// `slices`: the partial grid (att_slices); slices past the context exit.
+int launch_attention(LisaRunner* r, Ctx& c, int m, uint32_t slices, const uint16_t* qn, const uint16_t* kn,
+                     uint16_t* kc, uint16_t* vc) {
   LisaAttnParams a{};
   a.q_proj = c.q_proj;
   a.k_raw = c.k_raw;
@@ -468,7 +485,8 @@ int launch_attention(LisaRunner* r, Ctx& c, int m, const uint16_t* qn, const uin
   a.s_max = r->s_max;
   const int mi = m == 3 ? 1 : 0;
   LISA_TRY(prof_mark(r, LISA_KIND_ATTN_PARTIAL));
-  LISA_TRY(lisa_launch(r->dev, r->attn_part[mi], &a, sizeof a, r->s_max, LISA_ATT_KVH, 1, 256, 1, 1));
+  if (slices == 0 || slices > r->s_max) return lisa_fail(LISA_E_ARG, "attention grid of %u slices", slices);
+  LISA_TRY(lisa_launch(r->dev, r->attn_part[mi], &a, sizeof a, slices, LISA_ATT_KVH, 1, 256, 1, 1));
   LISA_TRY(prof_mark(r, LISA_KIND_ATTN_MERGE));
   return lisa_launch(r->dev, r->attn_merge[mi], &a, sizeof a, LISA_ATT_QH, m, 1, 256, 1, 1);
 }
@@ -511,7 +529,8 @@ int launch_finalize(LisaRunner* r, Ctx& c, int m, bool feedback, uint32_t advanc
 // One target forward of m rows (runner.rs:555-591 for m=1, 866-909 for m=3).
 // prof_mark(kind) is recorded before each launch (and a final -1 mark after
 // the last) when an eager profile step is running.
-int encode_target(LisaRunner* r, int m, bool capture, bool feedback) {
+// `slices`: attention slices per launch (att_slices of the last row's position).
+int encode_target(LisaRunner* r, int m, bool capture, bool feedback, uint32_t slices) {
   Ctx& c = r->tgt;
   const float inv = 1.0f / lisa_sqrt((float)LISA_GDN_HD);  // runner.rs:1316-1317
   for (int i = 0; i < r->cfg.layers; ++i) {
@@ -583,7 +602,7 @@ int encode_target(LisaRunner* r, int m, bool capture, bool feedback) {
                            {&l.k, nullptr, c.k_raw, LISA_EPI_STORE},
                            {&l.v, nullptr, c.v_raw, LISA_EPI_STORE}}));
       const size_t off = (size_t)l.cache_index * LISA_ATT_KVH * r->cfg.capacity * LISA_ATT_HD;
-      LISA_TRY(launch_attention(r, c, m, l.q_norm, l.k_norm, r->key_cache + off, r->value_cache + off));
+      LISA_TRY(launch_attention(r, c, m, slices, l.q_norm, l.k_norm, r->key_cache + off, r->value_cache + off));
       LISA_TRY(prof_mark(r, LISA_KIND_ATTN_OUT));
       LISA_TRY(launch_resid(r, c, m, LISA_ATT_OUT, c.gated, l.o));
     }
@@ -618,7 +637,8 @@ int encode_mtp(LisaRunner* r, const uint16_t* cond) {
                       {{&t.q, nullptr, c.q_proj, LISA_EPI_STORE},
                        {&t.k, nullptr, c.k_raw, LISA_EPI_STORE},
                        {&t.v, nullptr, c.v_raw, LISA_EPI_STORE}}));
-  LISA_TRY(launch_attention(r, c, 1, t.q_norm, t.k_norm, r->mtp_key, r->mtp_value));
+  LISA_TRY(launch_attention(r, c, 1, att_slices(r, r->mtp_position, false), t.q_norm, t.k_norm, r->mtp_key,
+                            r->mtp_value));
   LISA_TRY(launch_resid(r, c, 1, LISA_ATT_OUT, c.gated, t.o));
   LISA_TRY(launch_mlp(r, c, 1, t.post_norm, t.gate, t.up, t.down));
   LISA_TRY(launch_lm_head(r, c, 1, t.final_norm, c.xnorm));
@@ -650,10 +670,17 @@ int check_token(const LisaRunner* r, uint32_t token) {
   return LISA_OK;
 }
 
-// Record the M=1 step (with device-side token/position feedback) as a graph.
-int capture_step(LisaRunner* r) {
+// The captured M=1 step (device-side token/position feedback) that covers
+// position `pos`: recorded on first use for its slice bucket.
+int step_graph_for(LisaRunner* r, uint32_t pos, LisaGraph** out) {
+  const uint32_t slices = att_slices(r, pos, true);
+  auto it = r->step_graphs.find(slices);
+  if (it != r->step_graphs.end()) {
+    *out = it->second;
+    return LISA_OK;
+  }
   LISA_TRY(lisa_capture_begin(r->dev));
-  const int rc = encode_target(r, 1, false, true);
+  const int rc = encode_target(r, 1, false, true, slices);
   LisaGraph* g = nullptr;
   const int re = lisa_capture_end(r->dev, &g);
   if (rc) {
@@ -661,7 +688,8 @@ int capture_step(LisaRunner* r) {
     return rc;
   }
   LISA_TRY(re);
-  r->step_graph = g;
+  r->step_graphs[slices] = g;
+  *out = g;
   return LISA_OK;
 }
 
@@ -672,10 +700,11 @@ int do_decode(LisaRunner* r, uint32_t token, uint32_t* argmax, float* hidden, fl
   Ctx& c = r->tgt;
   LISA_TRY(upload_u32(r, c.tokens, &token, 1));
   if (r->cfg.use_graph) {
-    if (!r->step_graph) LISA_TRY(capture_step(r));
-    LISA_TRY(lisa_graph_launch(r->step_graph, r->dev));
+    LisaGraph* g = nullptr;
+    LISA_TRY(step_graph_for(r, r->position, &g));
+    LISA_TRY(lisa_graph_launch(g, r->dev));
   } else {
-    LISA_TRY(encode_target(r, 1, false, true));
+    LISA_TRY(encode_target(r, 1, false, true, att_slices(r, r->position, false)));
   }
   uint32_t am = 0;
   LISA_TRY(lisa_hip_check(hipMemcpyAsync(&am, c.argmax, 4, hipMemcpyDeviceToHost, r->dev->stream), "D2H argmax"));
@@ -780,7 +809,7 @@ extern "C" int lisa_runner_create(const LisaRunnerConfig* cfg, LisaRunner** out)
 extern "C" void lisa_runner_free(LisaRunner* r) {
   if (!r) return;
   if (r->dev) (void)hipStreamSynchronize(r->dev->stream);
-  lisa_graph_free(r->step_graph);
+  for (auto& kv : r->step_graphs) lisa_graph_free(kv.second);
   for (auto& a : r->qmv)
     for (auto& b : a)
       for (LisaFunction* f : b) delete f;
@@ -873,15 +902,17 @@ extern "C" int lisa_runner_decode_greedy(LisaRunner* r, uint32_t token, int32_t 
     return lisa_fail(LISA_E_CAPACITY, "KV capacity %d exhausted by %d steps", r->cfg.capacity, steps);
   if ((uint32_t)steps > kHistoryCap) return lisa_fail(LISA_E_ARG, "at most %u steps per call", kHistoryCap);
   Ctx& c = r->tgt;
-  if (r->cfg.use_graph && !r->step_graph) LISA_TRY(capture_step(r));
   const uint32_t zero = 0;
   LISA_TRY(upload_u32(r, c.tokens, &token, 1));
   LISA_TRY(upload_u32(r, c.step, &zero, 1));
   for (int s = 0; s < steps; ++s) {
-    if (r->step_graph) {
-      LISA_TRY(lisa_graph_launch(r->step_graph, r->dev));
+    const uint32_t pos = r->position + (uint32_t)s;
+    if (r->cfg.use_graph) {
+      LisaGraph* g = nullptr;
+      LISA_TRY(step_graph_for(r, pos, &g));
+      LISA_TRY(lisa_graph_launch(g, r->dev));
     } else {
-      LISA_TRY(encode_target(r, 1, false, true));
+      LISA_TRY(encode_target(r, 1, false, true, att_slices(r, pos, false)));
     }
   }
   LISA_TRY(lisa_hip_check(hipMemcpyAsync(tokens_out, c.history, (size_t)steps * 4, hipMemcpyDeviceToHost, r->dev->stream),
@@ -907,7 +938,7 @@ extern "C" int lisa_runner_profile_step(LisaRunner* r, uint32_t token, int32_t s
   r->prof.clear();
   r->dev->prof = &r->prof;
   int rc = LISA_OK;
-  for (int s = 0; s < steps && !rc; ++s) rc = encode_target(r, 1, false, true);
+  for (int s = 0; s < steps && !rc; ++s) rc = encode_target(r, 1, false, true, att_slices(r, r->position + s, false));
   r->dev->prof = nullptr;
   r->dev->prof_kind = -1;
   if (!rc) rc = sync(r);
@@ -936,7 +967,7 @@ extern "C" int lisa_runner_verify_block3(LisaRunner* r, const uint32_t tokens[3]
     return lisa_fail(LISA_E_CAPACITY, "KV capacity %d exhausted", r->cfg.capacity);
   Ctx& c = r->tgt;
   LISA_TRY(upload_u32(r, c.tokens, tokens, 3));
-  LISA_TRY(encode_target(r, 3, true, false));
+  LISA_TRY(encode_target(r, 3, true, false, att_slices(r, r->position + 2, false)));
   uint32_t am[3];
   LISA_TRY(lisa_hip_check(hipMemcpyAsync(am, c.argmax, 12, hipMemcpyDeviceToHost, r->dev->stream), "D2H argmax"));
   LISA_TRY(sync(r));

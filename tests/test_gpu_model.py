@@ -183,3 +183,30 @@ def test_mtp_checkpoint_restore(pair):
     r.free_mtp_checkpoint(ck)
     bad = r.mtp_checkpoint_state()
     r.free_mtp_checkpoint(bad)
+
+
+def test_graph_buckets_follow_the_context():
+    """The captured step launches attention slices for the live context
+    (runner.rs:1498-1500) in buckets of 512 positions: greedy decoding across
+    a bucket boundary switches graphs and still equals the oracle token for
+    token, on a runner whose capacity is far above the context."""
+    pkg, orc = load_pkg(), load_oracle()
+    cap = 2100
+    r = pkg.Runner(layers=LAYERS, vocab=VOCAB, capacity=cap, seed=SEED, use_graph=True)
+    m = orc.Model(LAYERS, VOCAB, cap, SEED)
+    try:
+        r.fill_state(500, CTX_SEED)
+        m.fill_state(500, CTX_SEED)
+        got = r.decode_greedy(41, 30)  # positions 500..529: slice buckets 8 then 16
+        tok, want = 41, []
+        for _ in range(30):
+            wam, _ = m.forward([tok])
+            tok = int(wam[0])
+            want.append(tok)
+        assert list(got) == want
+        am, h = r.forward_token_decode(tok, want_hidden=True)
+        wam, wh = m.forward([tok])
+        assert am == int(wam[0]) and np.array_equal(h.view(np.uint32), wh[0].view(np.uint32))
+    finally:
+        r.close()
+        m.close()
