@@ -134,6 +134,16 @@ uint64_t lisa_attention_workspace_bytes(uint32_t m_rows, uint32_t max_pos);
  * workspace per device, allocated and grown with hipMalloc on demand. Queued
  * on the device stream (no wait). */
 int lisa_attention_decode(LisaDevice* dev, LisaModule* mod, const LisaAttnDecodeArgs* args, LisaBuffer* workspace);
+/* No counterpart in the reference. For callers that cannot allocate device
+ * memory (HIP graph capture, tight serving loops, hosts that forbid hipMalloc):
+ * lisa_attention_decode with the slice partials in a fixed scratch array of
+ * the library (LISA_NOALLOC_SCRATCH_BYTES per GPU, held until the process
+ * ends); it calls no allocator. Rejects (LISA_E_ARG) a call whose
+ * lisa_attention_workspace_bytes exceed the scratch: up to position 43327 at
+ * one row, 14399 at three. Calls that overlap on one GPU share the scratch and
+ * race; calls queued on one stream do not. */
+#define LISA_NOALLOC_SCRATCH_BYTES (16u << 20)
+int lisa_attention_decode_noalloc(LisaDevice* dev, LisaModule* mod, const LisaAttnDecodeArgs* args);
 
 /* ============================ runner (runner.rs) ========================= */
 typedef struct LisaRunner LisaRunner;

@@ -197,6 +197,7 @@ _SIGS = {
     "lisa_event_elapsed_ms": (C.c_int, [_P, _P, C.POINTER(C.c_float)]),
     "lisa_attention_workspace_bytes": (C.c_uint64, [C.c_uint32, C.c_uint32]),
     "lisa_attention_decode": (C.c_int, [_P, _P, C.POINTER(AttnDecodeArgs), _P]),
+    "lisa_attention_decode_noalloc": (C.c_int, [_P, _P, C.POINTER(AttnDecodeArgs)]),
     "lisa_runner_create": (C.c_int, [C.POINTER(RunnerConfig), C.POINTER(_P)]),
     "lisa_runner_free": (None, [_P]),
     "lisa_runner_device": (_P, [_P]),
@@ -357,6 +358,12 @@ class Device:
     def attention_decode(self, args: "AttnDecodeArgs", workspace: "Buffer | None" = None, wait: bool = True) -> None:
         """lisa_attention_decode: one decode layer's attention core (config 2)."""
         _check(lib().lisa_attention_decode(self.h, self.module, C.byref(args), workspace.h if workspace else None))
+        if wait:
+            self.synchronize()
+
+    def attention_decode_noalloc(self, args: "AttnDecodeArgs", wait: bool = True) -> None:
+        """lisa_attention_decode_noalloc: the same with the library's fixed scratch."""
+        _check(lib().lisa_attention_decode_noalloc(self.h, self.module, C.byref(args)))
         if wait:
             self.synchronize()
 
