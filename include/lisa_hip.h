@@ -161,6 +161,71 @@ typedef struct LisaRunnerConfig {
 /* Load: allocate the resident weight arena, generate the synthetic
  * checkpoint in it, allocate state/KV/scratch, reset state. */
 int lisa_runner_create(const LisaRunnerConfig* cfg, LisaRunner** out);
+
+/* ============ checkpoint (src/format/safetensor.rs, src/model/weights.rs) ==
+ * Host-only (no device call): a snapshot can be opened and validated before a
+ * device exists. */
+/* Dtype of a safetensors header entry, in the order of the reference's enum
+ * (src/format/dtype.rs:3-16). */
+enum {
+  LISA_DT_BOOL = 0, LISA_DT_U8, LISA_DT_U16, LISA_DT_I16, LISA_DT_F16, LISA_DT_BF16,
+  LISA_DT_U32, LISA_DT_I32, LISA_DT_F32, LISA_DT_U64, LISA_DT_F64
+};
+#define LISA_MAX_DIMS 8
+typedef struct LisaWeightIndex LisaWeightIndex;
+/* WeightSlot (weights.rs:7-14): shard, byte offset from the start of that
+ * shard's data region (the shard's data region starts at data_start of the
+ * file: 8 + header length), byte length, dtype, shape. */
+typedef struct LisaWeightSlot {
+  int32_t shard;
+  int32_t dtype;
+  int32_t ndim;
+  int32_t pad0;
+  uint64_t offset;
+  uint64_t data_start;
+  uint64_t len;
+  uint64_t shape[LISA_MAX_DIMS];
+} LisaWeightSlot;
+/* WeightIndex::open (weights.rs:22-42) over safetensors shards
+ * (safetensor.rs:27-89: u64 LE header length, JSON header, data): each shard
+ * memory-mapped read-only; "__"-prefixed header keys skipped; a name in two
+ * shards is an error ("duplicate tensor <name>"), as are unknown dtypes
+ * ("unknown dtype <name>") and byte ranges outside the data region or not
+ * equal to dtype size x shape. */
+int lisa_weight_index_open(const char* const* paths, int32_t n, LisaWeightIndex** out);
+/* The sorted *.safetensors files of a snapshot directory (runner.rs:345-357):
+ * "read snapshot <dir>: <error>" / "no safetensors shards in <dir>". */
+int lisa_weight_index_open_snapshot(const char* dir, LisaWeightIndex** out);
+void lisa_weight_index_free(LisaWeightIndex* idx);
+int32_t lisa_weight_index_len(const LisaWeightIndex* idx);         /* WeightIndex::len */
+int32_t lisa_weight_index_shard_count(const LisaWeightIndex* idx); /* WeightIndex::shard_count */
+/* WeightIndex::slot (weights.rs:44-46); LISA_E_ARG "missing tensor <name>". */
+int lisa_weight_index_slot(const LisaWeightIndex* idx, const char* name, LisaWeightSlot* out);
+/* The checks of build_layers / q4() / bf16() / slot() (runner.rs:3769-3946)
+ * for a model of `layers` layers (0 = 64) and vocabulary `vocab` (0 = 248320)
+ * — every tensor the runner reads present with its dtype and shape, messages
+ * "missing tensor <name>" / "invalid tensor <name>: <dtype> <shape>, expected
+ * <dtype> <shape>" — or, with mtp != 0, those of build_mtp_weights
+ * (runner.rs:3861-3928) after MtpRunner::load's count check (runner.rs:2452-2457,
+ * "invalid MTP checkpoint: found <n> tensors, expected 31"). */
+int lisa_weight_index_validate(const LisaWeightIndex* idx, int32_t layers, int32_t vocab, int32_t mtp);
+
+/* QwenRunner::load (runner.rs:337-417) and, when mtp_snapshot is non-null,
+ * MtpRunner::load (runner.rs:2443-2502) sharing the target's embedding and
+ * lm_head: the snapshots' shards are validated as above, then copied once
+ * into the resident weight arena in the kernels' layout (packed words as
+ * stored; each 64-group's bf16 scale and bias interleaved into one 32-bit
+ * word). cfg supplies capacity, use_graph and device; cfg->layers and
+ * cfg->vocab give the expected geometry (0 = the reference's 64 and 248320);
+ * cfg->with_mtp and cfg->seed are ignored. */
+int lisa_runner_load(const char* target_snapshot, const char* mtp_snapshot, const LisaRunnerConfig* cfg,
+                     LisaRunner** out);
+/* MtpRunner::load(target, snapshot, capacity) (runner.rs:2443-2502) on a
+ * runner loaded or created without a drafter: validates the snapshot (31
+ * tensors), allocates the drafter's weights and KV caches (capacity must equal
+ * the target's) and uploads them; the drafter starts at position 0.
+ * LISA_E_STATE if the runner already holds one. */
+int lisa_mtp_load(LisaRunner* r, const char* mtp_snapshot, int32_t capacity);
 void lisa_runner_free(LisaRunner* r);
 LisaDevice* lisa_runner_device(LisaRunner* r);
 uint32_t lisa_runner_position(LisaRunner* r);

@@ -141,6 +141,16 @@ class RunnerConfig(C.Structure):
                 ("seed", C.c_uint64), ("use_graph", C.c_int32), ("device", C.c_int32)]
 
 
+MAX_DIMS = 8
+DTYPES = ["BOOL", "U8", "U16", "I16", "F16", "BF16", "U32", "I32", "F32", "U64", "F64"]
+
+
+class WeightSlotStruct(C.Structure):
+    _fields_ = [("shard", C.c_int32), ("dtype", C.c_int32), ("ndim", C.c_int32), ("pad0", C.c_int32),
+                ("offset", C.c_uint64), ("data_start", C.c_uint64), ("len", C.c_uint64),
+                ("shape", C.c_uint64 * MAX_DIMS)]
+
+
 class Acceptance(C.Structure):
     _fields_ = [("accepted_drafts", C.c_int32), ("emitted_count", C.c_int32), ("emitted", C.c_uint32 * 3),
                 ("target_trim", C.c_int32)]
@@ -200,6 +210,15 @@ _SIGS = {
     "lisa_attention_decode_noalloc": (C.c_int, [_P, _P, C.POINTER(AttnDecodeArgs)]),
     "lisa_runner_create": (C.c_int, [C.POINTER(RunnerConfig), C.POINTER(_P)]),
     "lisa_runner_free": (None, [_P]),
+    "lisa_runner_load": (C.c_int, [C.c_char_p, C.c_char_p, C.POINTER(RunnerConfig), C.POINTER(_P)]),
+    "lisa_mtp_load": (C.c_int, [_P, C.c_char_p, C.c_int32]),
+    "lisa_weight_index_open": (C.c_int, [C.POINTER(C.c_char_p), C.c_int32, C.POINTER(_P)]),
+    "lisa_weight_index_open_snapshot": (C.c_int, [C.c_char_p, C.POINTER(_P)]),
+    "lisa_weight_index_free": (None, [_P]),
+    "lisa_weight_index_len": (C.c_int32, [_P]),
+    "lisa_weight_index_shard_count": (C.c_int32, [_P]),
+    "lisa_weight_index_slot": (C.c_int, [_P, C.c_char_p, C.POINTER(WeightSlotStruct)]),
+    "lisa_weight_index_validate": (C.c_int, [_P, C.c_int32, C.c_int32, C.c_int32]),
     "lisa_runner_device": (_P, [_P]),
     "lisa_runner_position": (C.c_uint32, [_P]),
     "lisa_runner_weight_bytes": (C.c_uint64, [_P]),
@@ -398,16 +417,75 @@ def mtp_reconcile_plan(draft_count: int, round_appended: int, accepted: int):
     return p.trim, replay
 
 
+class WeightIndex:
+    """WeightIndex (src/model/weights.rs) over safetensors shards, host-only."""
+
+    def __init__(self, paths=None, snapshot=None):
+        h = C.c_void_p()
+        if snapshot is not None:
+            _check(lib().lisa_weight_index_open_snapshot(str(snapshot).encode(), C.byref(h)))
+        else:
+            arr = (C.c_char_p * len(paths))(*[str(x).encode() for x in paths])
+            _check(lib().lisa_weight_index_open(arr, len(paths), C.byref(h)))
+        self.h = h
+
+    def close(self) -> None:
+        if getattr(self, "h", None):
+            lib().lisa_weight_index_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def __len__(self) -> int:
+        return lib().lisa_weight_index_len(self.h)
+
+    @property
+    def shard_count(self) -> int:
+        return lib().lisa_weight_index_shard_count(self.h)
+
+    def slot(self, name: str) -> dict:
+        s = WeightSlotStruct()
+        _check(lib().lisa_weight_index_slot(self.h, name.encode(), C.byref(s)))
+        return {"shard": s.shard, "dtype": DTYPES[s.dtype], "shape": [s.shape[i] for i in range(s.ndim)],
+                "offset": s.offset, "data_start": s.data_start, "len": s.len}
+
+    def validate(self, layers: int = 0, vocab: int = 0, mtp: bool = False) -> None:
+        _check(lib().lisa_weight_index_validate(self.h, layers, vocab, 1 if mtp else 0))
+
+
 class Runner:
-    """QwenRunner + MtpRunner on one MI355X over synthetic q4 weights."""
+    """QwenRunner + MtpRunner on one MI355X over synthetic q4 weights, or over
+    a safetensors checkpoint (Runner.load)."""
 
     def __init__(self, layers: int = LAYERS, vocab: int = VOCAB, capacity: int = 4352, seed: int = 0x15A2026,
-                 with_mtp: bool = False, use_graph: bool = True, device: int = 0):
-        cfg = RunnerConfig(layers, vocab, capacity, 1 if with_mtp else 0, seed, 1 if use_graph else 0, device)
-        h = C.c_void_p()
-        _check(lib().lisa_runner_create(C.byref(cfg), C.byref(h)))
+                 with_mtp: bool = False, use_graph: bool = True, device: int = 0, _handle=None):
+        if _handle is None:
+            cfg = RunnerConfig(layers, vocab, capacity, 1 if with_mtp else 0, seed, 1 if use_graph else 0, device)
+            h = C.c_void_p()
+            _check(lib().lisa_runner_create(C.byref(cfg), C.byref(h)))
+        else:
+            h = _handle
         self.h = h
         self.layers, self.vocab, self.capacity, self.seed = layers, vocab, capacity, seed
+
+    @classmethod
+    def load(cls, target_snapshot, mtp_snapshot=None, capacity: int = 4352, layers: int = LAYERS,
+             vocab: int = VOCAB, use_graph: bool = True, device: int = 0) -> "Runner":
+        """QwenRunner::load (+ MtpRunner::load) from snapshot directories."""
+        cfg = RunnerConfig(layers, vocab, capacity, 0, 0, 1 if use_graph else 0, device)
+        h = C.c_void_p()
+        _check(lib().lisa_runner_load(str(target_snapshot).encode(),
+                                      None if mtp_snapshot is None else str(mtp_snapshot).encode(),
+                                      C.byref(cfg), C.byref(h)))
+        return cls(layers, vocab, capacity, 0, mtp_snapshot is not None, use_graph, device, _handle=h)
+
+    def load_mtp(self, mtp_snapshot, capacity: int) -> None:
+        """MtpRunner::load(target, snapshot, capacity) into this runner."""
+        _check(lib().lisa_mtp_load(self.h, str(mtp_snapshot).encode(), capacity))
 
     def close(self) -> None:
         if getattr(self, "h", None):

@@ -1780,7 +1780,7 @@ DEV void q4_gemm_body(const LisaGemmParams& p, uint16_t (*As)[GEMM_BM * GEMM_PAD
     const uint32_t st_ = min((uint32_t)(STEP), nk - 1);                                   \
     _Pragma("unroll") for (int i = 0; i < G::RA; ++i) A[i] = asrc[i][st_ * 8];            \
     _Pragma("unroll") for (int r = 0; r < G::RW; ++r) W[r] = wsrc[st_ * 2 + r];           \
-    SB = sbsrc[st_];                                                                      \
+    SB = sbsrc[st_] & ((uint32_t)(STEP) < nk ? 0xffffffffu : 0u);                         \
   }
   lisa_u32x4 a0[G::RA], a1[G::RA], w0[G::RW], w1[G::RW];
   uint32_t sb0, sb1;
@@ -1788,11 +1788,15 @@ DEV void q4_gemm_body(const LisaGemmParams& p, uint16_t (*As)[GEMM_BM * GEMM_PAD
   GEMM_GLOAD(a1, w1, sb1, 1);
   gemm_lstore<BN, NT>(As[0], Ws[0], tid, a0, w0, sb0);
   __syncthreads();
+  // Pairs of K steps. With an odd number of steps the second half of the
+  // last pair is a phantom step past K whose scale and bias words are zero, so
+  // its dequantized W rows are zero and it adds nothing; an exit inside the
+  // pair, or a separate tail step, would keep the accumulators out of the
+  // matrix registers (the eight-wave tile then spills).
   for (uint32_t step = 0; step < nk; step += 2) {
     GEMM_GLOAD(a0, w0, sb0, step + 2);
     gemm_step<BN, NT>(As[0], Ws[0], As[1], Ws[1], tid, wm, wn, lane, a1, w1, sb1, acc);
     __syncthreads();
-    if (step + 1 >= nk) break;  // odd number of K steps: the last one is done
     GEMM_GLOAD(a1, w1, sb1, step + 3);
     gemm_step<BN, NT>(As[1], Ws[1], As[0], Ws[0], tid, wm, wn, lane, a0, w0, sb0, acc);
     __syncthreads();

@@ -27,6 +27,7 @@
 
 #include "bridge.h"
 #include "lisa_hip.h"
+#include "loader.h"
 #include "lisa_kernels.h"
 #include "lisa_model.h"
 #include "lisa_numerics.h"
@@ -126,6 +127,8 @@ struct LisaRunner {
                *attn_partial_rows = nullptr, *attn_merge_rows = nullptr;
   // memory
   LisaBuffer *weights = nullptr, *state = nullptr, *scratch = nullptr;
+  // a drafter loaded after the target (lisa_mtp_load): its weights and KV
+  LisaBuffer *mtp_weights = nullptr, *mtp_state = nullptr;
   std::vector<LayerDev> layers;
   Q4Dev embed, head;
   uint16_t* final_norm = nullptr;
@@ -243,6 +246,8 @@ Q4Dev take_q4(Arena& A, uint32_t n, uint32_t k) {
   return q;
 }
 
+void plan_mtp_weights(LisaRunner* r, Arena& A);
+
 void plan_weights(LisaRunner* r, Arena& A) {
   const int L = r->cfg.layers;
   r->layers.assign(L, LayerDev());
@@ -279,7 +284,13 @@ void plan_weights(LisaRunner* r, Arena& A) {
   r->embed = take_q4(A, r->cfg.vocab, LISA_HIDDEN);
   r->head = take_q4(A, r->cfg.vocab, LISA_HIDDEN);
   r->final_norm = A.take<uint16_t>(LISA_HIDDEN);
-  if (r->cfg.with_mtp) {
+  if (r->cfg.with_mtp) plan_mtp_weights(r, A);
+}
+
+// The drafter's own tensors (MtpWeights, runner.rs:2452-2457); it shares the
+// target's embedding and lm_head.
+void plan_mtp_weights(LisaRunner* r, Arena& A) {
+  {
     MtpDev& t = r->mtp;
     t.pre_fc_emb = A.take<uint16_t>(LISA_HIDDEN);
     t.pre_fc_hid = A.take<uint16_t>(LISA_HIDDEN);
@@ -352,6 +363,150 @@ int generate_weights(LisaRunner* r) {
   return sync(r);
 }
 
+// ---- real checkpoint ---------------------------------------------------------
+// One tensor the runner reads, under its checkpoint name: a q4 linear (the
+// prefix of its .weight / .scales / .biases, q4() of runner.rs:3906-3928) or
+// a bf16 tensor of a fixed shape (bf16(), :3930-3932).
+struct WeightEntry {
+  std::string name;
+  const Q4Dev* q = nullptr;  // q4 destination (its n, k give the shapes)
+  uint16_t* vec = nullptr;   // bf16 destination
+  std::vector<uint64_t> shape;
+};
+
+void cat_q4(std::vector<WeightEntry>& c, const std::string& name, const Q4Dev& q) {
+  WeightEntry e;
+  e.name = name;
+  e.q = &q;
+  c.push_back(e);
+}
+
+void cat_vec(std::vector<WeightEntry>& c, const std::string& name, uint16_t* v, std::vector<uint64_t> shape) {
+  WeightEntry e;
+  e.name = name;
+  e.vec = v;
+  e.shape = std::move(shape);
+  c.push_back(e);
+}
+
+// The target's tensors in the order the reference resolves them: build_layers
+// (runner.rs:3769-3860), then embed_tokens, norm, lm_head (:359-361).
+std::vector<WeightEntry> target_catalogue(const LisaRunner* r) {
+  std::vector<WeightEntry> c;
+  const uint64_t H = LISA_HIDDEN;
+  for (int i = 0; i < r->cfg.layers; ++i) {
+    const LayerDev& l = r->layers[i];
+    const std::string pre = "language_model.model.layers." + std::to_string(i);
+    cat_vec(c, pre + ".input_layernorm.weight", l.input_norm, {H});
+    cat_vec(c, pre + ".post_attention_layernorm.weight", l.post_norm, {H});
+    cat_q4(c, pre + ".mlp.gate_proj", l.gate);
+    cat_q4(c, pre + ".mlp.up_proj", l.up);
+    cat_q4(c, pre + ".mlp.down_proj", l.down);
+    if (!l.attention) {
+      const std::string p = pre + ".linear_attn";
+      cat_q4(c, p + ".in_proj_qkv", l.qkv);
+      cat_q4(c, p + ".in_proj_z", l.z);
+      cat_q4(c, p + ".in_proj_a", l.a);
+      cat_q4(c, p + ".in_proj_b", l.b);
+      cat_q4(c, p + ".out_proj", l.out);
+      cat_vec(c, p + ".conv1d.weight", l.conv_w, {LISA_GDN_CONV_DIM, LISA_GDN_CONV_K, 1});
+      cat_vec(c, p + ".A_log", l.a_log, {LISA_GDN_VH});
+      cat_vec(c, p + ".dt_bias", l.dt_bias, {LISA_GDN_VH});
+      cat_vec(c, p + ".norm.weight", l.gnorm, {LISA_GDN_HD});
+    } else {
+      const std::string p = pre + ".self_attn";
+      cat_q4(c, p + ".q_proj", l.q);
+      cat_q4(c, p + ".k_proj", l.k);
+      cat_q4(c, p + ".v_proj", l.v);
+      cat_q4(c, p + ".o_proj", l.o);
+      cat_vec(c, p + ".q_norm.weight", l.q_norm, {LISA_ATT_HD});
+      cat_vec(c, p + ".k_norm.weight", l.k_norm, {LISA_ATT_HD});
+    }
+  }
+  cat_q4(c, "language_model.model.embed_tokens", r->embed);
+  cat_vec(c, "language_model.model.norm.weight", r->final_norm, {H});
+  cat_q4(c, "language_model.lm_head", r->head);
+  return c;
+}
+
+// The drafter's 31 tensors (build_mtp_weights, runner.rs:3861-3928).
+std::vector<WeightEntry> mtp_catalogue(const LisaRunner* r) {
+  std::vector<WeightEntry> c;
+  const uint64_t H = LISA_HIDDEN;
+  const MtpDev& t = r->mtp;
+  cat_vec(c, "pre_fc_norm_embedding.weight", t.pre_fc_emb, {H});
+  cat_vec(c, "pre_fc_norm_hidden.weight", t.pre_fc_hid, {H});
+  cat_q4(c, "fc", t.fc);
+  cat_vec(c, "layers.0.input_layernorm.weight", t.input_norm, {H});
+  cat_q4(c, "layers.0.self_attn.q_proj", t.q);
+  cat_q4(c, "layers.0.self_attn.k_proj", t.k);
+  cat_q4(c, "layers.0.self_attn.v_proj", t.v);
+  cat_q4(c, "layers.0.self_attn.o_proj", t.o);
+  cat_vec(c, "layers.0.self_attn.q_norm.weight", t.q_norm, {LISA_ATT_HD});
+  cat_vec(c, "layers.0.self_attn.k_norm.weight", t.k_norm, {LISA_ATT_HD});
+  cat_vec(c, "layers.0.post_attention_layernorm.weight", t.post_norm, {H});
+  cat_q4(c, "layers.0.mlp.gate_proj", t.gate);
+  cat_q4(c, "layers.0.mlp.up_proj", t.up);
+  cat_q4(c, "layers.0.mlp.down_proj", t.down);
+  cat_vec(c, "norm.weight", t.final_norm, {H});
+  return c;
+}
+
+constexpr int kMtpTensors = 31;  // MtpRunner::load (runner.rs:2452-2457)
+
+// slot() checks of every entry: q4 = U32 [out, in/8] + BF16 [out, in/64] twice.
+int check_catalogue(const LisaWeightIndex* idx, const std::vector<WeightEntry>& cat) {
+  for (const WeightEntry& e : cat) {
+    if (e.q) {
+      const uint64_t n = e.q->n, k = e.q->k;
+      LISA_TRY(lisa_index_expect(idx, e.name + ".weight", LISA_DT_U32, {n, k / 8}, nullptr));
+      LISA_TRY(lisa_index_expect(idx, e.name + ".scales", LISA_DT_BF16, {n, k / 64}, nullptr));
+      LISA_TRY(lisa_index_expect(idx, e.name + ".biases", LISA_DT_BF16, {n, k / 64}, nullptr));
+    } else {
+      LISA_TRY(lisa_index_expect(idx, e.name, LISA_DT_BF16, e.shape, nullptr));
+    }
+  }
+  return LISA_OK;
+}
+
+// Copies every entry into the planned arena: packed words and bf16 tensors as
+// stored, scales and biases interleaved into the kernels' one word per group
+// (scale | bias << 16).
+int upload_catalogue(LisaRunner* r, const LisaWeightIndex* idx, const std::vector<WeightEntry>& cat) {
+  std::vector<uint32_t> sb;
+  for (const WeightEntry& e : cat) {
+    if (e.q) {
+      const LisaSlotInfo *w, *s, *b;
+      const uint64_t n = e.q->n, k = e.q->k;
+      LISA_TRY(lisa_index_expect(idx, e.name + ".weight", LISA_DT_U32, {n, k / 8}, &w));
+      LISA_TRY(lisa_index_expect(idx, e.name + ".scales", LISA_DT_BF16, {n, k / 64}, &s));
+      LISA_TRY(lisa_index_expect(idx, e.name + ".biases", LISA_DT_BF16, {n, k / 64}, &b));
+      LISA_TRY(lisa_hip_check(hipMemcpy(e.q->w, lisa_index_bytes(idx, *w), w->len, hipMemcpyHostToDevice),
+                              "upload q4 words"));
+      const uint16_t* sp = reinterpret_cast<const uint16_t*>(lisa_index_bytes(idx, *s));
+      const uint16_t* bp = reinterpret_cast<const uint16_t*>(lisa_index_bytes(idx, *b));
+      const size_t groups = (size_t)(n * k / 64);
+      sb.resize(groups);
+      for (size_t g = 0; g < groups; ++g) {
+        uint16_t sv, bv;  // the mapping carries no alignment guarantee
+        std::memcpy(&sv, sp + g, 2);
+        std::memcpy(&bv, bp + g, 2);
+        sb[g] = (uint32_t)sv | ((uint32_t)bv << 16);
+      }
+      LISA_TRY(lisa_hip_check(hipMemcpy(e.q->sb, sb.data(), groups * 4, hipMemcpyHostToDevice),
+                              "upload q4 scales/biases"));
+    } else {
+      const LisaSlotInfo* v;
+      LISA_TRY(lisa_index_expect(idx, e.name, LISA_DT_BF16, e.shape, &v));
+      LISA_TRY(lisa_hip_check(hipMemcpy(e.vec, lisa_index_bytes(idx, *v), v->len, hipMemcpyHostToDevice),
+                              "upload bf16 tensor"));
+    }
+  }
+  return LISA_OK;
+}
+
+void plan_mtp_state(LisaRunner* r, Arena& A);
+
 void plan_state(LisaRunner* r, Arena& A) {
   const size_t cap = (size_t)r->cfg.capacity;
   r->gdn_state = A.take<float>((size_t)r->gdn_layers * LISA_GDN_STATE);
@@ -360,10 +515,14 @@ void plan_state(LisaRunner* r, Arena& A) {
   r->conv_slots = A.take<uint16_t>((size_t)2 * r->gdn_layers * 3 * LISA_GDN_CONV_DIM);
   r->key_cache = A.take<uint16_t>((size_t)r->attn_layers * LISA_ATT_KVH * cap * LISA_ATT_HD);
   r->value_cache = A.take<uint16_t>((size_t)r->attn_layers * LISA_ATT_KVH * cap * LISA_ATT_HD);
-  if (r->cfg.with_mtp) {
-    r->mtp_key = A.take<uint16_t>((size_t)LISA_ATT_KVH * cap * LISA_ATT_HD);
-    r->mtp_value = A.take<uint16_t>((size_t)LISA_ATT_KVH * cap * LISA_ATT_HD);
-  }
+  if (r->cfg.with_mtp) plan_mtp_state(r, A);
+}
+
+// The drafter's KV caches (MtpRunner::load, runner.rs:2469-2476).
+void plan_mtp_state(LisaRunner* r, Arena& A) {
+  const size_t cap = (size_t)r->cfg.capacity;
+  r->mtp_key = A.take<uint16_t>((size_t)LISA_ATT_KVH * cap * LISA_ATT_HD);
+  r->mtp_value = A.take<uint16_t>((size_t)LISA_ATT_KVH * cap * LISA_ATT_HD);
 }
 
 void plan_ctx(LisaRunner* r, Arena& A, Ctx& c, int rows) {
@@ -723,8 +882,12 @@ int do_decode(LisaRunner* r, uint32_t token, uint32_t* argmax, float* hidden, fl
 // =============================================================================
 // C ABI
 // =============================================================================
-extern "C" int lisa_runner_create(const LisaRunnerConfig* cfg, LisaRunner** out) {
-  if (!cfg || !out) return lisa_fail(LISA_E_ARG, "lisa_runner_create: null argument");
+namespace {
+
+// Everything of a runner but its weights' contents: device, kernels, the
+// planned weight arena, state, KV caches and scratch (QwenRunner::load,
+// runner.rs:337-417, after the checkpoint is resolved).
+int runner_init(const LisaRunnerConfig* cfg, std::unique_ptr<LisaRunner>& out) {
   if (cfg->layers <= 0 || cfg->layers % 4 != 0)
     return lisa_fail(LISA_E_ARG, "layers must be a positive multiple of 4 (got %d)", cfg->layers);
   if (cfg->vocab <= 0 || cfg->vocab % 8 != 0) return lisa_fail(LISA_E_ARG, "vocab must be a positive multiple of 8");
@@ -800,9 +963,132 @@ extern "C" int lisa_runner_create(const LisaRunnerConfig* cfg, LisaRunner** out)
   plan_ctx(r.get(), xa, r->tgt, 3);
   plan_ctx(r.get(), xa, r->drf, 1);
 
+  out = std::move(r);
+  return LISA_OK;
+}
+
+// The weight plan of a runner of this geometry without a device (pointers
+// null): the catalogue's shapes for host-only validation.
+void plan_host(LisaRunner& r, int32_t layers, int32_t vocab, bool mtp) {
+  r.cfg.layers = layers;
+  r.cfg.vocab = vocab;
+  r.cfg.with_mtp = mtp ? 1 : 0;
+  Arena a;
+  plan_weights(&r, a);
+}
+
+struct IndexCloser {
+  void operator()(LisaWeightIndex* i) const { lisa_weight_index_free(i); }
+};
+using IndexPtr = std::unique_ptr<LisaWeightIndex, IndexCloser>;
+
+int check_geometry(int32_t layers, int32_t vocab) {
+  if (layers <= 0 || layers % 4 != 0) return lisa_fail(LISA_E_ARG, "layers must be a positive multiple of 4 (got %d)", layers);
+  if (vocab <= 0 || vocab % 8 != 0) return lisa_fail(LISA_E_ARG, "vocab must be a positive multiple of 8");
+  return LISA_OK;
+}
+
+}  // namespace
+
+extern "C" int lisa_runner_create(const LisaRunnerConfig* cfg, LisaRunner** out) {
+  if (!cfg || !out) return lisa_fail(LISA_E_ARG, "lisa_runner_create: null argument");
+  std::unique_ptr<LisaRunner> r;
+  LISA_TRY(runner_init(cfg, r));
   LISA_TRY(generate_weights(r.get()));
   LISA_TRY(lisa_runner_reset_state(r.get()));
   *out = r.release();
+  return LISA_OK;
+}
+
+extern "C" int lisa_weight_index_validate(const LisaWeightIndex* idx, int32_t layers, int32_t vocab, int32_t mtp) {
+  if (!idx) return lisa_fail(LISA_E_ARG, "lisa_weight_index_validate: null index");
+  layers = layers ? layers : LISA_LAYERS;
+  vocab = vocab ? vocab : LISA_VOCAB;
+  LISA_TRY(check_geometry(layers, vocab));
+  LisaRunner plan;
+  plan_host(plan, layers, vocab, mtp != 0);
+  if (mtp) {
+    const int32_t n = lisa_weight_index_len(idx);
+    if (n != kMtpTensors)
+      return lisa_fail(LISA_E_ARG, "invalid MTP checkpoint: found %d tensors, expected %d", n, kMtpTensors);
+    return check_catalogue(idx, mtp_catalogue(&plan));
+  }
+  return check_catalogue(idx, target_catalogue(&plan));
+}
+
+extern "C" int lisa_runner_load(const char* target_snapshot, const char* mtp_snapshot, const LisaRunnerConfig* cfg,
+                                LisaRunner** out) {
+  if (!target_snapshot || !cfg || !out) return lisa_fail(LISA_E_ARG, "lisa_runner_load: null argument");
+  if (cfg->capacity <= 0) return lisa_fail(LISA_E_ARG, "KV capacity must be greater than zero");
+  LisaRunnerConfig c = *cfg;
+  c.layers = c.layers ? c.layers : LISA_LAYERS;
+  c.vocab = c.vocab ? c.vocab : LISA_VOCAB;
+  c.with_mtp = mtp_snapshot ? 1 : 0;
+  c.seed = 0;
+  LISA_TRY(check_geometry(c.layers, c.vocab));
+  LisaWeightIndex* raw = nullptr;
+  LISA_TRY(lisa_weight_index_open_snapshot(target_snapshot, &raw));
+  IndexPtr tgt(raw);
+  LISA_TRY(lisa_weight_index_validate(tgt.get(), c.layers, c.vocab, 0));
+  IndexPtr drf;
+  if (mtp_snapshot) {
+    raw = nullptr;
+    LISA_TRY(lisa_weight_index_open_snapshot(mtp_snapshot, &raw));
+    drf.reset(raw);
+    LISA_TRY(lisa_weight_index_validate(drf.get(), c.layers, c.vocab, 1));
+  }
+  std::unique_ptr<LisaRunner> r;
+  LISA_TRY(runner_init(&c, r));
+  LISA_TRY(upload_catalogue(r.get(), tgt.get(), target_catalogue(r.get())));
+  if (drf) LISA_TRY(upload_catalogue(r.get(), drf.get(), mtp_catalogue(r.get())));
+  LISA_TRY(lisa_runner_reset_state(r.get()));
+  *out = r.release();
+  return LISA_OK;
+}
+
+extern "C" int lisa_mtp_load(LisaRunner* r, const char* mtp_snapshot, int32_t capacity) {
+  if (!r || !mtp_snapshot) return lisa_fail(LISA_E_ARG, "lisa_mtp_load: null argument");
+  if (capacity <= 0) return lisa_fail(LISA_E_ARG, "MTP KV capacity must be greater than zero");
+  if (capacity != r->cfg.capacity)
+    return lisa_fail(LISA_E_ARG, "MTP KV capacity %d differs from the target's %d", capacity, r->cfg.capacity);
+  if (r->cfg.with_mtp) return lisa_fail(LISA_E_STATE, "runner already holds an MTP drafter");
+  LisaWeightIndex* raw = nullptr;
+  LISA_TRY(lisa_weight_index_open_snapshot(mtp_snapshot, &raw));
+  IndexPtr drf(raw);
+  LISA_TRY(lisa_weight_index_validate(drf.get(), r->cfg.layers, r->cfg.vocab, 1));
+  Arena wa;
+  plan_mtp_weights(r, wa);
+  Arena ka;
+  plan_mtp_state(r, ka);
+  LisaBuffer *wb = nullptr, *kb = nullptr;
+  LISA_TRY(lisa_buffer_alloc(r->dev, wa.used, &wb));
+  if (int rc = lisa_buffer_alloc(r->dev, ka.used, &kb)) {
+    lisa_buffer_free(wb);
+    return rc;
+  }
+  wa.base = (char*)wb->ptr;
+  wa.used = 0;
+  plan_mtp_weights(r, wa);
+  ka.base = (char*)kb->ptr;
+  ka.used = 0;
+  plan_mtp_state(r, ka);
+  r->mtp_weights = wb;
+  r->mtp_state = kb;
+  r->cfg.with_mtp = 1;
+  int rc = upload_catalogue(r, drf.get(), mtp_catalogue(r));
+  if (!rc) rc = lisa_hip_check(hipMemsetAsync(kb->ptr, 0, kb->len, r->dev->stream), "memset MTP KV");
+  if (!rc) rc = write_pos(r, r->drf, 0);
+  if (!rc) rc = sync(r);
+  if (rc) {
+    r->cfg.with_mtp = 0;
+    r->mtp = MtpDev{};
+    r->mtp_key = r->mtp_value = nullptr;
+    r->mtp_weights = r->mtp_state = nullptr;
+    lisa_buffer_free(wb);
+    lisa_buffer_free(kb);
+    return rc;
+  }
+  r->mtp_position = 0;
   return LISA_OK;
 }
 
@@ -824,6 +1110,8 @@ extern "C" void lisa_runner_free(LisaRunner* r) {
   lisa_buffer_free(r->scratch);
   lisa_buffer_free(r->state);
   lisa_buffer_free(r->weights);
+  lisa_buffer_free(r->mtp_state);
+  lisa_buffer_free(r->mtp_weights);
   lisa_module_free(r->mod);
   lisa_device_free(r->dev);
   delete r;
@@ -836,6 +1124,8 @@ extern "C" uint64_t lisa_runner_weight_bytes(LisaRunner* r) { return r && r->wei
 extern "C" int lisa_runner_reset_state(LisaRunner* r) {
   if (!r) return lisa_fail(LISA_E_ARG, "null runner");
   LISA_TRY(lisa_hip_check(hipMemsetAsync(r->state->ptr, 0, r->state->len, r->dev->stream), "memset state"));
+  if (r->mtp_state)
+    LISA_TRY(lisa_hip_check(hipMemsetAsync(r->mtp_state->ptr, 0, r->mtp_state->len, r->dev->stream), "memset MTP KV"));
   LISA_TRY(write_pos(r, r->tgt, 0));
   LISA_TRY(write_pos(r, r->drf, 0));
   LISA_TRY(sync(r));

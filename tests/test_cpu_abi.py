@@ -16,7 +16,7 @@ ROOT = Path(__file__).resolve().parents[1]
 def declared_entry_points():
     text = (ROOT / "include" / "lisa_hip.h").read_text()
     text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
-    names = re.findall(r"^\s*(?:const\s+)?(?:int|void|uint32_t|uint64_t|char)\s*\*?\s*(lisa_\w+)\s*\(", text, re.M)
+    names = re.findall(r"^\s*(?:const\s+)?\w+\s*\*?\s*(lisa_\w+)\s*\(", text, re.M)
     return sorted(set(names))
 
 
