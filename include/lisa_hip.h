@@ -269,6 +269,11 @@ enum {
   LISA_KIND_COUNT
 };
 int lisa_runner_profile_step(LisaRunner* r, uint32_t token, int32_t steps, float* kind_ms, int32_t* kind_count);
+/* The same per-kind profile of one eager M=3 verify pass (verify_block3's
+ * launches with slot capture); leaves the runner as lisa_runner_verify_block3
+ * does (position += 3, awaiting commit). No counterpart in the reference, whose
+ * diagnostic covers M=1 only. */
+int lisa_runner_profile_block3(LisaRunner* r, const uint32_t tokens[3], float* kind_ms, int32_t* kind_count);
 
 /* forward_prefill_with_progress (runner.rs:2129-2230): the `n` prompt tokens
  * in chunks of `chunk` rows (<= 2048; 0 = 2048; the reference's PREFILL_BATCH

@@ -229,6 +229,7 @@ _SIGS = {
     "lisa_runner_decode_greedy": (C.c_int, [_P, C.c_uint32, C.c_int32, _P]),
     "lisa_runner_forward_prefill": (C.c_int, [_P, _P, C.c_int32, C.c_int32, _P, _P]),
     "lisa_runner_profile_step": (C.c_int, [_P, C.c_uint32, C.c_int32, _P, _P]),
+    "lisa_runner_profile_block3": (C.c_int, [_P, _P, _P, _P]),
     "lisa_runner_verify_block3": (C.c_int, [_P, _P, _P, _P, _P]),
     "lisa_runner_commit_verified_prefix": (C.c_int, [_P, C.c_int32]),
     "lisa_runner_checkpoint_state": (C.c_int, [_P, C.POINTER(_P)]),
@@ -546,6 +547,14 @@ class Runner:
         ms = np.zeros(len(KINDS), np.float32)
         cnt = np.zeros(len(KINDS), np.int32)
         _check(lib().lisa_runner_profile_step(self.h, token, steps, _ptr(ms), _ptr(cnt)))
+        return {k: (float(ms[i]), int(cnt[i])) for i, k in enumerate(KINDS)}
+
+    def profile_block3(self, tokens) -> dict:
+        """One eager M=3 verify pass with hipEvents around every launch: {kind: (total_ms, launches)}."""
+        t = np.asarray(tokens, dtype=np.uint32)
+        ms = np.zeros(len(KINDS), np.float32)
+        cnt = np.zeros(len(KINDS), np.int32)
+        _check(lib().lisa_runner_profile_block3(self.h, _ptr(t), _ptr(ms), _ptr(cnt)))
         return {k: (float(ms[i]), int(cnt[i])) for i, k in enumerate(KINDS)}
 
     def verify_block3(self, tokens, want_hidden: bool = False, want_logits: bool = False):

@@ -393,9 +393,10 @@ DEV void x_process(unsigned char* lds, int m, const ProRaw<R>& raw) {
 // iteration i (clamped into the wave's range like its weights) and row m, lane
 // l loads the 16 bf16 values [1024 ii + 16 l, 1024 ii + 16 l + 16).
 template <int K, int M>
-DEV void wx_load(const LisaQmvParams& p, int it0, int it1, int lane, uint4 (&xr)[QmvCfg<K, M>::IMAX][M][2]) {
+DEV void wx_load(const LisaQmvParams& p, int it0, int it1, int lane, uint4 (&xr)[QmvCfg<K, M>::IMAX][M][2],
+                 int i0 = 0, int i1 = QmvCfg<K, M>::IMAX) {
 #pragma unroll
-  for (int i = 0; i < QmvCfg<K, M>::IMAX; ++i) {
+  for (int i = i0; i < i1; ++i) {
     const int ii = max(min(it0 + i, it1 - 1), 0);
 #pragma unroll
     for (int m = 0; m < M; ++m) {
@@ -716,7 +717,11 @@ DEV void qmv_body(const LisaQmvParams& p, unsigned char* lds) {
   // first iteration is in flight across it, which keeps the register count low
   // enough for every workgroup of the launch to be resident in one round.
   // Non-split plain-x launches (small and rare) issue their whole stream first.
-  if constexpr (WAVEX) wx_load<K, M>(p, it0, it1, lane, xr);
+  // Several input rows: each iteration's x is loaded with its weights (all of
+  // it up front held 120 registers at three rows, two waves per SIMD).
+  constexpr bool LAZYX = WAVEX && M > 1;
+  constexpr int XDEPTH = C::IMAX < 2 ? C::IMAX : 2;
+  if constexpr (WAVEX) wx_load<K, M>(p, it0, it1, lane, xr, 0, LAZYX ? XDEPTH : C::IMAX);
   else pro_load<K, M, MODE, WAVEX ? 1 : C::RR>(p, 0, raw);
   __builtin_amdgcn_sched_barrier(0);
   const TileRef tr = tile_ref<K>(p, tile_ok ? tile : tiles - 1, rp);
@@ -754,6 +759,7 @@ DEV void qmv_body(const LisaQmvParams& p, unsigned char* lds) {
     }
     if (i + DEPTH < C::IMAX) {
       __builtin_amdgcn_sched_barrier(0);
+      if constexpr (LAZYX) wx_load<K, M>(p, it0, it1, lane, xr, i + DEPTH, i + DEPTH + 1);
       load_unit<K, C::IMAX>(u, tr, it0, it1, li, i + DEPTH, i + DEPTH + 1);
       __builtin_amdgcn_sched_barrier(0);
     }
@@ -1045,10 +1051,11 @@ DEV void gdn_l2_prefetch(const LisaGdnParams& p) {
   for (int n = 0; n < MAXT; ++n) {
     const uint32_t t = x + 8 * (k + n * per);
     const bool ok = t < p.pf_tiles;
+    const uint32_t ts = ok ? t : 0;  // tiles past the matrix address tile 0 (and load nothing)
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const uint32_t i = min(threadIdx.x + 512u * r, wq + sq - 1);
-      const uint4* src = i < wq ? w + (size_t)t * wq + i : sb + (size_t)t * sq + (i - wq);
+      const uint4* src = i < wq ? w + (size_t)ts * wq + i : sb + (size_t)ts * sq + (i - wq);
       v[n][r] = ok ? *reinterpret_cast<const lisa_u32x4*>(src) : lisa_u32x4{0, 0, 0, 0};
     }
   }

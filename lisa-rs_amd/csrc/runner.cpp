@@ -1213,22 +1213,21 @@ extern "C" int lisa_runner_decode_greedy(LisaRunner* r, uint32_t token, int32_t 
   return LISA_OK;
 }
 
-extern "C" int lisa_runner_profile_step(LisaRunner* r, uint32_t token, int32_t steps, float* kind_ms,
-                                        int32_t* kind_count) {
-  if (!r || steps <= 0 || !kind_ms || !kind_count) return lisa_fail(LISA_E_ARG, "lisa_runner_profile_step: bad argument");
-  LISA_TRY(check_token(r, token));
-  if (r->position + (uint32_t)steps > (uint32_t)r->cfg.capacity)
-    return lisa_fail(LISA_E_CAPACITY, "KV capacity %d exhausted by %d steps", r->cfg.capacity, steps);
+namespace {
+
+// Timed eager passes (every launch between start/stop events attached to its
+// dispatch), summed per launch kind.
+int profile_pass(LisaRunner* r, int m, int32_t steps, float* kind_ms, int32_t* kind_count) {
   for (int k = 0; k < LISA_KIND_COUNT; ++k) {
     kind_ms[k] = 0.0f;
     kind_count[k] = 0;
   }
-  Ctx& c = r->tgt;
-  LISA_TRY(upload_u32(r, c.tokens, &token, 1));
   r->prof.clear();
   r->dev->prof = &r->prof;
   int rc = LISA_OK;
-  for (int s = 0; s < steps && !rc; ++s) rc = encode_target(r, 1, false, true, att_slices(r, r->position + s, false));
+  for (int s = 0; s < steps && !rc; ++s)
+    rc = m == 1 ? encode_target(r, 1, false, true, att_slices(r, r->position + s, false))
+                : encode_target(r, 3, true, false, att_slices(r, r->position + 2, false));
   r->dev->prof = nullptr;
   r->dev->prof_kind = -1;
   if (!rc) rc = sync(r);
@@ -1244,8 +1243,34 @@ extern "C" int lisa_runner_profile_step(LisaRunner* r, uint32_t token, int32_t s
     (void)hipEventDestroy(rec.stop);
   }
   r->prof.clear();
-  if (rc) return rc;
+  return rc;
+}
+
+}  // namespace
+
+extern "C" int lisa_runner_profile_step(LisaRunner* r, uint32_t token, int32_t steps, float* kind_ms,
+                                        int32_t* kind_count) {
+  if (!r || steps <= 0 || !kind_ms || !kind_count) return lisa_fail(LISA_E_ARG, "lisa_runner_profile_step: bad argument");
+  LISA_TRY(check_token(r, token));
+  if (r->position + (uint32_t)steps > (uint32_t)r->cfg.capacity)
+    return lisa_fail(LISA_E_CAPACITY, "KV capacity %d exhausted by %d steps", r->cfg.capacity, steps);
+  LISA_TRY(upload_u32(r, r->tgt.tokens, &token, 1));
+  LISA_TRY(profile_pass(r, 1, steps, kind_ms, kind_count));
   r->position += (uint32_t)steps;
+  r->verify_base = -1;
+  return LISA_OK;
+}
+
+extern "C" int lisa_runner_profile_block3(LisaRunner* r, const uint32_t tokens[3], float* kind_ms,
+                                          int32_t* kind_count) {
+  if (!r || !tokens || !kind_ms || !kind_count) return lisa_fail(LISA_E_ARG, "lisa_runner_profile_block3: bad argument");
+  for (int i = 0; i < 3; ++i) LISA_TRY(check_token(r, tokens[i]));
+  if (r->position + 3 > (uint32_t)r->cfg.capacity)
+    return lisa_fail(LISA_E_CAPACITY, "KV capacity %d exhausted", r->cfg.capacity);
+  LISA_TRY(upload_u32(r, r->tgt.tokens, tokens, 3));
+  LISA_TRY(profile_pass(r, 3, 1, kind_ms, kind_count));
+  r->verify_base = r->position;
+  r->position += 3;
   return LISA_OK;
 }
 
