@@ -325,6 +325,28 @@ def gemm_phase(pkg, reps=10):
             out.append(row)
             print(f"[bench] gemm {what} {m}x{n}x{k} {kern}: {us:.1f} us, {tflops:.1f} TFLOP/s", file=sys.stderr,
                   flush=True)
+        if what.startswith("mlp gate"):
+            # the gate/up pair as the prefill runs it: one launch, SwiGLU epilogue
+            actb = dev.buffer(m * n * 2)
+            pf = pkg.GemmParams(a=ab.ptr, w=wb.ptr, sb=sbb.ptr, m=m, n=n, k=k, ldc=n, w2=wb.ptr, sb2=sbb.ptr,
+                                act=actb.ptr)
+            grid = ((n + 127) // 128, (m + pkg.GEMM_TILE_M - 1) // pkg.GEMM_TILE_M)
+            dev.dispatch("lisa_q4_gemm_swiglu", pf, grid, (pkg.GEMM_THREADS_WIDE,))
+            pkg._check(L.lisa_event_record(ev0, dev.h))
+            for _ in range(reps):
+                dev.dispatch("lisa_q4_gemm_swiglu", pf, grid, (pkg.GEMM_THREADS_WIDE,), wait=False)
+            pkg._check(L.lisa_event_record(ev1, dev.h))
+            dev.synchronize()
+            ms = pkg.C.c_float()
+            pkg._check(L.lisa_event_elapsed_ms(ev0, ev1, pkg.C.byref(ms)))
+            us = 1e3 * ms.value / reps
+            tflops = 2.0 * m * (2 * n) * k / (us * 1e-6) / 1e12
+            out.append({"m": m, "n": 2 * n, "k": k, "what": "mlp gate+up pair (SwiGLU epilogue)",
+                        "kernel": "lisa_q4_gemm_swiglu", "us": round(us, 1), "tflops": round(tflops, 1),
+                        "mfma_frac": round(tflops / BF16_PEAK_TFLOPS, 4)})
+            print(f"[bench] gemm gate+up {m}x{2 * n}x{k} lisa_q4_gemm_swiglu: {us:.1f} us, {tflops:.1f} TFLOP/s",
+                  file=sys.stderr, flush=True)
+            del actb
         del wb, sbb, ab, cb
     return {"shapes": out, "peak_tflops": BF16_PEAK_TFLOPS, "dtype": "bf16 MFMA, f32 accumulate",
             "note": "dequantized q4 weights; peak = dense bf16 MFMA of MI355X"}

@@ -226,6 +226,13 @@ typedef struct LisaGemmParams {
   const uint32_t* sb;
   float* c;
   uint32_t m, n, k, ldc;
+  /* lisa_q4_gemm_swiglu (the MLP's gate/up pair, gemm.metal:273-341): w, sb
+   * are the gate projection, w2, sb2 the up projection (both n x k), and
+   * act[m][n] (row stride ldc) receives bf16(silu(bf16 g) * bf16 u); c is
+   * unused. Grid (ceil(n / 128), ceil(m / 256)) x LISA_GEMM_THREADS_WIDE. */
+  const uint32_t* w2;
+  const uint32_t* sb2;
+  uint16_t* act;
 } LisaGemmParams;
 
 /* lisa_rows: per-row kernels of the prefill, grid (x, m) x 256. */

@@ -95,7 +95,8 @@ class AttnParams(C.Structure):
 
 class GemmParams(C.Structure):
     _fields_ = [("a", C.c_uint64), ("w", C.c_uint64), ("sb", C.c_uint64), ("c", C.c_uint64),
-                ("m", C.c_uint32), ("n", C.c_uint32), ("k", C.c_uint32), ("ldc", C.c_uint32)]
+                ("m", C.c_uint32), ("n", C.c_uint32), ("k", C.c_uint32), ("ldc", C.c_uint32),
+                ("w2", C.c_uint64), ("sb2", C.c_uint64), ("act", C.c_uint64)]
 
 
 ROWS_EMBED, ROWS_NORM, ROWS_RESNORM, ROWS_SILU, ROWS_ARGMAX = range(5)

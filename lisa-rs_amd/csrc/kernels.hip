@@ -1755,12 +1755,18 @@ DEV void gemm_step(const uint16_t* as_r, const uint16_t* ws_r, uint16_t* as_w, u
   }
 }
 
-template <int BN, int NT>
+// SWIGLU: the tile's W rows are the gate and up rows of BN / 2 output
+// columns, laid out so that MFMA block j of wave wn holds matrix j (0 gate,
+// 1 up) of columns n0 + wn * 32 + (0..31); the epilogue then finds the gate
+// and up sums of an output in the same lane and writes bf16(silu(bf16 g) *
+// bf16 u) (mlp.metal:11-16) instead of the two f32 outputs.
+template <int BN, int NT, bool SWIGLU = false>
 DEV void q4_gemm_body(const LisaGemmParams& p, uint16_t (*As)[GEMM_BM * GEMM_PAD], uint16_t (*Ws)[BN * GEMM_PAD]) {
   using G = GemmCfg<BN, NT>;
+  static_assert(!SWIGLU || G::NB == 2, "the gate/up tile pairs two 32-wide blocks per wave");
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave / G::WN, wn = wave % G::WN;
-  const uint32_t m0 = blockIdx.y * GEMM_BM, n0 = blockIdx.x * BN;
+  const uint32_t m0 = blockIdx.y * GEMM_BM, n0 = blockIdx.x * (SWIGLU ? BN / 2 : BN);
   const uint32_t K = p.k, nk = K / 64;
 
   const lisa_u32x4* asrc[G::RA];
@@ -1770,9 +1776,16 @@ DEV void q4_gemm_body(const LisaGemmParams& p, uint16_t (*As)[GEMM_BM * GEMM_PAD
     const uint32_t row = min(m0 + (uint32_t)(u >> 3), p.m - 1);
     asrc[i] = reinterpret_cast<const lisa_u32x4*>(p.a + (size_t)row * K) + (u & 7);
   }
-  const uint32_t wrow = min(n0 + (uint32_t)((G::RW * tid) >> 1), p.n - 1);
-  const lisa_u32x4* wsrc = reinterpret_cast<const lisa_u32x4*>(p.w + (size_t)wrow * (K / 8)) + ((G::RW * tid) & 1);
-  const uint32_t* sbsrc = p.sb + (size_t)wrow * (K / 64);
+  // the W row this thread stages: LDS row l = (RW tid) / 2 (RW = 1 on the
+  // SWIGLU tile), of matrix (l / 32) % 2 and column n0 + (l / 64) 32 + l % 32
+  // there
+  const uint32_t lrow = (uint32_t)((G::RW * tid) >> 1);
+  const bool upm = SWIGLU && ((lrow >> 5) & 1);
+  const uint32_t wrow = min(SWIGLU ? n0 + (lrow >> 6) * 32 + (lrow & 31) : n0 + lrow, p.n - 1);
+  const uint32_t* wmat = upm ? p.w2 : p.w;
+  const uint32_t* sbmat = upm ? p.sb2 : p.sb;
+  const lisa_u32x4* wsrc = reinterpret_cast<const lisa_u32x4*>(wmat + (size_t)wrow * (K / 8)) + ((G::RW * tid) & 1);
+  const uint32_t* sbsrc = sbmat + (size_t)wrow * (K / 64);
 
   lisa_f32x16 acc[4][G::NB];
 #pragma unroll
@@ -1809,17 +1822,31 @@ DEV void q4_gemm_body(const LisaGemmParams& p, uint16_t (*As)[GEMM_BM * GEMM_PAD
     __syncthreads();
   }
 #undef GEMM_GLOAD
+  if constexpr (SWIGLU) {
+    const uint32_t col = n0 + wn * 32 + (lane & 31);
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
-#pragma unroll
-    for (int j = 0; j < G::NB; ++j) {
-      const uint32_t col = n0 + wn * (BN / G::WN) + j * 32 + (lane & 31);
+    for (int i = 0; i < 4; ++i)
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const uint32_t row = m0 + wm * 128 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-        if (row < p.m && col < p.n) p.c[(size_t)row * p.ldc + col] = acc[i][j][r];
+        if (row < p.m && col < p.n) {
+          const float a = lisa_bf16r(lisa_silu_exp2(lisa_bf16r(acc[i][0][r])) * lisa_bf16r(acc[i][1][r]));
+          p.act[(size_t)row * p.ldc + col] = lisa_f32_to_bf16(a);
+        }
       }
-    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < G::NB; ++j) {
+        const uint32_t col = n0 + wn * (BN / G::WN) + j * 32 + (lane & 31);
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const uint32_t row = m0 + wm * 128 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+          if (row < p.m && col < p.n) p.c[(size_t)row * p.ldc + col] = acc[i][j][r];
+        }
+      }
+  }
 }
 
 // lisa_q4_gemm: one 4-wave workgroup per CU (the LDS stages take 108 KB), so the
@@ -1837,6 +1864,14 @@ extern "C" __global__ __launch_bounds__(LISA_GEMM_THREADS_WIDE) __attribute__((a
   __shared__ __attribute__((aligned(16))) uint16_t As[2][GEMM_BM * GEMM_PAD];
   __shared__ __attribute__((aligned(16))) uint16_t Ws[2][LISA_GEMM_TILE_N_WIDE * GEMM_PAD];
   q4_gemm_body<LISA_GEMM_TILE_N_WIDE, LISA_GEMM_THREADS_WIDE>(p, As, Ws);
+}
+// The MLP's gate/up pair with the SwiGLU epilogue: 256 rows x 128 outputs per
+// workgroup (the eight-wave tile over 128 gate and 128 up rows).
+extern "C" __global__ __launch_bounds__(LISA_GEMM_THREADS_WIDE) __attribute__((amdgpu_waves_per_eu(2, 2))) void lisa_q4_gemm_swiglu(
+    LisaGemmParams p) {
+  __shared__ __attribute__((aligned(16))) uint16_t As[2][GEMM_BM * GEMM_PAD];
+  __shared__ __attribute__((aligned(16))) uint16_t Ws[2][LISA_GEMM_TILE_N_WIDE * GEMM_PAD];
+  q4_gemm_body<LISA_GEMM_TILE_N_WIDE, LISA_GEMM_THREADS_WIDE, true>(p, As, Ws);
 }
 
 // Per-row kernels. NORM/RESNORM follow the q4 prologue's arithmetic exactly

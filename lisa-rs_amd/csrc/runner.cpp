@@ -122,7 +122,7 @@ struct LisaRunner {
   LisaFunction *qmv_epi[2][7][5] = {};  // K = 5120 with a fixed epilogue: [m3][prologue][epilogue]
   LisaFunction *gdn[2] = {}, *attn_part[2] = {}, *attn_merge[2] = {}, *finalize = nullptr, *synth = nullptr;
   // batched prefill
-  LisaFunction *gemm = nullptr, *gemm_wide = nullptr, *rows = nullptr, *conv_rows = nullptr, *gdn_prep_rows = nullptr, *gdn_scan_rows = nullptr,
+  LisaFunction *gemm = nullptr, *gemm_wide = nullptr, *gemm_swiglu = nullptr, *rows = nullptr, *conv_rows = nullptr, *gdn_prep_rows = nullptr, *gdn_scan_rows = nullptr,
                *gdn_out_rows = nullptr, *attn_store_rows = nullptr,
                *attn_partial_rows = nullptr, *attn_merge_rows = nullptr;
   // memory
@@ -150,7 +150,7 @@ struct LisaRunner {
     uint32_t *tokens = nullptr, *argmax = nullptr, *pos = nullptr;
     uint16_t *H = nullptr, *X = nullptr, *gated = nullptr, *act = nullptr, *query = nullptr;
     float *B = nullptr, *qkv = nullptr, *conv_out = nullptr, *z = nullptr, *a = nullptr, *b = nullptr;
-    float *q_proj = nullptr, *k_raw = nullptr, *v_raw = nullptr, *G = nullptr, *U = nullptr, *logits = nullptr;
+    float *q_proj = nullptr, *k_raw = nullptr, *v_raw = nullptr, *logits = nullptr;
     float *part_o = nullptr, *part_ml = nullptr;
     float *gdn_qk = nullptr, *gdn_gates = nullptr, *gdn_y = nullptr;
   } pf;
@@ -930,6 +930,7 @@ int runner_init(const LisaRunnerConfig* cfg, std::unique_ptr<LisaRunner>& out) {
   LISA_TRY(lisa_function_get(r->mod, "lisa_synth_fill", &r->synth));
   LISA_TRY(lisa_function_get(r->mod, "lisa_q4_gemm", &r->gemm));
   LISA_TRY(lisa_function_get(r->mod, "lisa_q4_gemm_wide", &r->gemm_wide));
+  LISA_TRY(lisa_function_get(r->mod, "lisa_q4_gemm_swiglu", &r->gemm_swiglu));
   LISA_TRY(lisa_function_get(r->mod, "lisa_rows", &r->rows));
   LISA_TRY(lisa_function_get(r->mod, "lisa_gdn_conv_rows", &r->conv_rows));
   LISA_TRY(lisa_function_get(r->mod, "lisa_gdn_prep_rows", &r->gdn_prep_rows));
@@ -1103,7 +1104,7 @@ extern "C" void lisa_runner_free(LisaRunner* r) {
     for (auto& b : a)
       for (LisaFunction* f : b) delete f;
   for (LisaFunction* f : {r->gdn[0], r->gdn[1], r->attn_part[0], r->attn_part[1], r->attn_merge[0], r->attn_merge[1],
-                          r->finalize, r->synth, r->gemm, r->gemm_wide, r->rows, r->conv_rows, r->gdn_prep_rows, r->gdn_scan_rows, r->gdn_out_rows, r->attn_store_rows,
+                          r->finalize, r->synth, r->gemm, r->gemm_wide, r->gemm_swiglu, r->rows, r->conv_rows, r->gdn_prep_rows, r->gdn_scan_rows, r->gdn_out_rows, r->attn_store_rows,
                           r->attn_partial_rows, r->attn_merge_rows})
     delete f;
   lisa_buffer_free(r->pf.buf);
@@ -1575,8 +1576,6 @@ void plan_prefill(LisaRunner* r, Arena& A) {
   P.k_raw = A.take<float>(c * LISA_ATT_KV_OUT);
   P.v_raw = A.take<float>(c * LISA_ATT_KV_OUT);
   P.query = A.take<uint16_t>(c * LISA_ATT_OUT);
-  P.G = A.take<float>(c * LISA_INTER);
-  P.U = A.take<float>(c * LISA_INTER);
   P.act = A.take<uint16_t>(c * LISA_INTER);
   P.logits = A.take<float>(c * (size_t)r->cfg.vocab);
   P.gdn_qk = A.take<float>(c * 2 * LISA_GDN_KEY_DIM);
@@ -1625,6 +1624,27 @@ int launch_gemm(LisaRunner* r, const uint16_t* a, uint32_t m, const Q4Dev& w, fl
   const uint32_t rn = (gn * gm + cus - 1) / cus, rw = (gw * gm + cus - 1) / cus;
   if (rw * 3 <= rn * 2) return lisa_launch(r->dev, r->gemm_wide, &g, sizeof g, gw, gm, 1, LISA_GEMM_THREADS_WIDE, 1, 1);
   return lisa_launch(r->dev, r->gemm, &g, sizeof g, gn, gm, 1, 256, 1, 1);
+}
+
+// act[m][gate.n] = bf16(silu(bf16(A . deq(gate)^T)) * bf16(A . deq(up)^T)) in
+// one launch (the MLP's gate/up pair with the SwiGLU epilogue).
+int launch_gemm_swiglu(LisaRunner* r, const uint16_t* a, uint32_t m, const Q4Dev& gate, const Q4Dev& up,
+                       uint16_t* act) {
+  if (gate.n != up.n || gate.k != up.k) return lisa_fail(LISA_E_ARG, "gate and up projections differ in shape");
+  LisaGemmParams g{};
+  g.a = a;
+  g.w = gate.w;
+  g.sb = gate.sb;
+  g.w2 = up.w;
+  g.sb2 = up.sb;
+  g.act = act;
+  g.m = m;
+  g.n = gate.n;
+  g.k = gate.k;
+  g.ldc = gate.n;
+  const uint32_t gm = (m + LISA_GEMM_TILE_M - 1) / LISA_GEMM_TILE_M;
+  const uint32_t gn = (gate.n + LISA_GEMM_TILE_N_WIDE / 2 - 1) / (LISA_GEMM_TILE_N_WIDE / 2);
+  return lisa_launch(r->dev, r->gemm_swiglu, &g, sizeof g, gn, gm, 1, LISA_GEMM_THREADS_WIDE, 1, 1);
 }
 
 int launch_rows(LisaRunner* r, LisaRowsParams& p, uint32_t gx, uint32_t m) {
@@ -1730,15 +1750,7 @@ int mtp_prefill_chunk(LisaRunner* r, uint32_t m) {
   LISA_TRY(prefill_attention(r, m, r->mtp_position, t.q_norm, t.k_norm, r->mtp_key, r->mtp_value));
   LISA_TRY(launch_gemm(r, P.gated, m, t.o, P.B));
   LISA_TRY(rows_norm(r, m, P.H, P.B, t.post_norm, P.H, P.X));
-  LISA_TRY(launch_gemm(r, P.X, m, t.gate, P.G));
-  LISA_TRY(launch_gemm(r, P.X, m, t.up, P.U));
-  LisaRowsParams sw{};
-  sw.mode = LISA_ROWS_SILU;
-  sw.g_in = P.G;
-  sw.u_in = P.U;
-  sw.act_out = P.act;
-  sw.width = LISA_INTER;
-  LISA_TRY(launch_rows(r, sw, (LISA_INTER + 2047) / 2048, m));
+  LISA_TRY(launch_gemm_swiglu(r, P.X, m, t.gate, t.up, P.act));
   LISA_TRY(launch_gemm(r, P.act, m, t.down, P.B));
   LISA_TRY(rows_norm(r, m, P.H, P.B, t.final_norm, P.H, P.X));
   LISA_TRY(launch_gemm(r, P.X, m, r->head, P.logits));
@@ -1809,15 +1821,7 @@ int prefill_chunk(LisaRunner* r, uint32_t m) {
       LISA_TRY(launch_gemm(r, P.gated, m, l.o, P.B));
     }
     LISA_TRY(rows_norm(r, m, P.H, P.B, l.post_norm, P.H, P.X));
-    LISA_TRY(launch_gemm(r, P.X, m, l.gate, P.G));
-    LISA_TRY(launch_gemm(r, P.X, m, l.up, P.U));
-    LisaRowsParams sw{};
-    sw.mode = LISA_ROWS_SILU;
-    sw.g_in = P.G;
-    sw.u_in = P.U;
-    sw.act_out = P.act;
-    sw.width = LISA_INTER;
-    LISA_TRY(launch_rows(r, sw, (LISA_INTER + 2047) / 2048, m));
+    LISA_TRY(launch_gemm_swiglu(r, P.X, m, l.gate, l.up, P.act));
     LISA_TRY(launch_gemm(r, P.act, m, l.down, P.B));
   }
   LISA_TRY(rows_norm(r, m, P.H, P.B, r->final_norm, P.H, P.X));

@@ -73,6 +73,26 @@ def test_gemm_exact_integer_case(pkg, orc, dev, kernel, K):
     assert np.array_equal(got, orc.q4_gemm(a, w, s, b, N, K, M))
 
 
+@pytest.mark.parametrize("M,N,K", [(300, 600, 1024), (37, 256, 5120), (260, 130, 192)])
+def test_gemm_swiglu_equals_separate_gemms(pkg, orc, dev, M, N, K):
+    """lisa_q4_gemm_swiglu (the MLP's gate/up pair with the SwiGLU epilogue,
+    gemm.metal:273-341) equals the eight-wave GEMM of gate and of up followed
+    by bf16(silu(bf16 g) * bf16 u) (mlp.metal:11-16), bit for bit: the same
+    MFMA sums, one launch, no f32 intermediates. Output columns past a
+    128-wide tile and an odd number of K steps included."""
+    rng = np.random.default_rng(M + N + K)
+    gq, uq = DevQ4(dev, *rand_q4(rng, N, K)), DevQ4(dev, *rand_q4(rng, N, K))
+    a = bf16(rng.standard_normal((M, K)).astype(np.float32))
+    g = gemm(pkg, dev, a, gq, M, "lisa_q4_gemm_wide")
+    u = gemm(pkg, dev, a, uq, M, "lisa_q4_gemm_wide")
+    ab, act = dev.upload(a), dev.buffer(M * N * 2)
+    p = pkg.GemmParams(a=ab.ptr, w=gq.wbuf.ptr, sb=gq.sbbuf.ptr, m=M, n=N, k=K, ldc=N, w2=uq.wbuf.ptr,
+                       sb2=uq.sbbuf.ptr, act=act.ptr)
+    dev.dispatch("lisa_q4_gemm_swiglu", p, ((N + 127) // 128, (M + pkg.GEMM_TILE_M - 1) // pkg.GEMM_TILE_M),
+                 (pkg.GEMM_THREADS_WIDE,))
+    assert np.array_equal(act.read(np.uint16, M * N).reshape(M, N), orc.silu_mul(g, u).reshape(M, N))
+
+
 def rows(pkg, dev, p, gx, m):
     dev.dispatch("lisa_rows", p, (gx, m), (256,))
 
