@@ -61,8 +61,8 @@ int lisa_attention_launch(LisaDevice* dev, LisaModule* mod, const LisaAttnDecode
   p.capacity = a->capacity;
   p.s_max = slices;
   void* args[1] = {&p};
-  LISA_TRY(lisa_hip_check(hipModuleLaunchKernel(part_fn, slices, LISA_ATT_KVH, 1, 256, 1, 1, 0, dev->stream, args,
-                                                nullptr), "launch lisa_attn_partial"));
+  LISA_TRY(lisa_hip_check(hipModuleLaunchKernel(part_fn, slices, LISA_ATT_KVH, 1, LISA_ATT_PARTIAL_THREADS(a->m_rows),
+                                                1, 1, 0, dev->stream, args, nullptr), "launch lisa_attn_partial"));
   return lisa_hip_check(hipModuleLaunchKernel(merge_fn, LISA_ATT_QH, a->m_rows, 1, 256, 1, 1, 0, dev->stream, args,
                                               nullptr), "launch lisa_attn_merge");
 }

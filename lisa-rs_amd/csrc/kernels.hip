@@ -1459,10 +1459,12 @@ DEV void slice_pv3(const float* pb3, const uint16_t* Vt, int n, int dp, float (&
 // and rotated, and the appended rows written, while the slice is in flight.
 // Scores: one wave per pair of heads; P.V: thread (dp, hg) = (tid % 128,
 // tid / 128) owns dimensions 2dp, 2dp+1 of heads 3hg..3hg+2.
+// NT threads: 256 for one row, 512 for three (the three rows' score items
+// and P.V groups then take two passes, not three).
 typedef uint32_t lisa_u32x4 __attribute__((ext_vector_type(4)));
-template <int M>
+template <int M, int NT = 256>
 DEV void attn_partial_body(const LisaAttnParams& p) {
-  constexpr int T = LISA_ATT_SLICE, HD = LISA_ATT_HD, KP = HD + 8;
+  constexpr int T = LISA_ATT_SLICE, HD = LISA_ATT_HD, KP = HD + 8, NW = NT / 64;
   const int s = blockIdx.x, kvh = blockIdx.y;
   const uint32_t t0 = (uint32_t)s * T;
   __shared__ __attribute__((aligned(16))) uint16_t Kt[T * KP];
@@ -1473,14 +1475,14 @@ DEV void attn_partial_body(const LisaAttnParams& p) {
   const size_t cache_base = (size_t)kvh * p.capacity * HD;
   const uint32_t pos_v = vload_u32(p.pos);
 
-  // 0. the raw query heads of this wave (pairs pr = wave + 4j of row t = pr / 6,
+  // 0. the raw query heads of this wave (pairs pr = wave + NW j of row t = pr / 6,
   // head i = pr % 6), the RoPE frequency, and wave t < M: row t's raw key, its
   // norm weights and raw value
-  constexpr int QP = (6 * M + 3) / 4;
+  constexpr int QP = (6 * M + NW - 1) / NW;
   float qraw[QP][4], qw[QP][4];
 #pragma unroll
   for (int j = 0; j < QP; ++j) {
-    const int pr = min(wave + 4 * j, 6 * M - 1), t = pr / 6, i = pr % 6;
+    const int pr = min(wave + NW * j, 6 * M - 1), t = pr / 6, i = pr % 6;
     hnr_load(p.q_proj + (size_t)t * LISA_ATT_Q_OUT + (kvh * 6 + i) * 512, p.q_norm_w, lane, qraw[j], qw[j]);
   }
   float inv_freq = 0.0f;
@@ -1492,15 +1494,15 @@ DEV void attn_partial_body(const LisaAttnParams& p) {
 #pragma unroll
   for (int j = 0; j < 4; ++j) nvraw[j] = p.v_raw[(size_t)wr * LISA_ATT_KV_OUT + kvh * HD + lane + 64 * j];
   __builtin_amdgcn_sched_barrier(0);
-  // 1. every row of the slice (chunk c = tid + 256 i: row c / 32, columns
+  // 1. every row of the slice (chunk c = tid + NT i: row c / 32, columns
   // 8 (c % 32) ..), clamped below the capacity (native vector types: HIP's
   // uint4 struct copies lower to memcpy, which keeps an array of them out of
   // registers)
-  constexpr int R = T * (HD / 8) / 256;
+  constexpr int R = T * (HD / 8) / NT;
   lisa_u32x4 kr[R], vr[R];
 #pragma unroll
   for (int i = 0; i < R; ++i) {
-    const int c = tid + 256 * i, row = c / (HD / 8), col = (c % (HD / 8)) * 8;
+    const int c = tid + NT * i, row = c / (HD / 8), col = (c % (HD / 8)) * 8;
     const size_t off = cache_base + (size_t)min(t0 + row, p.capacity - 1) * HD + col;
     kr[i] = *reinterpret_cast<const lisa_u32x4*>(p.key_cache + off);
     vr[i] = *reinterpret_cast<const lisa_u32x4*>(p.value_cache + off);
@@ -1515,7 +1517,7 @@ DEV void attn_partial_body(const LisaAttnParams& p) {
   for (int t = 0; t < M; ++t) rope_sincos_f(base + t, inv_freq, rs[t], rc[t]);
 #pragma unroll
   for (int j = 0; j < QP; ++j) {
-    const int pr = wave + 4 * j;
+    const int pr = wave + NW * j;
     if (pr >= 6 * M) break;
     const int t = pr / 6, i = pr % 6;
     float qo[4];
@@ -1547,7 +1549,7 @@ DEV void attn_partial_body(const LisaAttnParams& p) {
   // past every row's context
 #pragma unroll
   for (int i = 0; i < R; ++i) {
-    const int c = tid + 256 * i, row = c / (HD / 8), col = (c % (HD / 8)) * 8;
+    const int c = tid + NT * i, row = c / (HD / 8), col = (c % (HD / 8)) * 8;
     if (t0 + row < base) {
       *reinterpret_cast<lisa_u32x4*>(&Kt[row * KP + col]) = kr[i];
       *reinterpret_cast<lisa_u32x4*>(&Vt[row * HD + col]) = vr[i];
@@ -1556,7 +1558,7 @@ DEV void attn_partial_body(const LisaAttnParams& p) {
   __syncthreads();
   // 5. scores and slice softmax statistics: item (row t, head pair k) per wave,
   // lane = token of the slice
-  for (int it = wave; it < 3 * M; it += 4) {
+  for (int it = wave; it < 3 * M; it += NW) {
     const int t = it / 3, i = 2 * (it % 3), h = kvh * 6 + i;
     const uint32_t ctx = base + t + 1;
     if (ctx <= t0) continue;
@@ -1567,9 +1569,11 @@ DEV void attn_partial_body(const LisaAttnParams& p) {
                   ml + (size_t)p.s_max * 2);
   }
   __syncthreads();
-  // 6. P.V
-  const int dp = tid & 127, hg = tid >> 7;
-  for (int t = 0; t < M; ++t) {
+  // 6. P.V: thread group g = tid / 128 takes the (row, head group) items
+  // g, g + NT / 128, .. of the 2 M items (row t = item / 2, heads 3 (item % 2) ..)
+  const int dp = tid & 127;
+  for (int item = tid >> 7; item < 2 * M; item += NT / 128) {
+    const int t = item >> 1, hg = item & 1;
     const uint32_t ctx = base + t + 1;
     if (ctx <= t0) continue;
     const int n = (int)min((uint32_t)T, ctx - t0);
@@ -1632,8 +1636,12 @@ DEV void attn_merge_body(const LisaAttnParams& p) {
   p.gated[(size_t)t * LISA_ATT_OUT + h * LISA_ATT_HD + tid] = lisa_f32_to_bf16(o * lisa_sigmoid_exp2(g));
 }
 
-extern "C" __global__ __launch_bounds__(256) void lisa_attn_partial_m1(LisaAttnParams p) { attn_partial_body<1>(p); }
-extern "C" __global__ __launch_bounds__(256) void lisa_attn_partial_m3(LisaAttnParams p) { attn_partial_body<3>(p); }
+extern "C" __global__ __launch_bounds__(LISA_ATT_PARTIAL_THREADS(1)) void lisa_attn_partial_m1(LisaAttnParams p) {
+  attn_partial_body<1, LISA_ATT_PARTIAL_THREADS(1)>(p);
+}
+extern "C" __global__ __launch_bounds__(LISA_ATT_PARTIAL_THREADS(3)) void lisa_attn_partial_m3(LisaAttnParams p) {
+  attn_partial_body<3, LISA_ATT_PARTIAL_THREADS(3)>(p);
+}
 extern "C" __global__ __launch_bounds__(256) void lisa_attn_merge_m1(LisaAttnParams p) { attn_merge_body<1>(p); }
 extern "C" __global__ __launch_bounds__(256) void lisa_attn_merge_m3(LisaAttnParams p) { attn_merge_body<3>(p); }
 

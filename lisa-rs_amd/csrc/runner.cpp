@@ -645,7 +645,8 @@ int launch_attention(LisaRunner* r, Ctx& c, int m, uint32_t slices, const uint16
   const int mi = m == 3 ? 1 : 0;
   LISA_TRY(prof_mark(r, LISA_KIND_ATTN_PARTIAL));
   if (slices == 0 || slices > r->s_max) return lisa_fail(LISA_E_ARG, "attention grid of %u slices", slices);
-  LISA_TRY(lisa_launch(r->dev, r->attn_part[mi], &a, sizeof a, slices, LISA_ATT_KVH, 1, 256, 1, 1));
+  LISA_TRY(lisa_launch(r->dev, r->attn_part[mi], &a, sizeof a, slices, LISA_ATT_KVH, 1, LISA_ATT_PARTIAL_THREADS(m),
+                       1, 1));
   LISA_TRY(prof_mark(r, LISA_KIND_ATTN_MERGE));
   return lisa_launch(r->dev, r->attn_merge[mi], &a, sizeof a, LISA_ATT_QH, m, 1, 256, 1, 1);
 }
