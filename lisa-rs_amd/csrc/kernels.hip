@@ -436,6 +436,91 @@ DEV void wx_stage(unsigned char* slot, int lane, const uint4 (&xr)[M][2]) {
 // moving them across).
 DEV void wave_lds_fence() { __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront"); }
 
+// PRENORM of several input rows: every row's residual chunks and the shared
+// norm gains, loaded in one batch before the weight stream.
+template <int M>
+struct PreRaw {
+  uint4 a[M][3], w[3];
+};
+
+template <int M>
+DEV void prenorm_rows_load(const LisaQmvParams& p, PreRaw<M>& raw) {
+  const int tid = threadIdx.x;
+#pragma unroll
+  for (int i = 0; i < 3; ++i) {
+    const int c = min(tid + 256 * i, kSegChunks - 1);
+    raw.w[i] = reinterpret_cast<const uint4*>(p.norm_w)[c];
+#pragma unroll
+    for (int m = 0; m < M; ++m) raw.a[m][i] = reinterpret_cast<const uint4*>(p.h_in + (size_t)m * LISA_HIDDEN)[c];
+  }
+}
+
+// Normalize and stage M rows (norm.metal:10-47): per row the chunk map, the
+// sums of squares, the reduction order and the staged values of the one-row
+// path (seg_process), with the rows' statistics formed in one round of
+// barriers (lane m of wave 0 forms row m's factor) rather than one per row.
+template <int K, int M>
+DEV void prenorm_rows(const LisaQmvParams& p, unsigned char* lds, const PreRaw<M>& raw) {
+  using C = QmvCfg<K, M>;
+  static_assert(K == LISA_HIDDEN && 5 * M <= C::RBYTES / 4, "PRENORM rows of the wrong width");
+  const int tid = threadIdx.x, wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  float* gsum = reinterpret_cast<float*>(lds + C::XBYTES);
+  float* red = gsum + M * C::G;
+  const bool has2 = wv < 2;  // chunk tid + 512 < 640: waves 0 and 1
+  float ss[M];
+#pragma unroll
+  for (int m = 0; m < M; ++m) {
+    ss[m] = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 3; ++i) {
+      if (i == 2 && !has2) break;
+      const bool valid = tid + 256 * i < kSegChunks;
+      float hv[8];
+      unpack_bf8(raw.a[m][i], hv);
+      const float part = ((hv[0] * hv[0] + hv[1] * hv[1]) + (hv[2] * hv[2] + hv[3] * hv[3])) +
+                         ((hv[4] * hv[4] + hv[5] * hv[5]) + (hv[6] * hv[6] + hv[7] * hv[7]));
+      if (valid) ss[m] = ss[m] + part;
+    }
+    ss[m] = tree64(ss[m]);
+  }
+  __syncthreads();
+  if ((tid & 63) == 0) {
+#pragma unroll
+    for (int m = 0; m < M; ++m) red[4 * m + wv] = ss[m];
+  }
+  __syncthreads();
+  if (tid < M) {
+    const float* rm = red + 4 * tid;
+    red[4 * M + tid] = lisa_rsqrt(((rm[0] + rm[1]) + (rm[2] + rm[3])) / (float)LISA_HIDDEN + LISA_EPS);
+  }
+  __syncthreads();
+  const bool writer = blockIdx.x == 0;
+#pragma unroll
+  for (int m = 0; m < M; ++m) {
+    const float inv = red[4 * M + m];
+#pragma unroll
+    for (int i = 0; i < 3; ++i) {
+      if (i == 2 && !has2) break;
+      const int c = tid + 256 * i;
+      const bool valid = c < kSegChunks;
+      float hv[8], wf[8], f[8], x[8];
+      uint4 xb;
+      unpack_bf8(raw.a[m][i], hv);
+      unpack_bf8(raw.w[i], wf);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) f[e] = (hv[e] * inv) * wf[e];
+      round_bf8(f, x, xb);
+      if (valid) put_chunk<K, M>(lds, m, 8 * c, x);
+      put_gsum<K, M>(gsum, m, 8 * c, valid, x);
+      if (valid && writer) {
+        if (p.r_out) reinterpret_cast<uint4*>(p.r_out + (size_t)m * LISA_HIDDEN)[c] = raw.a[m][i];
+        if (p.x_out) reinterpret_cast<uint4*>(p.x_out + (size_t)m * K)[c] = xb;
+      }
+    }
+  }
+  __syncthreads();
+}
+
 template <int K, int M, int MODE, int R>
 DEV void pro_load(const LisaQmvParams& p, int m, ProRaw<R>& raw) {
   if constexpr (MODE == LISA_PRO_LOADX) x_load<K, M, R>(p, m, raw);
@@ -703,7 +788,10 @@ DEV void qmv_body(const LisaQmvParams& p, unsigned char* lds) {
   const bool tile_ok = tile < tiles;
   const int it0 = C::SPLIT ? (C::ITER * wv) / 4 : 0;
   const int it1 = C::SPLIT ? (C::ITER * (wv + 1)) / 4 : C::ITER;
-  ProRaw<WAVEX ? 1 : C::RR> raw;
+  // several rows under PRENORM: all rows' loads up front, one statistic round
+  constexpr bool PRE_ROWS = MODE == LISA_PRO_PRENORM && M > 1;
+  ProRaw<WAVEX || PRE_ROWS ? 1 : C::RR> raw;
+  PreRaw<PRE_ROWS ? M : 1> pre_rows;
   uint4 xr[WAVEX ? C::IMAX : 1][M][2];
   // issue order: prologue loads, then the weight stream (the fences keep the
   // scheduler from interleaving them, so the prologue waits only for its own).
@@ -722,6 +810,7 @@ DEV void qmv_body(const LisaQmvParams& p, unsigned char* lds) {
   constexpr bool LAZYX = WAVEX && M > 1;
   constexpr int XDEPTH = C::IMAX < 2 ? C::IMAX : 2;
   if constexpr (WAVEX) wx_load<K, M>(p, it0, it1, lane, xr, 0, LAZYX ? XDEPTH : C::IMAX);
+  else if constexpr (PRE_ROWS) prenorm_rows_load<M>(p, pre_rows);
   else pro_load<K, M, MODE, WAVEX ? 1 : C::RR>(p, 0, raw);
   __builtin_amdgcn_sched_barrier(0);
   const TileRef tr = tile_ref<K>(p, tile_ok ? tile : tiles - 1, rp);
@@ -730,7 +819,8 @@ DEV void qmv_body(const LisaQmvParams& p, unsigned char* lds) {
   constexpr int EARLY = MODE == LISA_PRO_LOADX ? DEPTH : 1;
   load_unit<K, C::IMAX>(u, tr, it0, it1, li, 0, EARLY);
   __builtin_amdgcn_sched_barrier(0);
-  if constexpr (!WAVEX) qmv_prologue<K, M, MODE, WAVEX ? 1 : C::RR>(p, lds, raw);
+  if constexpr (PRE_ROWS) prenorm_rows<K, M>(p, lds, pre_rows);
+  else if constexpr (!WAVEX) qmv_prologue<K, M, MODE, WAVEX || PRE_ROWS ? 1 : C::RR>(p, lds, raw);
   __builtin_amdgcn_sched_barrier(0);
   load_unit<K, C::IMAX>(u, tr, it0, it1, li, EARLY, DEPTH);
   // epilogue inputs (residual pair, GDN conv state and taps): read here,

@@ -32,6 +32,7 @@
 #include "lisa_model.h"
 #include "lisa_numerics.h"
 #include "lisa_synth.h"
+#include "spec_round.h"
 
 namespace {
 
@@ -161,6 +162,12 @@ struct LisaRunner {
   // captured M=1 steps keyed by the attention slices they launch (a multiple
   // of kGraphSliceBucket): a replay covers every position whose context fits
   std::map<uint32_t, LisaGraph*> step_graphs;
+  // captured M=3 verifications by slice bucket, and captured drafter steps by
+  // (condition source, slice bucket)
+  std::map<uint32_t, LisaGraph*> verify_graphs;
+  std::map<uint32_t, LisaGraph*> mtp_graphs;
+  // pinned host staging of the speculative loop's rounds (spec_round.h)
+  uint32_t* pinned = nullptr;
   // per-launch timing of eager steps (lisa_runner_profile_step)
   std::vector<LisaProfRec> prof;
 };
@@ -776,7 +783,7 @@ int encode_target(LisaRunner* r, int m, bool capture, bool feedback, uint32_t sl
 }
 
 // MTP drafter step (runner.rs:2711-2765, attention/MLP encoders :3097-3271).
-int encode_mtp(LisaRunner* r, const uint16_t* cond) {
+int encode_mtp(LisaRunner* r, const uint16_t* cond, uint32_t slices) {
   Ctx& c = r->drf;
   const MtpDev& t = r->mtp;
   LisaQmvParams p{};
@@ -797,8 +804,7 @@ int encode_mtp(LisaRunner* r, const uint16_t* cond) {
                       {{&t.q, nullptr, c.q_proj, LISA_EPI_STORE},
                        {&t.k, nullptr, c.k_raw, LISA_EPI_STORE},
                        {&t.v, nullptr, c.v_raw, LISA_EPI_STORE}}));
-  LISA_TRY(launch_attention(r, c, 1, att_slices(r, r->mtp_position, false), t.q_norm, t.k_norm, r->mtp_key,
-                            r->mtp_value));
+  LISA_TRY(launch_attention(r, c, 1, slices, t.q_norm, t.k_norm, r->mtp_key, r->mtp_value));
   LISA_TRY(launch_resid(r, c, 1, LISA_ATT_OUT, c.gated, t.o));
   LISA_TRY(launch_mlp(r, c, 1, t.post_norm, t.gate, t.up, t.down));
   LISA_TRY(launch_lm_head(r, c, 1, t.final_norm, c.xnorm));
@@ -830,17 +836,20 @@ int check_token(const LisaRunner* r, uint32_t token) {
   return LISA_OK;
 }
 
-// The captured M=1 step (device-side token/position feedback) that covers
-// position `pos`: recorded on first use for its slice bucket.
-int step_graph_for(LisaRunner* r, uint32_t pos, LisaGraph** out) {
-  const uint32_t slices = att_slices(r, pos, true);
-  auto it = r->step_graphs.find(slices);
-  if (it != r->step_graphs.end()) {
+// The graph of `cache` under `key`, captured from encode() on first use.
+// Every captured launch reads its token, position and state through device
+// buffers, so a replay serves every call whose attention context fits the
+// slice bucket the graph was captured with.
+template <class Encode>
+int cached_graph(LisaRunner* r, std::map<uint32_t, LisaGraph*>& cache, uint32_t key, Encode encode,
+                 LisaGraph** out) {
+  auto it = cache.find(key);
+  if (it != cache.end()) {
     *out = it->second;
     return LISA_OK;
   }
   LISA_TRY(lisa_capture_begin(r->dev));
-  const int rc = encode_target(r, 1, false, true, slices);
+  const int rc = encode();
   LisaGraph* g = nullptr;
   const int re = lisa_capture_end(r->dev, &g);
   if (rc) {
@@ -848,8 +857,112 @@ int step_graph_for(LisaRunner* r, uint32_t pos, LisaGraph** out) {
     return rc;
   }
   LISA_TRY(re);
-  r->step_graphs[slices] = g;
+  cache[key] = g;
   *out = g;
+  return LISA_OK;
+}
+
+// The captured M=1 step (device-side token/position feedback) that covers
+// position `pos`: recorded on first use for its slice bucket.
+int step_graph_for(LisaRunner* r, uint32_t pos, LisaGraph** out) {
+  const uint32_t slices = att_slices(r, pos, true);
+  return cached_graph(r, r->step_graphs, slices, [&] { return encode_target(r, 1, false, true, slices); }, out);
+}
+
+// The captured M=3 verification whose last row sits at `last_pos`.
+int verify_graph_for(LisaRunner* r, uint32_t last_pos, LisaGraph** out) {
+  const uint32_t slices = att_slices(r, last_pos, true);
+  return cached_graph(r, r->verify_graphs, slices, [&] { return encode_target(r, 3, true, false, slices); }, out);
+}
+
+// The captured drafter step at the drafter's position, conditioned on `cond`
+// (cond_key names it: target rows 0..2, the drafter's normalized output, the
+// uploaded condition).
+int mtp_graph_for(LisaRunner* r, const uint16_t* cond, uint32_t cond_key, LisaGraph** out) {
+  const uint32_t slices = att_slices(r, r->mtp_position, true);
+  return cached_graph(r, r->mtp_graphs, cond_key << 24 | slices, [&] { return encode_mtp(r, cond, slices); }, out);
+}
+
+// The M=3 verification of the tokens in tgt.tokens at the current position
+// (captured or eager); the host position advances by 3.
+int launch_verify(LisaRunner* r) {
+  if (r->position + 3 > (uint32_t)r->cfg.capacity)
+    return lisa_fail(LISA_E_CAPACITY, "KV capacity %d exhausted", r->cfg.capacity);
+  if (r->cfg.use_graph) {
+    LisaGraph* g = nullptr;
+    LISA_TRY(verify_graph_for(r, r->position + 2, &g));
+    LISA_TRY(lisa_graph_launch(g, r->dev));
+  } else {
+    LISA_TRY(encode_target(r, 3, true, false, att_slices(r, r->position + 2, false)));
+  }
+  r->verify_base = r->position;
+  r->position += 3;
+  return LISA_OK;
+}
+
+// commit_verified_prefix's device work (the GDN and conv states of row
+// rows - 1 from their slots) and host position; the caller writes the device
+// position.
+int commit_enqueue(LisaRunner* r, int32_t rows) {
+  if (r->verify_base < 0) return lisa_fail(LISA_E_STATE, "no pending block-3 verification");
+  if (rows < 1 || rows > 3) {
+    r->verify_base = -1;
+    return lisa_fail(LISA_E_ARG, "verified prefix must contain 1 to 3 rows");
+  }
+  const uint32_t base = (uint32_t)r->verify_base;
+  r->verify_base = -1;
+  if (rows < 3) {
+    const size_t gs = (size_t)r->gdn_layers * LISA_GDN_STATE;
+    const size_t cs = (size_t)r->gdn_layers * 3 * LISA_GDN_CONV_DIM;
+    LISA_TRY(lisa_hip_check(hipMemcpyAsync(r->gdn_state, r->gdn_slots + (size_t)(rows - 1) * gs, gs * 4,
+                                           hipMemcpyDeviceToDevice, r->dev->stream),
+                            "D2D gdn slot"));
+    LISA_TRY(lisa_hip_check(hipMemcpyAsync(r->conv_state, r->conv_slots + (size_t)(rows - 1) * cs, cs * 2,
+                                           hipMemcpyDeviceToDevice, r->dev->stream),
+                            "D2D conv slot"));
+  }
+  r->position = base + (uint32_t)rows;
+  return LISA_OK;
+}
+
+// The drafter's conditioning row: target rows 0..2 (source 0), the drafter's
+// own normalized output (1), the uploaded condition (2).
+int mtp_cond(LisaRunner* r, int32_t cond_source, int32_t cond_row, const uint16_t** cond, uint32_t* key) {
+  switch (cond_source) {
+    case 0:
+      if (cond_row < 0 || cond_row > 2) return lisa_fail(LISA_E_ARG, "cond_row must be 0..2");
+      *cond = r->tgt.H + (size_t)cond_row * LISA_HIDDEN;
+      *key = (uint32_t)cond_row;
+      return LISA_OK;
+    case 1: *cond = r->drf.xnorm; *key = 3; return LISA_OK;
+    case 2: *cond = r->drf.cond; *key = 4; return LISA_OK;
+    default: return lisa_fail(LISA_E_ARG, "bad cond_source %d", cond_source);
+  }
+}
+
+int check_mtp_step(LisaRunner* r, int32_t cond_source, int32_t cond_row) {
+  if (!r->cfg.with_mtp) return lisa_fail(LISA_E_STATE, "runner was created without the MTP drafter");
+  if (r->mtp_position >= (uint32_t)r->cfg.capacity)
+    return lisa_fail(LISA_E_CAPACITY, "MTP KV capacity %d exhausted", r->cfg.capacity);
+  const uint16_t* cond = nullptr;
+  uint32_t key = 0;
+  return mtp_cond(r, cond_source, cond_row, &cond, &key);
+}
+
+// One drafter step on the token in drf.tokens (captured or eager); the host
+// position advances by 1.
+int launch_mtp(LisaRunner* r, int32_t cond_source, int32_t cond_row) {
+  const uint16_t* cond = nullptr;
+  uint32_t key = 0;
+  LISA_TRY(mtp_cond(r, cond_source, cond_row, &cond, &key));
+  if (r->cfg.use_graph) {
+    LisaGraph* g = nullptr;
+    LISA_TRY(mtp_graph_for(r, cond, key, &g));
+    LISA_TRY(lisa_graph_launch(g, r->dev));
+  } else {
+    LISA_TRY(encode_mtp(r, cond, att_slices(r, r->mtp_position, false)));
+  }
+  r->mtp_position += 1;
   return LISA_OK;
 }
 
@@ -1097,7 +1210,9 @@ extern "C" int lisa_mtp_load(LisaRunner* r, const char* mtp_snapshot, int32_t ca
 extern "C" void lisa_runner_free(LisaRunner* r) {
   if (!r) return;
   if (r->dev) (void)hipStreamSynchronize(r->dev->stream);
-  for (auto& kv : r->step_graphs) lisa_graph_free(kv.second);
+  for (auto* m : {&r->step_graphs, &r->verify_graphs, &r->mtp_graphs})
+    for (auto& kv : *m) lisa_graph_free(kv.second);
+  if (r->pinned) (void)hipHostFree(r->pinned);
   for (auto& a : r->qmv)
     for (auto& b : a)
       for (LisaFunction* f : b) delete f;
@@ -1284,7 +1399,7 @@ extern "C" int lisa_runner_verify_block3(LisaRunner* r, const uint32_t tokens[3]
     return lisa_fail(LISA_E_CAPACITY, "KV capacity %d exhausted", r->cfg.capacity);
   Ctx& c = r->tgt;
   LISA_TRY(upload_u32(r, c.tokens, tokens, 3));
-  LISA_TRY(encode_target(r, 3, true, false, att_slices(r, r->position + 2, false)));
+  LISA_TRY(launch_verify(r));
   uint32_t am[3];
   LISA_TRY(lisa_hip_check(hipMemcpyAsync(am, c.argmax, 12, hipMemcpyDeviceToHost, r->dev->stream), "D2H argmax"));
   LISA_TRY(sync(r));
@@ -1293,31 +1408,13 @@ extern "C" int lisa_runner_verify_block3(LisaRunner* r, const uint32_t tokens[3]
   if (logits)
     LISA_TRY(lisa_hip_check(hipMemcpy(logits, c.logits, (size_t)3 * r->cfg.vocab * 4, hipMemcpyDeviceToHost),
                             "D2H logits"));
-  r->verify_base = r->position;
-  r->position += 3;
   return LISA_OK;
 }
 
 extern "C" int lisa_runner_commit_verified_prefix(LisaRunner* r, int32_t rows) {
   if (!r) return lisa_fail(LISA_E_ARG, "null runner");
   if (r->verify_base < 0) return lisa_fail(LISA_E_STATE, "no pending block-3 verification");
-  if (rows < 1 || rows > 3) {
-    r->verify_base = -1;
-    return lisa_fail(LISA_E_ARG, "verified prefix must contain 1 to 3 rows");
-  }
-  const uint32_t base = (uint32_t)r->verify_base;
-  r->verify_base = -1;
-  if (rows < 3) {
-    const size_t gs = (size_t)r->gdn_layers * LISA_GDN_STATE;
-    const size_t cs = (size_t)r->gdn_layers * 3 * LISA_GDN_CONV_DIM;
-    LISA_TRY(lisa_hip_check(hipMemcpyAsync(r->gdn_state, r->gdn_slots + (size_t)(rows - 1) * gs, gs * 4,
-                                           hipMemcpyDeviceToDevice, r->dev->stream),
-                            "D2D gdn slot"));
-    LISA_TRY(lisa_hip_check(hipMemcpyAsync(r->conv_state, r->conv_slots + (size_t)(rows - 1) * cs, cs * 2,
-                                           hipMemcpyDeviceToDevice, r->dev->stream),
-                            "D2D conv slot"));
-  }
-  r->position = base + (uint32_t)rows;
+  LISA_TRY(commit_enqueue(r, rows));
   LISA_TRY(write_pos(r, r->tgt, r->position));
   return sync(r);
 }
@@ -1380,26 +1477,14 @@ extern "C" int lisa_mtp_forward(LisaRunner* r, uint32_t token, int32_t cond_sour
   if (!r) return lisa_fail(LISA_E_ARG, "null runner");
   if (!r->cfg.with_mtp) return lisa_fail(LISA_E_STATE, "runner was created without the MTP drafter");
   LISA_TRY(check_token(r, token));
-  if (r->mtp_position >= (uint32_t)r->cfg.capacity)
-    return lisa_fail(LISA_E_CAPACITY, "MTP KV capacity %d exhausted", r->cfg.capacity);
-  const uint16_t* cond;
-  switch (cond_source) {
-    case 0:
-      if (cond_row < 0 || cond_row > 2) return lisa_fail(LISA_E_ARG, "cond_row must be 0..2");
-      cond = r->tgt.H + (size_t)cond_row * LISA_HIDDEN;
-      break;
-    case 1: cond = r->drf.xnorm; break;
-    case 2: cond = r->drf.cond; break;
-    default: return lisa_fail(LISA_E_ARG, "bad cond_source %d", cond_source);
-  }
+  LISA_TRY(check_mtp_step(r, cond_source, cond_row));
   Ctx& c = r->drf;
   LISA_TRY(upload_u32(r, c.tokens, &token, 1));
-  LISA_TRY(encode_mtp(r, cond));
+  LISA_TRY(launch_mtp(r, cond_source, cond_row));
   uint32_t am = 0;
   LISA_TRY(lisa_hip_check(hipMemcpyAsync(&am, c.argmax, 4, hipMemcpyDeviceToHost, r->dev->stream), "D2H argmax"));
   LISA_TRY(sync(r));
   if (argmax) *argmax = am;
-  r->mtp_position += 1;
   return LISA_OK;
 }
 
@@ -1446,6 +1531,82 @@ extern "C" int lisa_mtp_trim_state(LisaRunner* r, int32_t count) {
   LISA_TRY(write_pos(r, r->drf, r->mtp_position));
   return sync(r);
 }
+
+// ---- stream-ordered round pieces (spec_round.h) ----------------------------
+int round_pinned(LisaRunner* r, uint32_t** out) {
+  if (!r->pinned) {
+    void* p = nullptr;
+    LISA_TRY(lisa_hip_check(hipHostMalloc(&p, ROUND_PIN_WORDS * sizeof(uint32_t), hipHostMallocDefault),
+                            "hipHostMalloc round staging"));
+    r->pinned = static_cast<uint32_t*>(p);
+    std::memset(r->pinned, 0, ROUND_PIN_WORDS * sizeof(uint32_t));
+  }
+  *out = r->pinned;
+  return LISA_OK;
+}
+
+namespace {
+int pinned_copy(LisaRunner* r, void* dst, const void* src, size_t n, hipMemcpyKind kind, const char* what) {
+  return lisa_hip_check(hipMemcpyAsync(dst, src, n, kind, r->dev->stream), what);
+}
+int need_pinned(LisaRunner* r) {
+  return r->pinned ? LISA_OK : lisa_fail(LISA_E_STATE, "round staging not allocated");
+}
+}  // namespace
+
+int round_mtp(LisaRunner* r, bool token_on_host, int32_t cond_source, int32_t cond_row) {
+  LISA_TRY(need_pinned(r));
+  LISA_TRY(check_mtp_step(r, cond_source, cond_row));
+  Ctx& c = r->drf;
+  if (token_on_host) {
+    LISA_TRY(check_token(r, r->pinned[ROUND_PIN_MTP_TOKEN]));
+    LISA_TRY(pinned_copy(r, c.tokens, r->pinned + ROUND_PIN_MTP_TOKEN, 4, hipMemcpyHostToDevice, "H2D token"));
+  } else {
+    LISA_TRY(pinned_copy(r, c.tokens, c.argmax, 4, hipMemcpyDeviceToDevice, "D2D token"));
+  }
+  return launch_mtp(r, cond_source, cond_row);
+}
+
+int round_forward_draft(LisaRunner* r, int slot, int host_word) {
+  LISA_TRY(need_pinned(r));
+  if (slot < 1 || slot > 2 || host_word >= ROUND_PIN_WORDS) return lisa_fail(LISA_E_ARG, "bad draft slot");
+  LISA_TRY(pinned_copy(r, r->tgt.tokens + slot, r->drf.argmax, 4, hipMemcpyDeviceToDevice, "D2D draft"));
+  if (host_word >= 0)
+    LISA_TRY(pinned_copy(r, r->pinned + host_word, r->drf.argmax, 4, hipMemcpyDeviceToHost, "D2H draft"));
+  return LISA_OK;
+}
+
+int round_set_verify_tokens(LisaRunner* r, int first, int n) {
+  LISA_TRY(need_pinned(r));
+  if (first < 0 || n < 1 || first + n > 3) return lisa_fail(LISA_E_ARG, "bad verify token range");
+  for (int i = first; i < first + n; ++i) LISA_TRY(check_token(r, r->pinned[ROUND_PIN_BONUS + i]));
+  return pinned_copy(r, r->tgt.tokens + first, r->pinned + ROUND_PIN_BONUS + first, 4 * (size_t)n,
+                     hipMemcpyHostToDevice, "H2D verify tokens");
+}
+
+int round_verify(LisaRunner* r) {
+  LISA_TRY(need_pinned(r));
+  LISA_TRY(launch_verify(r));
+  return pinned_copy(r, r->pinned + ROUND_PIN_TARGET, r->tgt.argmax, 12, hipMemcpyDeviceToHost, "D2H argmax");
+}
+
+int round_commit(LisaRunner* r, int32_t rows) {
+  LISA_TRY(need_pinned(r));
+  LISA_TRY(commit_enqueue(r, rows));
+  r->pinned[ROUND_PIN_TPOS] = r->position;
+  return pinned_copy(r, r->tgt.pos, r->pinned + ROUND_PIN_TPOS, 4, hipMemcpyHostToDevice, "H2D pos");
+}
+
+int round_trim(LisaRunner* r, int32_t count) {
+  LISA_TRY(need_pinned(r));
+  if (count < 0 || (uint32_t)count > r->mtp_position)
+    return lisa_fail(LISA_E_ARG, "cannot trim %d MTP positions from %u", count, r->mtp_position);
+  r->mtp_position -= (uint32_t)count;
+  r->pinned[ROUND_PIN_DPOS] = r->mtp_position;
+  return pinned_copy(r, r->drf.pos, r->pinned + ROUND_PIN_DPOS, 4, hipMemcpyHostToDevice, "H2D pos");
+}
+
+int round_sync(LisaRunner* r) { return sync(r); }
 
 // MtpRunner::checkpoint_state / restore_state (runner.rs:2382-2420): the
 // drafter's KV caches (device-to-device copies of the whole capacity) and its

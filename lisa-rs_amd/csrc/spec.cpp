@@ -7,6 +7,7 @@
 #include "bridge.h"
 #include "lisa_hip.h"
 #include "lisa_synth.h"
+#include "spec_round.h"
 
 // speculative/mod.rs:16-32
 extern "C" int lisa_accept_greedy(const uint32_t* drafts, int32_t n, const uint32_t* target, LisaAcceptance* out) {
@@ -36,7 +37,12 @@ extern "C" int lisa_mtp_reconcile_plan(int32_t draft_count, int32_t round_append
 }
 
 // run_block3_loop (speculative/mod.rs:102-198) after
-// generate_greedy_block3_prefilled (:384-413).
+// generate_greedy_block3_prefilled (:384-413). A round is enqueued without
+// waiting for the device until its verification: the drafter's argmaxes
+// reach the verify tokens and the next drafter step on the device, and the
+// host reads them, with the verified rows, after one wait per round. The
+// tokens, acceptance, commits and trims are those of the step-by-step loop
+// (lisa_mtp_forward, lisa_runner_verify_block3, ... in turn).
 extern "C" int lisa_generate_greedy_block3(LisaRunner* r, uint32_t bonus, const float* target_hidden,
                                            uint32_t mtp_seed_token, const float* mtp_seed_hidden,
                                            int32_t max_tokens, const uint32_t* force_truth, int32_t force_len,
@@ -55,7 +61,11 @@ extern "C" int lisa_generate_greedy_block3(LisaRunner* r, uint32_t bonus, const 
   // (speculative/mod.rs:117-122)
   LISA_TRY(lisa_runner_upload_hidden(r, 0, target_hidden));
   LISA_TRY(lisa_mtp_upload_normalized(r, mtp_seed_hidden));
-  bool have_seed = true;
+  uint32_t* pin = nullptr;
+  LISA_TRY(round_pinned(r, &pin));
+  // the round's first draft: the seed token on the host (first round), else
+  // the argmax of the drafter step that closed the previous round
+  bool seed_on_device = false;
   uint32_t seed_token = mtp_seed_token;
   const uint64_t force_key = lisa_stream_key(force_seed, 0x5eedull);
   uint64_t force_ctr = 0;
@@ -72,57 +82,64 @@ extern "C" int lisa_generate_greedy_block3(LisaRunner* r, uint32_t bonus, const 
       }
       break;
     }
-    uint32_t drafts[2];
-    int round_appended;
-    if (have_seed) {
-      uint32_t d1 = 0;
-      LISA_TRY(lisa_mtp_forward(r, seed_token, 1, 0, &d1));
-      drafts[0] = seed_token;
-      drafts[1] = d1;
-      round_appended = 1;
-      have_seed = false;
+    // drafts: the seed, then one drafter step from it (conditioned on the
+    // drafter's own normalized output)
+    if (seed_on_device) {
+      LISA_TRY(round_forward_draft(r, 1, ROUND_PIN_SEED));
+      LISA_TRY(round_mtp(r, false, 1, 0));
     } else {
-      uint32_t d0 = 0, d1 = 0;
-      LISA_TRY(lisa_mtp_forward(r, bonus, 0, 0, &d0));
-      LISA_TRY(lisa_mtp_forward(r, d0, 1, 0, &d1));
-      drafts[0] = d0;
-      drafts[1] = d1;
-      round_appended = 2;
+      pin[ROUND_PIN_DRAFTS] = seed_token;
+      LISA_TRY(round_set_verify_tokens(r, 1, 1));
+      pin[ROUND_PIN_MTP_TOKEN] = seed_token;
+      LISA_TRY(round_mtp(r, true, 1, 0));
     }
+    LISA_TRY(round_forward_draft(r, 2, ROUND_PIN_D1));
+    const int round_appended = 1;
+    // forced drafts replace the drafter's on the device before the verification
+    bool forced[2] = {false, false};
+    uint32_t forced_tok[2] = {0, 0};
     if (force_truth) {
       for (int j = 0; j < 2; ++j) {
         const size_t idx = out.size() + (size_t)j;
         if ((int64_t)idx < force_len) {
           const float u = lisa_rand_unit(lisa_rand64(force_key, force_ctr++));
           const uint32_t truth = force_truth[idx];
-          drafts[j] = (u < p_accept) ? truth : (truth + 1u) % vocab;
+          forced[j] = true;
+          forced_tok[j] = (u < p_accept) ? truth : (truth + 1u) % vocab;
+          pin[ROUND_PIN_DRAFTS + j] = forced_tok[j];
+          LISA_TRY(round_set_verify_tokens(r, 1 + j, 1));
         }
       }
     }
-    const uint32_t verify_tokens[3] = {bonus, drafts[0], drafts[1]};
-    uint32_t target[3];
-    LISA_TRY(lisa_runner_verify_block3(r, verify_tokens, target, nullptr, nullptr));
+    pin[ROUND_PIN_BONUS] = bonus;
+    LISA_TRY(round_set_verify_tokens(r, 0, 1));
+    LISA_TRY(round_verify(r));
+    LISA_TRY(round_sync(r));
     st.target_forwards += 1;
+    uint32_t drafts[2] = {seed_on_device ? pin[ROUND_PIN_SEED] : seed_token, pin[ROUND_PIN_D1]};
+    for (int j = 0; j < 2; ++j)
+      if (forced[j]) drafts[j] = forced_tok[j];
+    const uint32_t target[3] = {pin[ROUND_PIN_TARGET], pin[ROUND_PIN_TARGET + 1], pin[ROUND_PIN_TARGET + 2]};
     LisaAcceptance acc;
     LISA_TRY(lisa_accept_greedy(drafts, 2, target, &acc));
-    LISA_TRY(lisa_runner_commit_verified_prefix(r, acc.accepted_drafts + 1));
+    LISA_TRY(round_commit(r, acc.accepted_drafts + 1));
     LisaReconcilePlan plan;
     LISA_TRY(lisa_mtp_reconcile_plan(2, round_appended, acc.accepted_drafts, &plan));
-    LISA_TRY(lisa_mtp_trim_state(r, plan.trim));
-    // only the last replay entry is forwarded (speculative/mod.rs:169-183)
+    LISA_TRY(round_trim(r, plan.trim));
+    // only the last replay entry is forwarded (speculative/mod.rs:169-183);
+    // its argmax seeds the next round on the device
     const int last = plan.replay[plan.replay_count - 1];
-    const uint32_t token = last >= 0 ? drafts[last] : acc.emitted[acc.emitted_count - 1];
+    pin[ROUND_PIN_MTP_TOKEN] = last >= 0 ? drafts[last] : acc.emitted[acc.emitted_count - 1];
     const int cond_row = last >= 0 ? last : acc.accepted_drafts;
-    uint32_t next_seed = 0;
-    LISA_TRY(lisa_mtp_forward(r, token, 0, cond_row, &next_seed));
-    seed_token = next_seed;
-    have_seed = true;
+    LISA_TRY(round_mtp(r, true, 0, cond_row));
+    seed_on_device = true;
     bonus = acc.emitted[acc.emitted_count - 1];
     for (int i = 0; i < acc.emitted_count; ++i) out.push_back(acc.emitted[i]);
     st.rounds += 1;
     st.accepted_drafts += acc.accepted_drafts;
     st.drafted_tokens += 2;
   }
+  LISA_TRY(round_sync(r));
   std::memcpy(tokens_out, out.data(), sizeof(uint32_t) * (size_t)max_tokens);
   if (stats) *stats = st;
   return LISA_OK;
