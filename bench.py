@@ -203,7 +203,8 @@ def kernel_configs(pkg, copies=8, reps=40):
             aps.append(a)
 
         def launch(i):
-            dev.dispatch("lisa_attn_partial_m1", aps[i % copies], (s_max, 4), (256,), wait=False)
+            dev.dispatch("lisa_attn_partial_m1", aps[i % copies], (s_max, 4), (pkg.ATT_PARTIAL_THREADS[1],),
+                         wait=False)
             dev.dispatch("lisa_attn_merge_m1", aps[i % copies], (24, 1), (256,), wait=False)
 
         us = timed(pkg, dev, launch, reps)

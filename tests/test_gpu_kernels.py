@@ -350,7 +350,7 @@ def attention_case(pkg, orc, dev, M, ctx, seed):
     a.key_cache, a.value_cache = bufs["kc"].ptr, bufs["vc"].ptr
     a.part_o, a.part_ml, a.pos, a.gated = bufs["po"].ptr, bufs["pm"].ptr, bufs["pos"].ptr, bufs["g"].ptr
     a.capacity, a.s_max = cap, s_max
-    dev.dispatch(f"lisa_attn_partial_m{M}", a, (s_max, 4), (512 if M == 3 else 256,))
+    dev.dispatch(f"lisa_attn_partial_m{M}", a, (s_max, 4), (pkg.ATT_PARTIAL_THREADS[M],))
     dev.dispatch(f"lisa_attn_merge_m{M}", a, (24, M), (256,))
     got = bufs["g"].read(np.uint16, M * 6144).reshape(M, 6144)
     return got, want, bufs["kc"].read(np.uint16, 4 * cap * 256), kc_w, bufs["vc"].read(np.uint16, 4 * cap * 256), vc_w
@@ -391,6 +391,6 @@ def test_attention_batch3_row_equals_single(pkg, orc, dev):
     a.key_cache, a.value_cache = bufs["kc"].ptr, bufs["vc"].ptr
     a.part_o, a.part_ml, a.pos, a.gated = bufs["po"].ptr, bufs["pm"].ptr, bufs["pos"].ptr, bufs["g"].ptr
     a.capacity, a.s_max = cap, s_max
-    dev.dispatch("lisa_attn_partial_m1", a, (s_max, 4), (256,))
+    dev.dispatch("lisa_attn_partial_m1", a, (s_max, 4), (pkg.ATT_PARTIAL_THREADS[1],))
     dev.dispatch("lisa_attn_merge_m1", a, (24, 1), (256,))
     assert np.array_equal(bufs["g"].read(np.uint16, 6144), got3[2])
