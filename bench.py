@@ -224,7 +224,7 @@ def speculative_phase(pkg, steps=128, p_accept=0.6, seed=0x5EED):
     at ctx 4096, drafts forced to a seeded Bernoulli(p_accept) agreement with
     the target-only greedy stream (speculative/mod.rs:102-198); the emitted
     stream must equal that greedy stream."""
-    cap = CTX + 2 * steps + 64
+    cap = CTX + 2 * steps + 64 + 6
     r = pkg.Runner(layers=LAYERS, vocab=VOCAB, capacity=cap, seed=SEED, with_mtp=True, use_graph=True)
     try:
         r.fill_state(CTX, CTX_SEED)
@@ -247,9 +247,16 @@ def speculative_phase(pkg, steps=128, p_accept=0.6, seed=0x5EED):
         pkg._check(L.lisa_device_synchronize(dev))
         ms = pkg.C.c_float()
         pkg._check(L.lisa_event_elapsed_ms(ev0, ev1, pkg.C.byref(ms)))
+        # one eager M=3 verify pass at the loop's end position, hipEvents around every launch (the
+        # verify rows are committed in full, then the pass is repeated on the committed state)
+        r.profile_block3([toks[-1], 5, 6])
+        r.commit_verified_prefix(3)
+        prof = r.profile_block3([toks[-1], 5, 6])
+        r.commit_verified_prefix(3)
     finally:
         r.close()
     return {"speculative_decode_tok_s": round(steps / (ms.value / 1e3), 2),
+            "kernels_us_per_verify": {k: round(1e3 * v[0], 2) for k, v in prof.items()},
             "acceptance": round(st["accepted_drafts"] / max(1, st["drafted_tokens"]), 4),
             "tokens": steps, "rounds": st["rounds"], "target_forwards": st["target_forwards"],
             "exact_match": bool(list(toks) == truth), "p_accept_forced": p_accept,
