@@ -263,31 +263,43 @@ def speculative_phase(pkg, steps=128, p_accept=0.6, seed=0x5EED):
             "_tokens": [int(t) for t in toks]}
 
 
-def capacity_phase(pkg, steps, warmup, capacity=32768):
+def capacity_phase(pkg, steps, warmup, capacity=32768, repeats=3):
     """M=1 decode at ctx 4096 on a runner whose KV capacity is the reference's
-    serving default (src/cli/serve.rs:160): the attention grid follows the
-    live context (runner.rs:1498-1500), so the step costs what it costs at a
-    capacity just above the context."""
-    r = pkg.Runner(layers=LAYERS, vocab=VOCAB, capacity=capacity, seed=SEED, use_graph=True)
-    try:
-        L = pkg.lib()
-        dev = L.lisa_runner_device(r.h)
-        r.fill_state(CTX, CTX_SEED)
-        r.decode_greedy(FIRST_TOKEN, warmup)
-        r.fill_state(CTX, CTX_SEED)
-        ev0, ev1 = pkg.C.c_void_p(), pkg.C.c_void_p()
-        pkg._check(L.lisa_event_create(pkg.C.byref(ev0)))
-        pkg._check(L.lisa_event_create(pkg.C.byref(ev1)))
-        pkg._check(L.lisa_device_synchronize(dev))
-        pkg._check(L.lisa_event_record(ev0, dev))
-        toks = r.decode_greedy(FIRST_TOKEN, steps)
-        pkg._check(L.lisa_event_record(ev1, dev))
-        ms = pkg.C.c_float()
-        pkg._check(L.lisa_event_elapsed_ms(ev0, ev1, pkg.C.byref(ms)))
-    finally:
-        r.close()
-    return {"capacity": capacity, "ctx": CTX, "steps": steps, "tok_s": round(steps / (ms.value / 1e3), 3),
-            "ms_per_step": round(ms.value / steps, 4), "_tokens": [int(t) for t in toks]}
+    serving default (src/cli/serve.rs:160), against a runner whose capacity
+    just covers the run, measured the same way (median of `repeats` timed
+    regions from the same state, HIP events): the attention grid follows the
+    live context (runner.rs:1498-1500), so the two should cost the same."""
+    def one(cap):
+        r = pkg.Runner(layers=LAYERS, vocab=VOCAB, capacity=cap, seed=SEED, use_graph=True)
+        try:
+            L = pkg.lib()
+            dev = L.lisa_runner_device(r.h)
+            r.fill_state(CTX, CTX_SEED)
+            r.decode_greedy(FIRST_TOKEN, warmup)
+            ev0, ev1 = pkg.C.c_void_p(), pkg.C.c_void_p()
+            pkg._check(L.lisa_event_create(pkg.C.byref(ev0)))
+            pkg._check(L.lisa_event_create(pkg.C.byref(ev1)))
+            times = []
+            for _ in range(repeats):
+                r.fill_state(CTX, CTX_SEED)
+                pkg._check(L.lisa_device_synchronize(dev))
+                pkg._check(L.lisa_event_record(ev0, dev))
+                toks = r.decode_greedy(FIRST_TOKEN, steps)
+                pkg._check(L.lisa_event_record(ev1, dev))
+                ms = pkg.C.c_float()
+                pkg._check(L.lisa_event_elapsed_ms(ev0, ev1, pkg.C.byref(ms)))
+                times.append(ms.value)
+        finally:
+            r.close()
+        med = float(np.median(times))
+        return {"capacity": cap, "tok_s": round(steps / (med / 1e3), 3), "ms_per_step": round(med / steps, 4),
+                "_tokens": [int(t) for t in toks]}
+    small = one(CTX + steps + warmup + 64)
+    big = one(capacity)
+    return {"capacity": capacity, "ctx": CTX, "steps": steps, "repeats": repeats, "tok_s": big["tok_s"],
+            "ms_per_step": big["ms_per_step"], "small_capacity": small["capacity"],
+            "small_capacity_tok_s": small["tok_s"], "ratio": round(big["tok_s"] / small["tok_s"], 4),
+            "_tokens": big["_tokens"], "_small_tokens": small["_tokens"]}
 
 
 GEMM_SHAPES = [(2048, INTER, HIDDEN, "mlp gate (and up)"), (2048, HIDDEN, INTER, "mlp down"),
@@ -516,8 +528,8 @@ def main():
         result["speculative"] = spec
         print(f"[bench] configs {result['kernel_configs']}; speculative {spec}", file=sys.stderr, flush=True)
         cap = capacity_phase(pkg, K, W)
-        cap_tokens = cap.pop("_tokens")
-        cap["same_tokens"] = bool(cap_tokens == [int(t) for t in tokens])
+        cap_tokens, small_tokens = cap.pop("_tokens"), cap.pop("_small_tokens")
+        cap["same_tokens"] = bool(cap_tokens == [int(t) for t in tokens] and small_tokens == cap_tokens)
         result["capacity_32768"] = cap
         print(f"[bench] capacity 32768 at ctx {CTX}: {cap}", file=sys.stderr, flush=True)
 
