@@ -40,7 +40,7 @@ PROMPT_SEED = 0x2048
 FIRST_TOKEN = 2005  # the reference CLI's default prompt token (src/cli/run.rs:177)
 CTX = 4096
 HBM_PEAK_GBS = 8000.0
-ROOFLINE_KERNEL = "lisa_qmv_k5120_m1_prenorm_gateup"
+ROOFLINE_KERNEL = "lisa_qmv_k5120_m1_prenorm_gateup_wide"
 TRAFFIC_SUMMARY = ROOT / "profiles" / "qmv_gateup_traffic.txt"
 
 HIDDEN, INTER, VOCAB, LAYERS = 5120, 17408, 248320, 64

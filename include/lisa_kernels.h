@@ -28,6 +28,14 @@
  * function of K. */
 #define LISA_QMV_MAX_MATS 4
 
+/* lisa_qmv_k5120_m3_prenorm_gateup_wide: the three-row MLP gate/up (one
+ * GATEUP matrix pair, PRENORM prologue) on workgroups of LISA_QMV_WIDE_THREADS
+ * threads, each owning LISA_QMV_WIDE_TILES consecutive 8-row tiles; grid
+ * ceil(tiles / LISA_QMV_WIDE_TILES). Outputs are the bits of the four-wave
+ * lisa_qmv_k5120_m3_prenorm_gateup. */
+#define LISA_QMV_WIDE_THREADS 1024
+#define LISA_QMV_WIDE_TILES 17
+
 enum {
   LISA_PRO_LOADX = 0,   /* x = bf16 x_in[M][K] */
   LISA_PRO_RESNORM = 1, /* r = bf16(h_in + bf16(o_in)); x = RMSNorm(r, norm_w) */

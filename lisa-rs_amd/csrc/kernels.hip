@@ -597,6 +597,10 @@ struct TileRef {
   const uint32_t *sp0, *sp1;
   void* out;
   uint32_t rows, kind;
+  // the same rows as wave-uniform matrix bases and per-lane (clamped) row
+  // indices, for loads that add a 32-bit byte offset to a scalar base
+  const uint32_t *wb0, *wb1, *sb0, *sb1;
+  uint32_t c0, c1;
 };
 
 // Tile count of a launch, tile_start[n_mats], selected from the entries
@@ -662,7 +666,34 @@ DEV TileRef tile_ref(const LisaQmvParams& p, uint32_t tile, int rp) {
   t.wp1 = reinterpret_cast<const uint4*>(w1 + (size_t)c1 * (K / 8));
   t.sp0 = s0 + (size_t)c0 * G;
   t.sp1 = s1 + (size_t)c1 * G;
+  t.wb0 = w0; t.wb1 = w1; t.sb0 = s0; t.sb1 = s1;
+  t.c0 = c0; t.c1 = c1;
   return t;
+}
+
+// load_unit with each address a scalar matrix base plus a 32-bit per-lane
+// byte offset (one register per address instead of a 64-bit pointer); the
+// row offsets stay below 2^32 bytes for every matrix of the model.
+template <int K, int IMAX>
+DEV void load_unit_off(Unit<IMAX>& u, const TileRef& t, int it0, int it1, int li, int i0, int i1) {
+  auto w16 = [](const uint32_t* base, uint32_t off) {
+    return *reinterpret_cast<const uint4*>(reinterpret_cast<const char*>(base) + off);
+  };
+  auto w4 = [](const uint32_t* base, uint32_t off) {
+    return *reinterpret_cast<const uint32_t*>(reinterpret_cast<const char*>(base) + off);
+  };
+#pragma unroll
+  for (int i = i0; i < i1; ++i) {
+    const int ii = max(min(it0 + i, it1 - 1), 0);
+    const uint32_t g = 16 * ii + li;
+    const uint32_t o0 = t.c0 * (uint32_t)(K / 2) + 32 * g, o1 = t.c1 * (uint32_t)(K / 2) + 32 * g;
+    u.a0[i] = w16(t.wb0, o0);
+    u.b0[i] = w16(t.wb0, o0 + 16);
+    u.a1[i] = w16(t.wb1, o1);
+    u.b1[i] = w16(t.wb1, o1 + 16);
+    u.s0[i] = w4(t.sb0, t.c0 * (uint32_t)(K / 16) + 4 * g);
+    u.s1[i] = w4(t.sb1, t.c1 * (uint32_t)(K / 16) + 4 * g);
+  }
 }
 
 // Every load is unconditional (iterations past the wave's range re-read its
@@ -1053,6 +1084,222 @@ QMV_KERNEL_EPI(5120, 1, LISA_PRO_PRENORM, prenorm, LISA_EPI_GATEUP, gateup)
 QMV_KERNEL_EPI(5120, 3, LISA_PRO_PRENORM, prenorm, LISA_EPI_GATEUP, gateup)
 QMV_KERNEL_EPI(5120, 1, LISA_PRO_PRENORM, prenorm, LISA_EPI_ARGMAX, argmax)
 QMV_KERNEL_EPI(5120, 3, LISA_PRO_PRENORM, prenorm, LISA_EPI_ARGMAX, argmax)
+
+// ---------------------------------------------------------------------------
+// Several-row K = 5120 launches on one workgroup of 16 waves per CU.
+//
+// With M rows staged the x buffer is M times the one-row one (65 KB at three
+// rows), so four-wave workgroups fit two per CU: two waves per SIMD, and the
+// MLP gate/up's 1088 workgroups run in three rounds with the normalizing
+// prologue repeated by each. Here one workgroup of 16 waves owns
+// LISA_QMV_WIDE_TILES = 17 tiles (the gate/up's 4352 tiles are 256 x 17):
+// waves 0..15 run one tile each exactly as the four-wave kernel does, and the
+// five group iterations of the 17th tile run one each on waves 0..4, which
+// store the per-group terms; after a barrier wave 15 adds them in iteration
+// order from 0 and finishes that tile. A tile's running sum is the sum of
+// its per-group terms in iteration order from 0 either way, so every output
+// is the bits of the four-wave kernel (and of the one-row step).
+// ---------------------------------------------------------------------------
+
+template <int M>
+struct WideCfg {
+  using C = QmvCfg<LISA_HIDDEN, M>;
+  static constexpr int NW = 16;
+  static constexpr int XB = C::XBYTES + C::GBYTES;      // staged rows, then X_g
+  static constexpr int RED = XB;                        // statistics: [M][4] partials, [M] factors
+  static constexpr int SCR = RED + 64 * 4;              // chunk sums [M][640] / extra-tile terms
+  static constexpr int SCR_BYTES = (M * kSegChunks > C::IMAX * 64 * 2 * M ? M * kSegChunks : C::IMAX * 64 * 2 * M) * 4;
+  static constexpr int BYTES = SCR + SCR_BYTES;
+  static_assert(5 * M <= 64, "statistics slots");
+};
+
+// PRENORM of M rows over 1024 threads: thread c < 640 holds chunk c of every
+// row. The per-thread sums of squares of the 256-thread prologue (chunks t,
+// t + 256, t + 512, added in that order) are formed by threads 0..255 from
+// the chunk sums the owners put in LDS, then tree64 and (W0 + W1) + (W2 + W3)
+// as there: the statistic, the staged x and X_g are the bits of prenorm_rows.
+template <int M>
+DEV void prenorm_wide(const LisaQmvParams& p, unsigned char* lds, const uint4 (&ha)[M], const uint4& hw) {
+  using W = WideCfg<M>;
+  using C = QmvCfg<LISA_HIDDEN, M>;
+  const int tid = threadIdx.x, lane = tid & 63, wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  float* gsum = reinterpret_cast<float*>(lds + C::XBYTES);
+  float* red = reinterpret_cast<float*>(lds + W::RED);
+  float* parts = reinterpret_cast<float*>(lds + W::SCR);
+  const int c = tid;
+  const bool valid = c < kSegChunks;
+#pragma unroll
+  for (int m = 0; m < M; ++m) {
+    float hv[8];
+    unpack_bf8(ha[m], hv);
+    const float part = ((hv[0] * hv[0] + hv[1] * hv[1]) + (hv[2] * hv[2] + hv[3] * hv[3])) +
+                       ((hv[4] * hv[4] + hv[5] * hv[5]) + (hv[6] * hv[6] + hv[7] * hv[7]));
+    if (valid) parts[m * kSegChunks + c] = part;
+  }
+  __syncthreads();
+  if (wv < 4) {
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+      const float* pm = parts + m * kSegChunks;
+      float ss = pm[tid];
+      ss = ss + pm[tid + 256];
+      if (wv < 2) ss = ss + pm[tid + 512];
+      ss = tree64(ss);
+      if (lane == 0) red[4 * m + wv] = ss;
+    }
+  }
+  __syncthreads();
+  if (tid < M) {
+    const float* rm = red + 4 * tid;
+    red[4 * M + tid] = lisa_rsqrt(((rm[0] + rm[1]) + (rm[2] + rm[3])) / (float)LISA_HIDDEN + LISA_EPS);
+  }
+  __syncthreads();
+  const bool writer = blockIdx.x == 0;
+  float wf[8];
+  unpack_bf8(hw, wf);
+#pragma unroll
+  for (int m = 0; m < M; ++m) {
+    const float inv = red[4 * M + m];
+    float hv[8], f[8], x[8];
+    uint4 xb;
+    unpack_bf8(ha[m], hv);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) f[e] = (hv[e] * inv) * wf[e];
+    round_bf8(f, x, xb);
+    if (valid) put_chunk<LISA_HIDDEN, M>(lds, m, 8 * c, x);
+    put_gsum<LISA_HIDDEN, M>(gsum, m, 8 * c, valid, x);
+    if (valid && writer) {
+      if (p.r_out) reinterpret_cast<uint4*>(p.r_out + (size_t)m * LISA_HIDDEN)[c] = ha[m];
+      if (p.x_out) reinterpret_cast<uint4*>(p.x_out + (size_t)m * LISA_HIDDEN)[c] = xb;
+    }
+  }
+  __syncthreads();
+}
+
+// The MLP gate/up (SwiGLU epilogue) of M rows; launch LISA_QMV_WIDE_THREADS
+// threads per workgroup and tiles / LISA_QMV_WIDE_TILES workgroups. EARLY of
+// the tile's group iterations are issued before the prologue, DEPTH are in
+// flight during the loop.
+template <int M, int EARLY = 1, int DEPTH = 2>
+DEV void qmv_wide_gateup(const LisaQmvParams& p, unsigned char* lds) {
+  constexpr int K = LISA_HIDDEN;
+  using C = QmvCfg<K, M>;
+  using W = WideCfg<M>;
+  static_assert(LISA_QMV_WIDE_TILES == W::NW + 1 && C::IMAX <= W::NW - 1, "extra-tile layout");
+  const float* gsum = reinterpret_cast<const float*>(lds + C::XBYTES);
+  float* xterm = reinterpret_cast<float*>(lds + W::SCR);  // [IMAX][64 lanes][2M]
+
+  const int tid = threadIdx.x, lane = tid & 63, wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int li = lane & 15, rp = lane >> 4;
+  {
+    const uint32_t* kw = reinterpret_cast<const uint32_t*>(&p);
+    asm volatile("" : : "s"(kw[0]), "s"(kw[16]), "s"(kw[32]), "s"(kw[48]), "s"(kw[64]), "s"(kw[80]), "s"(kw[96]));
+  }
+  const uint32_t tiles = qmv_tiles(p);
+  const uint32_t base = blockIdx.x * LISA_QMV_WIDE_TILES;
+  const uint32_t tile = base + wv, xtile = base + W::NW;
+  const bool tile_ok = tile < tiles;
+  const bool xwave = wv < C::IMAX;  // runs iteration wv of the extra tile
+
+  uint4 ha[M], hw;
+  {
+    const int c = min(tid, kSegChunks - 1);
+    hw = reinterpret_cast<const uint4*>(p.norm_w)[c];
+#pragma unroll
+    for (int m = 0; m < M; ++m) ha[m] = reinterpret_cast<const uint4*>(p.h_in + (size_t)m * LISA_HIDDEN)[c];
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  const TileRef tr = tile_ref<K>(p, tile_ok ? tile : tiles - 1, rp);
+  Unit<C::IMAX> u;
+  Unit<1> xu;
+  static_assert(1 <= EARLY && EARLY <= DEPTH && DEPTH <= C::IMAX, "pipeline depths");
+  load_unit_off<K, C::IMAX>(u, tr, 0, C::ITER, li, 0, EARLY);
+  if (xwave) {
+    const TileRef xr = tile_ref<K>(p, xtile < tiles ? xtile : tiles - 1, rp);
+    load_unit_off<K, 1>(xu, xr, wv, wv + 1, li, 0, 1);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  prenorm_wide<M>(p, lds, ha, hw);
+  __builtin_amdgcn_sched_barrier(0);
+  // waves 0..4 first run the extra tile's iteration wv (its weights were
+  // issued with the prologue's loads) and issue the tile's second iteration
+  // after it, so the extra weights never sit beside two of the tile's
+  if (xwave) {
+    float X0[M], X1[M];
+#pragma unroll
+    for (int m = 0; m < M; ++m) { X0[m] = 0.0f; X1[m] = 0.0f; }
+    group_dot2<C::ROWBYTES, C::G, M>(lds, 16 * wv + li, xu.a0[0], xu.b0[0], xu.a1[0], xu.b1[0], xu.s0[0],
+                                     xu.s1[0], gsum, X0, X1);
+    float* dst = xterm + (wv * 64 + lane) * 2 * M;
+#pragma unroll
+    for (int m = 0; m < M; ++m) { dst[m] = X0[m]; dst[M + m] = X1[m]; }
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  load_unit_off<K, C::IMAX>(u, tr, 0, C::ITER, li, EARLY, DEPTH);
+  __builtin_amdgcn_sched_barrier(0);
+
+  float T0[M], T1[M];
+#pragma unroll
+  for (int m = 0; m < M; ++m) { T0[m] = 0.0f; T1[m] = 0.0f; }
+#pragma unroll
+  for (int i = 0; i < C::IMAX; ++i) {
+    group_dot2<C::ROWBYTES, C::G, M>(lds, 16 * i + li, u.a0[i], u.b0[i], u.a1[i], u.b1[i], u.s0[i], u.s1[i], gsum,
+                                     T0, T1);
+    if (i + DEPTH < C::IMAX) {
+      __builtin_amdgcn_sched_barrier(0);
+      load_unit_off<K, C::IMAX>(u, tr, 0, C::ITER, li, i + DEPTH, i + DEPTH + 1);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+  // mlp.metal:11-16
+  auto gateup_store = [&](const TileRef& t, const float (&A)[M], const float (&B)[M], int sl) {
+    uint16_t* out = static_cast<uint16_t*>(t.out);
+    // the row is opaque here, so its store addresses are formed now rather
+    // than before the loop and carried across it
+    uint32_t r = t.r0;
+    asm volatile("" : "+v"(r));
+#pragma unroll
+    for (int m = 0; m < M; ++m)
+      if (sl == m && t.v0) {
+        const float gte = lisa_bf16r(A[m]), up = lisa_bf16r(B[m]);
+        out[(size_t)m * t.rows + r] = lisa_f32_to_bf16(lisa_silu_exp2(gte) * up);
+      }
+  };
+#pragma unroll
+  for (int m = 0; m < M; ++m) { T0[m] = tree16(T0[m]); T1[m] = tree16(T1[m]); }
+  if (tile_ok) gateup_store(tr, T0, T1, li);
+  __syncthreads();
+  if (wv == W::NW - 1 && xtile < tiles) {
+    // lane indices formed again here, not carried across the loop
+    int fl = (int)threadIdx.x;
+    asm volatile("" : "+v"(fl));
+    fl &= 63;
+    const TileRef xr = tile_ref<K>(p, xtile, fl >> 4);
+    float A[M], B[M];
+#pragma unroll
+    for (int m = 0; m < M; ++m) { A[m] = 0.0f; B[m] = 0.0f; }
+#pragma unroll
+    for (int i = 0; i < C::IMAX; ++i) {
+      const float* src = xterm + (i * 64 + fl) * 2 * M;
+#pragma unroll
+      for (int m = 0; m < M; ++m) { A[m] = A[m] + src[m]; B[m] = B[m] + src[M + m]; }
+    }
+#pragma unroll
+    for (int m = 0; m < M; ++m) { A[m] = tree16(A[m]); B[m] = tree16(B[m]); }
+    gateup_store(xr, A, B, fl & 15);
+  }
+}
+
+extern "C" __global__ __launch_bounds__(LISA_QMV_WIDE_THREADS) void lisa_qmv_k5120_m3_prenorm_gateup_wide(
+    LisaQmvParams p) {
+  __shared__ __attribute__((aligned(16))) unsigned char lds[WideCfg<3>::BYTES];
+  qmv_wide_gateup<3>(p, lds);
+}
+extern "C" __global__ __launch_bounds__(LISA_QMV_WIDE_THREADS) void lisa_qmv_k5120_m1_prenorm_gateup_wide(
+    LisaQmvParams p) {
+  __shared__ __attribute__((aligned(16))) unsigned char lds[WideCfg<1>::BYTES];
+  qmv_wide_gateup<1>(p, lds);
+}
 
 // ===========================================================================
 // GDN recurrence (gdn.metal:245-328) + gates (gdn.metal:170-205) + gated

@@ -121,6 +121,7 @@ struct LisaRunner {
   // kernels
   LisaFunction *qmv[2][5][7] = {};  // [m3][K index][prologue mode]
   LisaFunction *qmv_epi[2][7][5] = {};  // K = 5120 with a fixed epilogue: [m3][prologue][epilogue]
+  LisaFunction *qmv_gateup_wide[2] = {};  // MLP gate/up, PRENORM: 17 tiles per 16-wave workgroup [m3]
   LisaFunction *gdn[2] = {}, *attn_part[2] = {}, *attn_merge[2] = {}, *finalize = nullptr, *synth = nullptr;
   // batched prefill
   LisaFunction *gemm = nullptr, *gemm_wide = nullptr, *gemm_swiglu = nullptr, *rows = nullptr, *conv_rows = nullptr, *gdn_prep_rows = nullptr, *gdn_scan_rows = nullptr,
@@ -587,6 +588,11 @@ int launch_qmv(LisaRunner* r, int m_rows, uint32_t K, LisaQmvParams& p, const st
     if (LisaFunction* f = r->qmv_epi[m_rows == 3 ? 1 : 0][p.pro_mode][mats[0].kind]) fn = f;
   }
   if (!fn) return lisa_fail(LISA_E_ARG, "no q4 kernel for K=%u M=%d prologue %u", K, m_rows, p.pro_mode);
+  // the MLP gate/up alone under the PRENORM prologue: one 16-wave workgroup per
+  // 17 tiles (the 4352 tiles of the model's pair are 256 x 17), the bits of
+  // the four-wave kernel
+  const bool wide = K == LISA_HIDDEN && mats.size() == 1 && mats[0].kind == LISA_EPI_GATEUP &&
+                    p.pro_mode == LISA_PRO_PRENORM && !p.gate_ab && !p.am_val;
   p.n_mats = (uint32_t)mats.size();
   uint32_t tiles = 0, rows_total = 0;
   for (size_t e = 0; e < mats.size(); ++e) {
@@ -608,6 +614,11 @@ int launch_qmv(LisaRunner* r, int m_rows, uint32_t K, LisaQmvParams& p, const st
   p.tile_start[mats.size()] = tiles;
   (void)rows_total;
   p.ksplit = qmv_split(K) ? 4 : 1;
+  if (wide) {
+    const uint32_t grid = std::max<uint32_t>(1, (tiles + LISA_QMV_WIDE_TILES - 1) / LISA_QMV_WIDE_TILES);
+    return lisa_launch(r->dev, r->qmv_gateup_wide[m_rows == 3 ? 1 : 0], &p, sizeof p, grid, 1, 1,
+                       LISA_QMV_WIDE_THREADS, 1, 1);
+  }
   const uint32_t grid = std::max<uint32_t>(1, qmv_grid(K, tiles));
   return lisa_launch(r->dev, fn, &p, sizeof p, grid, 1, 1, 256, 1, 1);
 }
@@ -1039,6 +1050,8 @@ int runner_init(const LisaRunnerConfig* cfg, std::unique_ptr<LisaRunner>& out) {
     LISA_TRY(lisa_function_get(r->mod, (std::string("lisa_gdn_recurrence") + sfx).c_str(), &r->gdn[mi]));
     LISA_TRY(lisa_function_get(r->mod, (std::string("lisa_attn_partial") + sfx).c_str(), &r->attn_part[mi]));
     LISA_TRY(lisa_function_get(r->mod, (std::string("lisa_attn_merge") + sfx).c_str(), &r->attn_merge[mi]));
+    LISA_TRY(lisa_function_get(r->mod, (std::string("lisa_qmv_k5120") + sfx + "_prenorm_gateup_wide").c_str(),
+                               &r->qmv_gateup_wide[mi]));
   }
   LISA_TRY(lisa_function_get(r->mod, "lisa_step_finalize", &r->finalize));
   LISA_TRY(lisa_function_get(r->mod, "lisa_synth_fill", &r->synth));
@@ -1220,6 +1233,7 @@ extern "C" void lisa_runner_free(LisaRunner* r) {
     for (auto& b : a)
       for (LisaFunction* f : b) delete f;
   for (LisaFunction* f : {r->gdn[0], r->gdn[1], r->attn_part[0], r->attn_part[1], r->attn_merge[0], r->attn_merge[1],
+                          r->qmv_gateup_wide[0], r->qmv_gateup_wide[1],
                           r->finalize, r->synth, r->gemm, r->gemm_wide, r->gemm_swiglu, r->rows, r->conv_rows, r->gdn_prep_rows, r->gdn_scan_rows, r->gdn_out_rows, r->attn_store_rows,
                           r->attn_partial_rows, r->attn_merge_rows})
     delete f;

@@ -65,11 +65,12 @@ class DevQ4:
 PROLOGUE_NAMES = ["x", "resnorm", "embed", "cast", "norm", "mtpfc", "prenorm"]
 
 
-def launch_qmv(pkg, dev, K, M, params, mats):
+def launch_qmv(pkg, dev, K, M, params, mats, wide=True):
     """Restates launch_qmv of lisa-rs_amd/csrc/runner.cpp. mats: list of
     (DevQ4, DevQ4-or-None, out_ptr, kind). One 8-row tile per wave (K = 5120,
     four tiles per workgroup) or per workgroup with the group iterations split
-    over its four waves (every other K)."""
+    over its four waves (every other K); the MLP gate/up alone under PRENORM
+    runs on the 16-wave kernel unless wide=False."""
     tiles = 0
     for e, (q, q2, out, kind) in enumerate(mats):
         m = params.mats[e]
@@ -91,5 +92,11 @@ def launch_qmv(pkg, dev, K, M, params, mats):
     if K == 5120 and params.pro_mode in (pkg.PRO_RESNORM, pkg.PRO_PRENORM) and kinds in ({pkg.EPI_GATEUP},
                                                                                     {pkg.EPI_ARGMAX}):
         name += "_gateup" if kinds == {pkg.EPI_GATEUP} else "_argmax"  # the runner's specialized kernels
+    if (wide and K == 5120 and len(mats) == 1 and kinds == {pkg.EPI_GATEUP} and params.pro_mode == pkg.PRO_PRENORM
+            and not params.gate_ab and not params.am_val):
+        # the runner's 16-wave gate/up: LISA_QMV_WIDE_TILES tiles per workgroup
+        grid = max(1, (tiles + pkg.QMV_WIDE_TILES - 1) // pkg.QMV_WIDE_TILES)
+        dev.dispatch(name + "_wide", params, (grid,), (pkg.QMV_WIDE_THREADS,))
+        return params.ksplit, grid
     dev.dispatch(name, params, (grid,), (256,))
     return params.ksplit, grid

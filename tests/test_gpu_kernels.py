@@ -191,6 +191,44 @@ def test_qmv_resid_then_prenorm_gateup(pkg, orc, dev, M):
     assert np.array_equal(act.read(np.uint16, M * N), orc.silu_mul(g, u))
 
 
+@pytest.mark.parametrize("M", [1, 3])
+@pytest.mark.parametrize("N", [1001, 17408])
+def test_qmv_wide_gateup_equals_four_wave(pkg, orc, dev, M, N):
+    """The 16-wave MLP gate/up (17 tiles per workgroup, the 17th tile's five
+    group iterations on waves 0..4, summed in iteration order by wave 15)
+    against the four-wave kernel on the same inputs, bit for bit: at the
+    model's 17408 rows (256 full workgroups) and at 1001 rows (a ragged last
+    tile and a last workgroup of 13 tiles whose 17th is out of range); at
+    1001 rows also against the oracle (mlp.metal:6-17)."""
+    rng = np.random.default_rng(90 + M + N)
+    H = 5120
+    gw, gs, gb = rand_q4(rng, N, H)
+    uw, us, ub = rand_q4(rng, N, H)
+    h = bf16((rng.standard_normal((M, H)) * 4).astype(np.float32))
+    nw = bf16(rng.uniform(0.9, 1.1, H).astype(np.float32))
+    hb, nb = dev.upload(h), dev.upload(nw)
+    qg, qu = DevQ4(dev, gw, gs, gb), DevQ4(dev, uw, us, ub)
+    runs = []
+    for wide in (True, False):
+        act, xo = dev.buffer(M * N * 2), dev.buffer(M * H * 2)
+        q = pkg.QmvParams()
+        q.pro_mode = pkg.PRO_PRENORM
+        q.h_in, q.norm_w, q.x_out = hb.ptr, nb.ptr, xo.ptr
+        ks, grid = launch_qmv(pkg, dev, H, M, q, [(qg, qu, act.ptr, pkg.EPI_GATEUP)], wide=wide)
+        runs.append((act.read(np.uint16, M * N), xo.read(np.uint16, M * H), grid, ks))
+    tiles = (N + 3) // 4
+    assert runs[0][2] == (tiles + pkg.QMV_WIDE_TILES - 1) // pkg.QMV_WIDE_TILES  # the wide launch ran
+    assert runs[1][2] == (tiles + 3) // 4
+    assert np.array_equal(runs[0][0], runs[1][0])
+    assert np.array_equal(runs[0][1], runs[1][1])
+    if N < 2048:
+        xn = np.stack([orc.rms_norm_tiles(h[m], nw) for m in range(M)])
+        assert np.array_equal(runs[0][1].reshape(M, H), xn)
+        g = orc.q4_linear(xn, gw, gs, gb, N, H, M, runs[0][3])
+        u = orc.q4_linear(xn, uw, us, ub, N, H, M, runs[0][3])
+        assert np.array_equal(runs[0][0], orc.silu_mul(g, u))
+
+
 # ---------------------------------------------------------------- config 1
 @pytest.mark.parametrize("M", [1, 3])
 def test_gdn_layer_config1(pkg, orc, dev, M):
