@@ -2100,139 +2100,15 @@ DEV void gemm_step(const uint16_t* as_r, const uint16_t* ws_r, uint16_t* as_w, u
   }
 }
 
-// ---- W staged as q4 (QW) -------------------------------------------------
-// Per K step a W row is its 8 q4 words, stored as [w0 w2 w4 w6 | w1 w3 w5 w7]
-// so that a lane's four 16-k slices (words 2 ks + h, h = lane / 32) are one
-// 16-byte read, then its scale/bias word: 12 dwords per row (48 bytes, so the
-// 16 lanes of a read pass touch disjoint banks). Each wave dequantizes its
-// own B fragments in registers: a fragment of one 16-k slice is exactly one
-// q4 word, bf16(fma(s, q, b)) per nibble (q as an f16 subnormal into
-// v_fma_mix_f32 with s scaled by 2^24, or 2^20 for the fields at bit 4),
-// the values the dequantizing staging writes, in the same k order. LDS bytes
-// per K step: W 12 KB written and 16 KB read instead of 32 KB and 64 KB.
-constexpr int GEMM_WQ = 12;
-
-DEV lisa_bf16x8 gemm_deq8(uint32_t w, float s24, float s20, float b) {
-  const uint32_t p0 = w & 0x000f000fu, p1 = w & 0x00f000f0u, t = w >> 8;
-  const uint32_t p2 = t & 0x000f000fu, p3 = t & 0x00f000f0u;
-  const float v0 = fmix_lo(s24, p0, b), v4 = fmix_hi(s24, p0, b);
-  const float v1 = fmix_lo(s20, p1, b), v5 = fmix_hi(s20, p1, b);
-  const float v2 = fmix_lo(s24, p2, b), v6 = fmix_hi(s24, p2, b);
-  const float v3 = fmix_lo(s20, p3, b), v7 = fmix_hi(s20, p3, b);
-  const lisa_u32x4 u = {lisa_f32x2_to_bf16x2(v0, v1), lisa_f32x2_to_bf16x2(v2, v3), lisa_f32x2_to_bf16x2(v4, v5),
-                        lisa_f32x2_to_bf16x2(v6, v7)};
-  return __builtin_bit_cast(lisa_bf16x8, u);
-}
-
-// A chunks as gemm_lstore; W chunk c = u & 1 (words 4c .. 4c + 3) of row
-// u / 2, u = RW tid + r, into the permuted q4 row, with the row's
-// scale/bias word.
-template <int BN, int NT>
-DEV void gemm_wq_store(uint32_t* wq, int tid, const lisa_u32x4* w, uint32_t sb) {
-  using G = GemmCfg<BN, NT>;
-  static_assert(G::RW == 1 || G::RW == 2, "one or two W chunks per thread");
-#pragma unroll
-  for (int r = 0; r < G::RW; ++r) {
-    const int u = G::RW * tid + r, c = u & 1;
-    uint32_t* dst = wq + (u >> 1) * GEMM_WQ;
-    *reinterpret_cast<uint2*>(dst + 2 * c) = make_uint2(w[r].x, w[r].z);
-    *reinterpret_cast<uint2*>(dst + 4 + 2 * c) = make_uint2(w[r].y, w[r].w);
-    if (c == 0) dst[8] = sb;
-  }
-}
-
-template <int BN, int NT>
-DEV void gemm_lstore_q(uint16_t* as, uint32_t* wq, int tid, const lisa_u32x4* a, const lisa_u32x4* w, uint32_t sb) {
-  using G = GemmCfg<BN, NT>;
-#pragma unroll
-  for (int i = 0; i < G::RA; ++i) {
-    const int u = tid + NT * i;
-    *reinterpret_cast<lisa_u32x4*>(&as[(u >> 3) * GEMM_PAD + (u & 7) * 8]) = a[i];
-  }
-  gemm_wq_store<BN, NT>(wq, tid, w, sb);
-}
-
-template <int NT>
-DEV void gemm_afrags(const uint16_t* as, int wm, int lane, int ks, lisa_bf16x8 (&af)[4]) {
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-    af[i] = *reinterpret_cast<const lisa_bf16x8*>(
-        &as[(wm * 128 + i * 32 + (lane & 31)) * GEMM_PAD + ks * 16 + 8 * (lane >> 5)]);
-}
-
-template <int BN, int NT>
-DEV void gemm_step_q(const uint16_t* as_r, const uint32_t* wq_r, uint16_t* as_w, uint32_t* wq_w, int tid, int wm,
-                     int wn, int lane, const lisa_u32x4* a, const lisa_u32x4* w, uint32_t sb,
-                     lisa_f32x16 (&acc)[4][GemmCfg<BN, NT>::NB]) {
-  using G = GemmCfg<BN, NT>;
-  lisa_u32x4 wq[G::NB];
-  float s24[G::NB], s20[G::NB], bb[G::NB];
-#pragma unroll
-  for (int j = 0; j < G::NB; ++j) {
-    const uint32_t* row = wq_r + (wn * (BN / G::WN) + j * 32 + (lane & 31)) * GEMM_WQ;
-    wq[j] = *reinterpret_cast<const lisa_u32x4*>(row + 4 * (lane >> 5));
-    const uint32_t sbw = row[8];
-    const float sc = lo_bf(sbw);
-    s24[j] = sc * 16777216.0f;
-    s20[j] = sc * 1048576.0f;
-    bb[j] = hi_bf(sbw);
-  }
-  lisa_bf16x8 af[2][4], bf[2][G::NB];
-  gemm_afrags<NT>(as_r, wm, lane, 0, af[0]);
-#pragma unroll
-  for (int j = 0; j < G::NB; ++j) bf[0][j] = gemm_deq8(wq[j][0], s24[j], s20[j], bb[j]);
-#pragma unroll
-  for (int ks = 0; ks < 4; ++ks) {
-    const int c = ks & 1;
-    if (ks + 1 < 4) {
-      gemm_afrags<NT>(as_r, wm, lane, ks + 1, af[c ^ 1]);
-#pragma unroll
-      for (int j = 0; j < G::NB; ++j) bf[c ^ 1][j] = gemm_deq8(wq[j][ks + 1], s24[j], s20[j], bb[j]);
-    }
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-      for (int j = 0; j < G::NB; ++j)
-        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[c][i], bf[c][j], acc[i][j], 0, 0, 0);
-    if (ks == 0) gemm_wq_store<BN, NT>(wq_w, tid, w, sb);
-#pragma unroll
-    for (int i = ks * (G::RA / 4); i < (ks + 1) * (G::RA / 4); ++i) {
-      const int u = tid + NT * i;
-      *reinterpret_cast<lisa_u32x4*>(&as_w[(u >> 3) * GEMM_PAD + (u & 7) * 8]) = a[i];
-    }
-    // masks: 0x100 LDS read, 0x008 MFMA, 0x002 VALU, 0x200 LDS write
-    if (ks + 1 < 4) {
-      __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
-#pragma unroll
-      for (int q = 0; q < 4 * G::NB; ++q) {
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(0x002, 17 / 4 + 1, 0);
-      }
-    } else {
-#pragma unroll
-      for (int q = 0; q < 4 * G::NB; ++q) {
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(0x002, 1, 0);
-      }
-    }
-    if (ks == 0) __builtin_amdgcn_sched_group_barrier(0x200, G::RA / 4 + 2 * G::RW + 1, 0);
-    else __builtin_amdgcn_sched_group_barrier(0x200, G::RA / 4, 0);
-  }
-}
-
 // SWIGLU: the tile's W rows are the gate and up rows of BN / 2 output
 // columns, laid out so that MFMA block j of wave wn holds matrix j (0 gate,
 // 1 up) of columns n0 + wn * 32 + (0..31); the epilogue then finds the gate
 // and up sums of an output in the same lane and writes bf16(silu(bf16 g) *
 // bf16 u) (mlp.metal:11-16) instead of the two f32 outputs.
-template <int BN, int NT, bool SWIGLU = false, bool QW = false>
+template <int BN, int NT, bool SWIGLU = false>
 DEV void q4_gemm_body(const LisaGemmParams& p, uint16_t (*As)[GEMM_BM * GEMM_PAD], uint16_t (*Ws)[BN * GEMM_PAD]) {
-  // QW: Ws points at two stages of BN q4 rows (GEMM_WQ dwords each) instead
-  // of dequantized ones
-  uint32_t* Wq0 = reinterpret_cast<uint32_t*>(Ws[0]);
-  uint32_t* Wq1 = Wq0 + BN * GEMM_WQ;
   using G = GemmCfg<BN, NT>;
-  static_assert(!SWIGLU || G::NB % 2 == 0, "the gate/up tile pairs 32-wide blocks per wave");
+  static_assert(!SWIGLU || G::NB == 2, "the gate/up tile pairs two 32-wide blocks per wave");
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave / G::WN, wn = wave % G::WN;
   const uint32_t m0 = blockIdx.y * GEMM_BM, n0 = blockIdx.x * (SWIGLU ? BN / 2 : BN);
@@ -2275,8 +2151,7 @@ DEV void q4_gemm_body(const LisaGemmParams& p, uint16_t (*As)[GEMM_BM * GEMM_PAD
   uint32_t sb0, sb1;
   GEMM_GLOAD(a0, w0, sb0, 0);
   GEMM_GLOAD(a1, w1, sb1, 1);
-  if constexpr (QW) gemm_lstore_q<BN, NT>(As[0], Wq0, tid, a0, w0, sb0);
-  else gemm_lstore<BN, NT>(As[0], Ws[0], tid, a0, w0, sb0);
+  gemm_lstore<BN, NT>(As[0], Ws[0], tid, a0, w0, sb0);
   __syncthreads();
   // Pairs of K steps. With an odd number of steps the second half of the
   // last pair is a phantom step past K whose scale and bias words are zero, so
@@ -2285,31 +2160,25 @@ DEV void q4_gemm_body(const LisaGemmParams& p, uint16_t (*As)[GEMM_BM * GEMM_PAD
   // matrix registers (the eight-wave tile then spills).
   for (uint32_t step = 0; step < nk; step += 2) {
     GEMM_GLOAD(a0, w0, sb0, step + 2);
-    if constexpr (QW) gemm_step_q<BN, NT>(As[0], Wq0, As[1], Wq1, tid, wm, wn, lane, a1, w1, sb1, acc);
-    else gemm_step<BN, NT>(As[0], Ws[0], As[1], Ws[1], tid, wm, wn, lane, a1, w1, sb1, acc);
+    gemm_step<BN, NT>(As[0], Ws[0], As[1], Ws[1], tid, wm, wn, lane, a1, w1, sb1, acc);
     __syncthreads();
     GEMM_GLOAD(a1, w1, sb1, step + 3);
-    if constexpr (QW) gemm_step_q<BN, NT>(As[1], Wq1, As[0], Wq0, tid, wm, wn, lane, a0, w0, sb0, acc);
-    else gemm_step<BN, NT>(As[1], Ws[1], As[0], Ws[0], tid, wm, wn, lane, a0, w0, sb0, acc);
+    gemm_step<BN, NT>(As[1], Ws[1], As[0], Ws[0], tid, wm, wn, lane, a0, w0, sb0, acc);
     __syncthreads();
   }
 #undef GEMM_GLOAD
   if constexpr (SWIGLU) {
+    const uint32_t col = n0 + wn * 32 + (lane & 31);
 #pragma unroll
-    for (int jp = 0; jp < G::NB / 2; ++jp) {
-      const uint32_t col = n0 + wn * (BN / G::WN / 2) + jp * 32 + (lane & 31);
+    for (int i = 0; i < 4; ++i)
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const uint32_t row = m0 + wm * 128 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-          if (row < p.m && col < p.n) {
-            const float a =
-                lisa_bf16r(lisa_silu_exp2(lisa_bf16r(acc[i][2 * jp][r])) * lisa_bf16r(acc[i][2 * jp + 1][r]));
-            p.act[(size_t)row * p.ldc + col] = lisa_f32_to_bf16(a);
-          }
+      for (int r = 0; r < 16; ++r) {
+        const uint32_t row = m0 + wm * 128 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+        if (row < p.m && col < p.n) {
+          const float a = lisa_bf16r(lisa_silu_exp2(lisa_bf16r(acc[i][0][r])) * lisa_bf16r(acc[i][1][r]));
+          p.act[(size_t)row * p.ldc + col] = lisa_f32_to_bf16(a);
         }
-    }
+      }
   } else {
 #pragma unroll
     for (int i = 0; i < 4; ++i)
@@ -2328,13 +2197,7 @@ DEV void q4_gemm_body(const LisaGemmParams& p, uint16_t (*As)[GEMM_BM * GEMM_PAD
 // lisa_q4_gemm: one 4-wave workgroup per CU (the LDS stages take 108 KB), so the
 // whole register file is available to its waves. lisa_q4_gemm_wide: eight
 // waves, two per SIMD (252 registers each), so one wave's MFMAs run while the
-// other waits on a barrier, an LDS read or its dequant; W is staged as q4
-// (QW), which cut the LDS bytes per K step from 256 to ~190 KB (gate/up
-// 2048x17408x5120 516 -> 464 us, the SwiGLU pair 906 -> 830 us, down 521 ->
-// 485 us, same outputs). Four waves of 128 x 128 on the q4-staged tile (half
-// the A fragment reads) measured slower (591 us), and so did q4 staging in
-// lisa_q4_gemm (2048x1024x5120 93 -> 105 us): one wave per SIMD does not cover
-// the in-register dequant's latency.
+// other waits on a barrier, an LDS read or its dequant.
 extern "C" __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void lisa_q4_gemm(
     LisaGemmParams p) {
   __shared__ __attribute__((aligned(16))) uint16_t As[2][GEMM_BM * GEMM_PAD];
@@ -2344,18 +2207,16 @@ extern "C" __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(
 extern "C" __global__ __launch_bounds__(LISA_GEMM_THREADS_WIDE) __attribute__((amdgpu_waves_per_eu(2, 2))) void lisa_q4_gemm_wide(
     LisaGemmParams p) {
   __shared__ __attribute__((aligned(16))) uint16_t As[2][GEMM_BM * GEMM_PAD];
-  __shared__ __attribute__((aligned(16))) uint32_t Wq[2][LISA_GEMM_TILE_N_WIDE * GEMM_WQ];
-  q4_gemm_body<LISA_GEMM_TILE_N_WIDE, LISA_GEMM_THREADS_WIDE, false, true>(
-      p, As, reinterpret_cast<uint16_t (*)[LISA_GEMM_TILE_N_WIDE * GEMM_PAD]>(Wq));
+  __shared__ __attribute__((aligned(16))) uint16_t Ws[2][LISA_GEMM_TILE_N_WIDE * GEMM_PAD];
+  q4_gemm_body<LISA_GEMM_TILE_N_WIDE, LISA_GEMM_THREADS_WIDE>(p, As, Ws);
 }
 // The MLP's gate/up pair with the SwiGLU epilogue: 256 rows x 128 outputs per
 // workgroup (the eight-wave tile over 128 gate and 128 up rows).
 extern "C" __global__ __launch_bounds__(LISA_GEMM_THREADS_WIDE) __attribute__((amdgpu_waves_per_eu(2, 2))) void lisa_q4_gemm_swiglu(
     LisaGemmParams p) {
   __shared__ __attribute__((aligned(16))) uint16_t As[2][GEMM_BM * GEMM_PAD];
-  __shared__ __attribute__((aligned(16))) uint32_t Wq[2][LISA_GEMM_TILE_N_WIDE * GEMM_WQ];
-  q4_gemm_body<LISA_GEMM_TILE_N_WIDE, LISA_GEMM_THREADS_WIDE, true, true>(
-      p, As, reinterpret_cast<uint16_t (*)[LISA_GEMM_TILE_N_WIDE * GEMM_PAD]>(Wq));
+  __shared__ __attribute__((aligned(16))) uint16_t Ws[2][LISA_GEMM_TILE_N_WIDE * GEMM_PAD];
+  q4_gemm_body<LISA_GEMM_TILE_N_WIDE, LISA_GEMM_THREADS_WIDE, true>(p, As, Ws);
 }
 
 // Per-row kernels. NORM/RESNORM follow the q4 prologue's arithmetic exactly
