@@ -74,3 +74,42 @@ def test_python_launch_sizes_match_the_kernels():
     hdr = (Path(pkg.PKG_DIR).parent / "include" / "lisa_kernels.h").read_text()
     assert int(re.search(r"#define LISA_QMV_WIDE_TILES (\d+)", hdr).group(1)) == pkg.QMV_WIDE_TILES
     assert int(re.search(r"#define LISA_QMV_WIDE_THREADS (\d+)", hdr).group(1)) == pkg.QMV_WIDE_THREADS
+
+
+STRUCTS = {  # Python mirror -> C typedef (include/lisa_kernels.h, include/lisa_hip.h)
+    "Q4Mat": "LisaQ4Mat", "QmvParams": "LisaQmvParams", "GdnParams": "LisaGdnParams",
+    "AttnParams": "LisaAttnParams", "GemmParams": "LisaGemmParams", "RowsParams": "LisaRowsParams",
+    "ConvRowsParams": "LisaConvRowsParams", "SynthParams": "LisaSynthParams", "CopyParams": "LisaCopyParams",
+    "AttnDecodeArgs": "LisaAttnDecodeArgs", "RunnerConfig": "LisaRunnerConfig", "WeightSlotStruct": "LisaWeightSlot",
+    "Acceptance": "LisaAcceptance", "ReconcilePlan": "LisaReconcilePlan", "SpecStats": "LisaSpecStats",
+}
+
+
+@pytest.mark.skipif(shutil.which("g++") is None, reason="no host C++ compiler")
+def test_python_structs_match_the_headers(tmp_path):
+    """Every argument block the Python package passes by value has the C
+    header's size and field offsets (a kernel reads its block by those
+    offsets, so a field the mirror lacks would be read from past the end)."""
+    pkg = load_pkg()
+    inc = Path(pkg.PKG_DIR).parent / "include"
+    lines = ['#include <cstdio>', '#include <cstddef>', '#include "lisa_kernels.h"', '#include "lisa_hip.h"',
+             "int main() {"]
+    want = {}
+    for py, c in STRUCTS.items():
+        cls = getattr(pkg, py)
+        lines.append(f'  std::printf("{py} size %zu\\n", sizeof({c}));')
+        want[f"{py} size"] = pkg.C.sizeof(cls)
+        for name, _ in cls._fields_:
+            if name.startswith("pad"):
+                continue
+            lines.append(f'  std::printf("{py}.{name} %zu\\n", offsetof({c}, {name}));')
+            want[f"{py}.{name}"] = getattr(cls, name).offset
+    lines += ["  return 0;", "}"]
+    src, exe = tmp_path / "layout.cpp", tmp_path / "layout"
+    src.write_text("\n".join(lines) + "\n")
+    subprocess.run(["g++", "-std=c++17", f"-I{inc}", str(src), "-o", str(exe)], check=True, capture_output=True)
+    got = {}
+    for line in subprocess.run([str(exe)], check=True, capture_output=True, text=True).stdout.splitlines():
+        key, val = line.rsplit(" ", 1)
+        got[key] = int(val)
+    assert got == want
