@@ -116,12 +116,10 @@ def calibrate_copy(mb):
 
 
 FILL_WORDS, FILL_BF16, FILL_F32, FILL_SB, FILL_KV = range(5)  # lisa_kernels.h LISA_FILL_*
-DIST_NORMAL = 2  # lisa_synth.h LISA_DIST_NORMAL
 
 
 def synth_fill(pkg, dev, buf, n, kind, key, key2=0, capacity=0, filled=0):
-    p = pkg.SynthParams(buf.ptr, n, key, key2, kind, DIST_NORMAL, 0.0, 1.0, capacity, filled)
-    dev.dispatch("lisa_synth_fill", p, (4096,), (256,))
+    dev.synth_fill(buf, n, kind, key, key2, capacity=capacity, filled=filled)
 
 
 def timed(pkg, dev, launch, reps):

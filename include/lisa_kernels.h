@@ -36,6 +36,14 @@
 #define LISA_QMV_WIDE_THREADS 1024
 #define LISA_QMV_WIDE_TILES 17
 
+/* lisa_qmv_k5120_m{1,3}_prenorm_wide{7,8}: a PRENORM launch of STORE and CONV
+ * matrices (optionally with the GDN gate contributions) on workgroups of
+ * 64 NW threads, NW = 7 or 8, one 8-row tile per wave; grid ceil(tiles / NW).
+ * The runner takes them when tiles = LISA_QMV_WIDE_GROUPS x NW (the GDN and
+ * attention in-projections: one workgroup per CU). Outputs are the bits of
+ * the four-wave lisa_qmv_k5120_m{1,3}_prenorm. */
+#define LISA_QMV_WIDE_GROUPS 256
+
 enum {
   LISA_PRO_LOADX = 0,   /* x = bf16 x_in[M][K] */
   LISA_PRO_RESNORM = 1, /* r = bf16(h_in + bf16(o_in)); x = RMSNorm(r, norm_w) */

@@ -46,6 +46,8 @@ KINDS = ["gdn_in_proj", "gdn_recurrence", "gdn_out_proj", "attn_in_proj", "attn_
 # lisa_kernels.h enums
 PRO_LOADX, PRO_RESNORM, PRO_EMBED, PRO_CAST, PRO_NORM, PRO_MTPFC, PRO_PRENORM = range(7)
 EPI_STORE, EPI_GATEUP, EPI_CONV, EPI_ARGMAX, EPI_RESID = range(5)
+FILL_WORDS, FILL_BF16, FILL_F32, FILL_SB, FILL_KV = range(5)
+DIST_BITS, DIST_UNIFORM, DIST_NORMAL = range(3)  # lisa_synth.h LISA_DIST_*
 
 
 class LisaError(RuntimeError):
@@ -108,6 +110,7 @@ ATT_ROWS_PER_WG = 8  # lisa_attn_partial_rows rows per workgroup (LISA_ATT_ROWS_
 ATT_PARTIAL_THREADS = {1: 1024, 3: 1024}  # lisa_attn_partial_m{1,3} workgroup size (LISA_ATT_PARTIAL_THREADS)
 QMV_WIDE_THREADS = 1024  # lisa_qmv_k5120_m{1,3}_prenorm_gateup_wide workgroup size (LISA_QMV_WIDE_THREADS)
 QMV_WIDE_TILES = 17  # 8-row tiles per workgroup of that kernel (LISA_QMV_WIDE_TILES)
+QMV_WIDE_GROUPS = 256  # workgroups of a lisa_qmv_k5120_m{1,3}_prenorm_wide{7,8} launch (LISA_QMV_WIDE_GROUPS)
 
 
 class RowsParams(C.Structure):
@@ -363,6 +366,23 @@ class Device:
             _check(lib().lisa_function_get(self.module, name.encode(), C.byref(f)))
             self._fns[name] = f
         return self._fns[name]
+
+    def synth_fill(self, buf: "Buffer", n: int, kind: int, key: int, key2: int = 0, dist: int = DIST_NORMAL,
+                   a: float = 0.0, b: float = 1.0, capacity: int = 0, filled: int = 0) -> None:
+        """lisa_synth_fill of n elements of `kind` into buf; refuses on the host
+        any fill that would write past the buffer (the kernel has no size)."""
+        if kind == FILL_KV:
+            if not 0 < filled <= capacity or n != ATT_KVH * filled * ATT_HD:
+                raise ValueError(f"KV fill: n={n} filled={filled} capacity={capacity}")
+            need = ATT_KVH * capacity * ATT_HD * 2
+        elif kind in (FILL_WORDS, FILL_F32, FILL_SB, FILL_BF16):
+            need = n * (2 if kind == FILL_BF16 else 4)
+        else:
+            raise ValueError(f"unknown fill kind {kind}")
+        if need > buf.nbytes:
+            raise ValueError(f"fill of {need} bytes into a {buf.nbytes}-byte buffer")
+        self.dispatch("lisa_synth_fill", SynthParams(buf.ptr, n, key, key2, kind, dist, a, b, capacity, filled),
+                      (4096,), (256,))
 
     def dispatch(self, kernel: str, params: C.Structure, grid, block, wait: bool = True) -> None:
         """One dispatch of a kernel taking one argument block (lisa_kernels.h)."""

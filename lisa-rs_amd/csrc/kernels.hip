@@ -792,6 +792,80 @@ DEV void epi_preload(const LisaQmvParams& p, const TileRef& tr, int li, EpiPre<M
   }
 }
 
+// The epilogue of a tile's finished sums T0/T1 (EPI, or the tile's matrix
+// kind when EPI < 0); argmax candidates update best_v/best_i.
+template <int M, int EPI>
+DEV void qmv_epilogue(const LisaQmvParams& p, const TileRef& tr, int li, EpiPre<M>& pre, const float (&T0)[M],
+                      const float (&T1)[M], float (&best_v)[M], uint32_t (&best_i)[M]) {
+  // the preloaded epilogue inputs are first used here: without this, their
+  // conversions are hoisted to the loads and the wave waits for its whole
+  // weight stream right after issuing it
+  if (EPI < 0 || EPI == LISA_EPI_RESID || EPI == LISA_EPI_CONV) {
+#pragma unroll
+    for (int m = 0; m < M; ++m) asm volatile("" : "+v"(pre.h[m]));
+#pragma unroll
+    for (int i = 0; i < 3; ++i) asm volatile("" : "+v"(pre.cs[i]));
+    asm volatile("" : "+v"(pre.cw.x), "+v"(pre.cw.y));
+  }
+  const struct { void* out; uint32_t rows, kind; } mt{tr.out, tr.rows, tr.kind};
+  const uint32_t r0 = tr.r0, r1 = tr.r1;
+  const bool v0 = tr.v0, v1 = tr.v1;
+  switch (EPI >= 0 ? (uint32_t)EPI : mt.kind) {
+    case LISA_EPI_STORE: {
+      float* out = static_cast<float*>(mt.out);
+#pragma unroll
+      for (int m = 0; m < M; ++m) {
+        if (li == 2 * m && v0) out[(size_t)m * mt.rows + r0] = T0[m];
+        if (li == 2 * m + 1 && v1) out[(size_t)m * mt.rows + r1] = T1[m];
+      }
+      break;
+    }
+    case LISA_EPI_GATEUP: {
+      uint16_t* out = static_cast<uint16_t*>(mt.out);
+#pragma unroll
+      for (int m = 0; m < M; ++m)
+        if (li == m && v0) {
+          // mlp.metal:11-16
+          const float gte = lisa_bf16r(T0[m]), up = lisa_bf16r(T1[m]);
+          out[(size_t)m * mt.rows + r0] = lisa_f32_to_bf16(lisa_silu_exp2(gte) * up);
+        }
+      break;
+    }
+    case LISA_EPI_CONV: {
+      if (li == 0 && v0) conv_epilogue<M>(p, static_cast<float*>(mt.out), (int)r0, T0, pre.cs, pre.cw);
+      if (li == 1 && v1) conv_epilogue<M>(p, static_cast<float*>(mt.out), (int)r1, T1, pre.cs, pre.cw);
+      break;
+    }
+    case LISA_EPI_RESID: {
+      // r = bf16(h + bf16(y)) in place
+      uint16_t* hres = const_cast<uint16_t*>(p.h_in);  // read-write for this epilogue
+#pragma unroll
+      for (int m = 0; m < M; ++m) {
+        if (li == 0 && v0 && v1) {
+          const float ra = lisa_bf16r(lo_bf(pre.h[m]) + lisa_bf16r(T0[m]));
+          const float rb = lisa_bf16r(hi_bf(pre.h[m]) + lisa_bf16r(T1[m]));
+          hres[(size_t)m * LISA_HIDDEN + r0] = lisa_f32_to_bf16(ra);
+          hres[(size_t)m * LISA_HIDDEN + r1] = lisa_f32_to_bf16(rb);
+        }
+      }
+      break;
+    }
+    default: { /* ARGMAX */
+      float* out = static_cast<float*>(mt.out);
+#pragma unroll
+      for (int m = 0; m < M; ++m) {
+        if (li == 2 * m && v0) out[(size_t)m * mt.rows + r0] = T0[m];
+        if (li == 2 * m + 1 && v1) out[(size_t)m * mt.rows + r1] = T1[m];
+        if (li == 0) {
+          if (v0 && better(T0[m], r0, best_v[m], best_i[m])) { best_v[m] = T0[m]; best_i[m] = r0; }
+          if (v1 && better(T1[m], r1, best_v[m], best_i[m])) { best_v[m] = T1[m]; best_i[m] = r1; }
+        }
+      }
+      break;
+    }
+  }
+}
+
 // EPI: the epilogue of every matrix of the launch, or -1 to read it per tile.
 template <int K, int M, int MODE, int EPI>
 DEV void qmv_body(const LisaQmvParams& p, unsigned char* lds) {
@@ -916,75 +990,7 @@ DEV void qmv_body(const LisaQmvParams& p, unsigned char* lds) {
 #pragma unroll
   for (int m = 0; m < M; ++m) { best_v[m] = -INFINITY; best_i[m] = 0xffffffffu; }
 
-  if (active) {
-    // the preloaded epilogue inputs are first used here: without this, their
-    // conversions are hoisted to the loads and the wave waits for its whole
-    // weight stream right after issuing it
-    if (EPI < 0 || EPI == LISA_EPI_RESID || EPI == LISA_EPI_CONV) {
-#pragma unroll
-      for (int m = 0; m < M; ++m) asm volatile("" : "+v"(pre.h[m]));
-#pragma unroll
-      for (int i = 0; i < 3; ++i) asm volatile("" : "+v"(pre.cs[i]));
-      asm volatile("" : "+v"(pre.cw.x), "+v"(pre.cw.y));
-    }
-    const struct { void* out; uint32_t rows, kind; } mt{tr.out, tr.rows, tr.kind};
-    const uint32_t r0 = tr.r0, r1 = tr.r1;
-    const bool v0 = tr.v0, v1 = tr.v1;
-    switch (EPI >= 0 ? (uint32_t)EPI : mt.kind) {
-      case LISA_EPI_STORE: {
-        float* out = static_cast<float*>(mt.out);
-#pragma unroll
-        for (int m = 0; m < M; ++m) {
-          if (li == 2 * m && v0) out[(size_t)m * mt.rows + r0] = T0[m];
-          if (li == 2 * m + 1 && v1) out[(size_t)m * mt.rows + r1] = T1[m];
-        }
-        break;
-      }
-      case LISA_EPI_GATEUP: {
-        uint16_t* out = static_cast<uint16_t*>(mt.out);
-#pragma unroll
-        for (int m = 0; m < M; ++m)
-          if (li == m && v0) {
-            // mlp.metal:11-16
-            const float gte = lisa_bf16r(T0[m]), up = lisa_bf16r(T1[m]);
-            out[(size_t)m * mt.rows + r0] = lisa_f32_to_bf16(lisa_silu_exp2(gte) * up);
-          }
-        break;
-      }
-      case LISA_EPI_CONV: {
-        if (li == 0 && v0) conv_epilogue<M>(p, static_cast<float*>(mt.out), (int)r0, T0, pre.cs, pre.cw);
-        if (li == 1 && v1) conv_epilogue<M>(p, static_cast<float*>(mt.out), (int)r1, T1, pre.cs, pre.cw);
-        break;
-      }
-      case LISA_EPI_RESID: {
-        // r = bf16(h + bf16(y)) in place
-        uint16_t* hres = const_cast<uint16_t*>(p.h_in);  // read-write for this epilogue
-#pragma unroll
-        for (int m = 0; m < M; ++m) {
-          if (li == 0 && v0 && v1) {
-            const float ra = lisa_bf16r(lo_bf(pre.h[m]) + lisa_bf16r(T0[m]));
-            const float rb = lisa_bf16r(hi_bf(pre.h[m]) + lisa_bf16r(T1[m]));
-            hres[(size_t)m * LISA_HIDDEN + r0] = lisa_f32_to_bf16(ra);
-            hres[(size_t)m * LISA_HIDDEN + r1] = lisa_f32_to_bf16(rb);
-          }
-        }
-        break;
-      }
-      default: { /* ARGMAX */
-        float* out = static_cast<float*>(mt.out);
-#pragma unroll
-        for (int m = 0; m < M; ++m) {
-          if (li == 2 * m && v0) out[(size_t)m * mt.rows + r0] = T0[m];
-          if (li == 2 * m + 1 && v1) out[(size_t)m * mt.rows + r1] = T1[m];
-          if (li == 0) {
-            if (v0 && better(T0[m], r0, best_v[m], best_i[m])) { best_v[m] = T0[m]; best_i[m] = r0; }
-            if (v1 && better(T1[m], r1, best_v[m], best_i[m])) { best_v[m] = T1[m]; best_i[m] = r1; }
-          }
-        }
-        break;
-      }
-    }
-  }
+  if (active) qmv_epilogue<M, EPI>(p, tr, li, pre, T0, T1, best_v, best_i);
 
   if (p.am_val) {
     // workgroup (max, lowest index) per input row
@@ -1086,25 +1092,29 @@ QMV_KERNEL_EPI(5120, 1, LISA_PRO_PRENORM, prenorm, LISA_EPI_ARGMAX, argmax)
 QMV_KERNEL_EPI(5120, 3, LISA_PRO_PRENORM, prenorm, LISA_EPI_ARGMAX, argmax)
 
 // ---------------------------------------------------------------------------
-// Several-row K = 5120 launches on one workgroup of 16 waves per CU.
+// K = 5120 PRENORM launches on one workgroup per CU.
 //
-// With M rows staged the x buffer is M times the one-row one (65 KB at three
-// rows), so four-wave workgroups fit two per CU: two waves per SIMD, and the
-// MLP gate/up's 1088 workgroups run in three rounds with the normalizing
-// prologue repeated by each. Here one workgroup of 16 waves owns
-// LISA_QMV_WIDE_TILES = 17 tiles (the gate/up's 4352 tiles are 256 x 17):
-// waves 0..15 run one tile each exactly as the four-wave kernel does, and the
-// five group iterations of the 17th tile run one each on waves 0..4, which
-// store the per-group terms; after a barrier wave 15 adds them in iteration
-// order from 0 and finishes that tile. A tile's running sum is the sum of
-// its per-group terms in iteration order from 0 either way, so every output
-// is the bits of the four-wave kernel (and of the one-row step).
+// Four-wave workgroups own four 8-row tiles each and run the normalizing
+// prologue once per workgroup. With M rows staged the x buffer is M times the
+// one-row one (65 KB at three rows), so they fit two per CU: the MLP
+// gate/up's 1088 workgroups then run in three rounds, repeating the prologue
+// in each. qmv_wide gives a CU one workgroup of NW waves owning NW + XT
+// consecutive tiles and runs the prologue once over its 64 NW threads:
+// * the MLP gate/up (LISA_QMV_WIDE_TILES = 17 tiles, 4352 = 256 x 17): 16
+//   waves run one tile each exactly as the four-wave kernel does, and the five
+//   group iterations of the 17th tile (XT = 1) run one each on waves 0..4,
+//   which store the per-group terms; after a barrier wave 15 adds them in
+//   iteration order from 0 and finishes that tile. A tile's running sum is
+//   the sum of its per-group terms in iteration order from 0 either way;
+// * the GDN and attention in-projections (2048 = 256 x 8 and 1792 = 256 x 7
+//   tiles): 8 or 7 waves, one tile each (XT = 0), each tile's own epilogue
+//   (STORE or CONV), and the GDN gate contributions from workgroups 0..47.
+// Every output is the bits of the four-wave kernel (and of the one-row step).
 // ---------------------------------------------------------------------------
 
 template <int M>
 struct WideCfg {
   using C = QmvCfg<LISA_HIDDEN, M>;
-  static constexpr int NW = 16;
   static constexpr int XB = C::XBYTES + C::GBYTES;      // staged rows, then X_g
   static constexpr int RED = XB;                        // statistics: [M][4] partials, [M] factors
   static constexpr int SCR = RED + 64 * 4;              // chunk sums [M][640] / extra-tile terms
@@ -1113,28 +1123,38 @@ struct WideCfg {
   static_assert(5 * M <= 64, "statistics slots");
 };
 
-// PRENORM of M rows over 1024 threads: thread c < 640 holds chunk c of every
-// row. The per-thread sums of squares of the 256-thread prologue (chunks t,
-// t + 256, t + 512, added in that order) are formed by threads 0..255 from
-// the chunk sums the owners put in LDS, then tree64 and (W0 + W1) + (W2 + W3)
-// as there: the statistic, the staged x and X_g are the bits of prenorm_rows.
-template <int M>
-DEV void prenorm_wide(const LisaQmvParams& p, unsigned char* lds, const uint4 (&ha)[M], const uint4& hw) {
+// Chunks per thread of a prologue over NT threads.
+template <int NT>
+constexpr int kWideChunks = (kSegChunks + NT - 1) / NT;
+
+// PRENORM of M rows over NT >= 256 threads: thread t holds chunks t, t + NT,
+// .. (< 640) of every row. The per-thread sums of squares of the 256-thread
+// prologue (chunks t, t + 256, t + 512, added in that order) are formed by
+// threads 0..255 from the chunk sums the owners put in LDS, then tree64 and
+// (W0 + W1) + (W2 + W3) as there: the statistic, the staged x and X_g are the
+// bits of prenorm_rows.
+template <int M, int NT>
+DEV void prenorm_wide(const LisaQmvParams& p, unsigned char* lds, const uint4 (&ha)[kWideChunks<NT>][M],
+                      const uint4 (&hw)[kWideChunks<NT>]) {
   using W = WideCfg<M>;
   using C = QmvCfg<LISA_HIDDEN, M>;
+  constexpr int CH = kWideChunks<NT>;
+  static_assert(NT >= 256 && NT % 64 == 0, "prologue threads");
   const int tid = threadIdx.x, lane = tid & 63, wv = __builtin_amdgcn_readfirstlane(tid >> 6);
   float* gsum = reinterpret_cast<float*>(lds + C::XBYTES);
   float* red = reinterpret_cast<float*>(lds + W::RED);
   float* parts = reinterpret_cast<float*>(lds + W::SCR);
-  const int c = tid;
-  const bool valid = c < kSegChunks;
 #pragma unroll
-  for (int m = 0; m < M; ++m) {
-    float hv[8];
-    unpack_bf8(ha[m], hv);
-    const float part = ((hv[0] * hv[0] + hv[1] * hv[1]) + (hv[2] * hv[2] + hv[3] * hv[3])) +
-                       ((hv[4] * hv[4] + hv[5] * hv[5]) + (hv[6] * hv[6] + hv[7] * hv[7]));
-    if (valid) parts[m * kSegChunks + c] = part;
+  for (int i = 0; i < CH; ++i) {
+    const int c = tid + NT * i;
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+      float hv[8];
+      unpack_bf8(ha[i][m], hv);
+      const float part = ((hv[0] * hv[0] + hv[1] * hv[1]) + (hv[2] * hv[2] + hv[3] * hv[3])) +
+                         ((hv[4] * hv[4] + hv[5] * hv[5]) + (hv[6] * hv[6] + hv[7] * hv[7]));
+      if (c < kSegChunks) parts[m * kSegChunks + c] = part;
+    }
   }
   __syncthreads();
   if (wv < 4) {
@@ -1155,37 +1175,45 @@ DEV void prenorm_wide(const LisaQmvParams& p, unsigned char* lds, const uint4 (&
   }
   __syncthreads();
   const bool writer = blockIdx.x == 0;
-  float wf[8];
-  unpack_bf8(hw, wf);
 #pragma unroll
-  for (int m = 0; m < M; ++m) {
-    const float inv = red[4 * M + m];
-    float hv[8], f[8], x[8];
-    uint4 xb;
-    unpack_bf8(ha[m], hv);
+  for (int i = 0; i < CH; ++i) {
+    const int c = tid + NT * i;
+    const bool valid = c < kSegChunks;
+    float wf[8];
+    unpack_bf8(hw[i], wf);
 #pragma unroll
-    for (int e = 0; e < 8; ++e) f[e] = (hv[e] * inv) * wf[e];
-    round_bf8(f, x, xb);
-    if (valid) put_chunk<LISA_HIDDEN, M>(lds, m, 8 * c, x);
-    put_gsum<LISA_HIDDEN, M>(gsum, m, 8 * c, valid, x);
-    if (valid && writer) {
-      if (p.r_out) reinterpret_cast<uint4*>(p.r_out + (size_t)m * LISA_HIDDEN)[c] = ha[m];
-      if (p.x_out) reinterpret_cast<uint4*>(p.x_out + (size_t)m * LISA_HIDDEN)[c] = xb;
+    for (int m = 0; m < M; ++m) {
+      const float inv = red[4 * M + m];
+      float hv[8], f[8], x[8];
+      uint4 xb;
+      unpack_bf8(ha[i][m], hv);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) f[e] = (hv[e] * inv) * wf[e];
+      round_bf8(f, x, xb);
+      if (valid) put_chunk<LISA_HIDDEN, M>(lds, m, 8 * c, x);
+      put_gsum<LISA_HIDDEN, M>(gsum, m, 8 * c, valid, x);
+      if (valid && writer) {
+        if (p.r_out) reinterpret_cast<uint4*>(p.r_out + (size_t)m * LISA_HIDDEN)[c] = ha[i][m];
+        if (p.x_out) reinterpret_cast<uint4*>(p.x_out + (size_t)m * LISA_HIDDEN)[c] = xb;
+      }
     }
   }
   __syncthreads();
 }
 
-// The MLP gate/up (SwiGLU epilogue) of M rows; launch LISA_QMV_WIDE_THREADS
-// threads per workgroup and tiles / LISA_QMV_WIDE_TILES workgroups. EARLY of
-// the tile's group iterations are issued before the prologue, DEPTH are in
-// flight during the loop.
-template <int M, int EARLY = 1, int DEPTH = 2>
-DEV void qmv_wide_gateup(const LisaQmvParams& p, unsigned char* lds) {
-  constexpr int K = LISA_HIDDEN;
+// M rows, NW waves each owning one tile, XT (0 or 1) extra tile spread over
+// waves 0..4, epilogue EPI (-1: per tile kind; no ARGMAX). EARLY of a tile's
+// group iterations are issued before the prologue, DEPTH are in flight during
+// the loop. Launch 64 NW threads per workgroup and tiles / (NW + XT)
+// workgroups.
+template <int M, int NW, int XT, int EPI, int EARLY, int DEPTH>
+DEV void qmv_wide(const LisaQmvParams& p, unsigned char* lds) {
+  constexpr int K = LISA_HIDDEN, NT = 64 * NW, TPW = NW + XT, CH = kWideChunks<NT>;
   using C = QmvCfg<K, M>;
   using W = WideCfg<M>;
-  static_assert(LISA_QMV_WIDE_TILES == W::NW + 1 && C::IMAX <= W::NW - 1, "extra-tile layout");
+  static_assert(XT == 0 || (XT == 1 && NW == 16 && EPI == LISA_EPI_GATEUP && C::IMAX <= NW - 1), "extra-tile layout");
+  static_assert(EPI != LISA_EPI_ARGMAX, "no argmax partials");
+  static_assert(0 <= EARLY && EARLY <= DEPTH && DEPTH <= C::IMAX, "pipeline depths");
   const float* gsum = reinterpret_cast<const float*>(lds + C::XBYTES);
   float* xterm = reinterpret_cast<float*>(lds + W::SCR);  // [IMAX][64 lanes][2M]
 
@@ -1196,47 +1224,52 @@ DEV void qmv_wide_gateup(const LisaQmvParams& p, unsigned char* lds) {
     asm volatile("" : : "s"(kw[0]), "s"(kw[16]), "s"(kw[32]), "s"(kw[48]), "s"(kw[64]), "s"(kw[80]), "s"(kw[96]));
   }
   const uint32_t tiles = qmv_tiles(p);
-  const uint32_t base = blockIdx.x * LISA_QMV_WIDE_TILES;
-  const uint32_t tile = base + wv, xtile = base + W::NW;
+  const uint32_t base = blockIdx.x * TPW;
+  const uint32_t tile = base + wv, xtile = base + NW;
   const bool tile_ok = tile < tiles;
-  const bool xwave = wv < C::IMAX;  // runs iteration wv of the extra tile
+  const bool xwave = XT > 0 && wv < C::IMAX;  // runs iteration wv of the extra tile
 
-  uint4 ha[M], hw;
-  {
-    const int c = min(tid, kSegChunks - 1);
-    hw = reinterpret_cast<const uint4*>(p.norm_w)[c];
+  uint4 ha[CH][M], hw[CH];
 #pragma unroll
-    for (int m = 0; m < M; ++m) ha[m] = reinterpret_cast<const uint4*>(p.h_in + (size_t)m * LISA_HIDDEN)[c];
+  for (int i = 0; i < CH; ++i) {
+    const int c = min(tid + NT * i, kSegChunks - 1);
+    hw[i] = reinterpret_cast<const uint4*>(p.norm_w)[c];
+#pragma unroll
+    for (int m = 0; m < M; ++m) ha[i][m] = reinterpret_cast<const uint4*>(p.h_in + (size_t)m * LISA_HIDDEN)[c];
   }
   __builtin_amdgcn_sched_barrier(0);
   const TileRef tr = tile_ref<K>(p, tile_ok ? tile : tiles - 1, rp);
   Unit<C::IMAX> u;
   Unit<1> xu;
-  static_assert(0 <= EARLY && EARLY <= DEPTH && DEPTH <= C::IMAX, "pipeline depths");
   load_unit_off<K, C::IMAX>(u, tr, 0, C::ITER, li, 0, EARLY);
   if (xwave) {
     const TileRef xr = tile_ref<K>(p, xtile < tiles ? xtile : tiles - 1, rp);
     load_unit_off<K, 1>(xu, xr, wv, wv + 1, li, 0, 1);
   }
   __builtin_amdgcn_sched_barrier(0);
-  prenorm_wide<M>(p, lds, ha, hw);
+  prenorm_wide<M, NT>(p, lds, ha, hw);
   __builtin_amdgcn_sched_barrier(0);
   // waves 0..4 first run the extra tile's iteration wv (its weights were
-  // issued with the prologue's loads) and issue the tile's second iteration
+  // issued with the prologue's loads) and issue the tile's further iterations
   // after it, so the extra weights never sit beside two of the tile's
-  if (xwave) {
-    float X0[M], X1[M];
+  if constexpr (XT > 0) {
+    if (xwave) {
+      float X0[M], X1[M];
 #pragma unroll
-    for (int m = 0; m < M; ++m) { X0[m] = 0.0f; X1[m] = 0.0f; }
-    group_dot2<C::ROWBYTES, C::G, M>(lds, 16 * wv + li, xu.a0[0], xu.b0[0], xu.a1[0], xu.b1[0], xu.s0[0],
-                                     xu.s1[0], gsum, X0, X1);
-    float* dst = xterm + (wv * 64 + lane) * 2 * M;
+      for (int m = 0; m < M; ++m) { X0[m] = 0.0f; X1[m] = 0.0f; }
+      group_dot2<C::ROWBYTES, C::G, M>(lds, 16 * wv + li, xu.a0[0], xu.b0[0], xu.a1[0], xu.b1[0], xu.s0[0],
+                                       xu.s1[0], gsum, X0, X1);
+      float* dst = xterm + (wv * 64 + lane) * 2 * M;
 #pragma unroll
-    for (int m = 0; m < M; ++m) { dst[m] = X0[m]; dst[M + m] = X1[m]; }
+      for (int m = 0; m < M; ++m) { dst[m] = X0[m]; dst[M + m] = X1[m]; }
+    }
+    __builtin_amdgcn_sched_barrier(0);
   }
-  __builtin_amdgcn_sched_barrier(0);
   load_unit_off<K, C::IMAX>(u, tr, 0, C::ITER, li, EARLY, DEPTH);
   __builtin_amdgcn_sched_barrier(0);
+  // the epilogue's global inputs (GDN conv state and taps), behind the weights
+  EpiPre<M> pre;
+  if constexpr (EPI != LISA_EPI_GATEUP) epi_preload<M, EPI>(p, tr, li, pre);
 
   float T0[M], T1[M];
 #pragma unroll
@@ -1267,44 +1300,94 @@ DEV void qmv_wide_gateup(const LisaQmvParams& p, unsigned char* lds) {
   };
 #pragma unroll
   for (int m = 0; m < M; ++m) { T0[m] = tree16(T0[m]); T1[m] = tree16(T1[m]); }
-  if (tile_ok) gateup_store(tr, T0, T1, li);
-  __syncthreads();
-  if (wv == W::NW - 1 && xtile < tiles) {
-    // lane indices formed again here, not carried across the loop
-    int fl = (int)threadIdx.x;
-    asm volatile("" : "+v"(fl));
-    fl &= 63;
-    const TileRef xr = tile_ref<K>(p, xtile, fl >> 4);
-    float A[M], B[M];
+  if (tile_ok) {
+    if constexpr (EPI == LISA_EPI_GATEUP) {
+      gateup_store(tr, T0, T1, li);
+    } else {
+      float best_v[M];
+      uint32_t best_i[M];
 #pragma unroll
-    for (int m = 0; m < M; ++m) { A[m] = 0.0f; B[m] = 0.0f; }
-#pragma unroll
-    for (int i = 0; i < C::IMAX; ++i) {
-      const float* src = xterm + (i * 64 + fl) * 2 * M;
-#pragma unroll
-      for (int m = 0; m < M; ++m) { A[m] = A[m] + src[m]; B[m] = B[m] + src[M + m]; }
+      for (int m = 0; m < M; ++m) { best_v[m] = -INFINITY; best_i[m] = 0xffffffffu; }
+      qmv_epilogue<M, EPI>(p, tr, li, pre, T0, T1, best_v, best_i);
     }
+  }
+  if constexpr (XT > 0) {
+    __syncthreads();
+    if (wv == NW - 1 && xtile < tiles) {
+      // lane indices formed again here, not carried across the loop
+      int fl = (int)threadIdx.x;
+      asm volatile("" : "+v"(fl));
+      fl &= 63;
+      const TileRef xr = tile_ref<K>(p, xtile, fl >> 4);
+      float A[M], B[M];
 #pragma unroll
-    for (int m = 0; m < M; ++m) { A[m] = tree16(A[m]); B[m] = tree16(B[m]); }
-    gateup_store(xr, A, B, fl & 15);
+      for (int m = 0; m < M; ++m) { A[m] = 0.0f; B[m] = 0.0f; }
+#pragma unroll
+      for (int i = 0; i < C::IMAX; ++i) {
+        const float* src = xterm + (i * 64 + fl) * 2 * M;
+#pragma unroll
+        for (int m = 0; m < M; ++m) { A[m] = A[m] + src[m]; B[m] = B[m] + src[M + m]; }
+      }
+#pragma unroll
+      for (int m = 0; m < M; ++m) { A[m] = tree16(A[m]); B[m] = tree16(B[m]); }
+      gateup_store(xr, A, B, fl & 15);
+    }
+  }
+  // GDN in-projection: workgroup w < 48 forms the per-group contributions of
+  // rows w of the a and b matrices against the staged x, as the four-wave
+  // kernel does
+  if constexpr (EPI != LISA_EPI_GATEUP) {
+    if (p.gate_ab != nullptr && blockIdx.x < LISA_GDN_VH && tid < C::G) {
+      const uint32_t hh = blockIdx.x;
+      const uint4* aw = reinterpret_cast<const uint4*>(p.gate_a_w + (size_t)hh * (K / 8));
+      const uint4* bw = reinterpret_cast<const uint4*>(p.gate_b_w + (size_t)hh * (K / 8));
+      const uint4 a0 = aw[2 * tid], b0 = aw[2 * tid + 1], a1 = bw[2 * tid], b1 = bw[2 * tid + 1];
+      const uint32_t s0 = p.gate_a_sb[(size_t)hh * C::G + tid], s1 = p.gate_b_sb[(size_t)hh * C::G + tid];
+      float G0[M], G1[M];
+#pragma unroll
+      for (int m = 0; m < M; ++m) { G0[m] = 0.0f; G1[m] = 0.0f; }
+      group_dot2<C::ROWBYTES, C::G, M>(lds, tid, a0, b0, a1, b1, s0, s1, gsum, G0, G1);
+#pragma unroll
+      for (int m = 0; m < M; ++m) {
+        float* dst = p.gate_ab + ((size_t)m * LISA_GDN_VH + hh) * LISA_GDN_GATE_FLOATS + 12 * (tid & 15) + (tid >> 4);
+        dst[0] = G0[m];
+        dst[5] = G1[m];
+      }
+    }
   }
 }
 
+// The MLP gate/up. Three rows are VALU-bound: no weights ahead of the
+// prologue, so its residual loads are not queued behind the weight stream and
+// the dot products start earlier (35.2 -> 31.0 us); one row is memory-bound
+// and keeps a one-iteration head start (without it 20.7 -> 22.1 us).
 extern "C" __global__ __launch_bounds__(LISA_QMV_WIDE_THREADS) void lisa_qmv_k5120_m3_prenorm_gateup_wide(
     LisaQmvParams p) {
   __shared__ __attribute__((aligned(16))) unsigned char lds[WideCfg<3>::BYTES];
-  // three rows are VALU-bound: no weights ahead of the prologue, so its
-  // residual loads are not queued behind the weight stream and the dot
-  // products start earlier (35.2 -> 31.0 us; at one row the same order is
-  // slower, 20.7 -> 22.1 us, and so is it for the four-wave M=3 launches,
-  // whose 256-thread prologue is bound by its own arithmetic)
-  qmv_wide_gateup<3, 0, 2>(p, lds);
+  qmv_wide<3, 16, 1, LISA_EPI_GATEUP, 0, 2>(p, lds);
 }
 extern "C" __global__ __launch_bounds__(LISA_QMV_WIDE_THREADS) void lisa_qmv_k5120_m1_prenorm_gateup_wide(
     LisaQmvParams p) {
   __shared__ __attribute__((aligned(16))) unsigned char lds[WideCfg<1>::BYTES];
-  qmv_wide_gateup<1>(p, lds);
+  qmv_wide<1, 16, 1, LISA_EPI_GATEUP, 1, 2>(p, lds);
 }
+
+// The GDN and attention in-projections (STORE and CONV matrices, GDN gate
+// contributions): NW = 8 or 7 waves, one tile each, with a one-iteration
+// weight head start. Three rows: 20.9 -> 19.4 us (GDN) and 17.3 -> 15.9 us
+// (attention) against the four-wave kernel; one row: level (10.8 -> 10.7,
+// 9.4 -> 9.2 us). Without the head start three rows gain less (20.5, 17.5 us)
+// and one row loses (11.8, 10.4 us).
+#define LISA_QMV_INPROJ_WIDE(M, NW)                                                                            \
+  extern "C" __global__ __launch_bounds__(64 * NW) void lisa_qmv_k5120_m##M##_prenorm_wide##NW(LisaQmvParams p) { \
+    __shared__ __attribute__((aligned(16))) unsigned char lds[WideCfg<M>::BYTES];                                \
+    qmv_wide<M, NW, 0, -1, 1, 2>(p, lds);                                                                          \
+  }
+LISA_QMV_INPROJ_WIDE(1, 7)
+LISA_QMV_INPROJ_WIDE(1, 8)
+LISA_QMV_INPROJ_WIDE(3, 7)
+LISA_QMV_INPROJ_WIDE(3, 8)
+#undef LISA_QMV_INPROJ_WIDE
 
 // ===========================================================================
 // GDN recurrence (gdn.metal:245-328) + gates (gdn.metal:170-205) + gated

@@ -69,8 +69,9 @@ def launch_qmv(pkg, dev, K, M, params, mats, wide=True):
     """Restates launch_qmv of lisa-rs_amd/csrc/runner.cpp. mats: list of
     (DevQ4, DevQ4-or-None, out_ptr, kind). One 8-row tile per wave (K = 5120,
     four tiles per workgroup) or per workgroup with the group iterations split
-    over its four waves (every other K); the MLP gate/up alone under PRENORM
-    runs on the 16-wave kernel unless wide=False."""
+    over its four waves (every other K); unless wide=False, the MLP gate/up
+    alone under PRENORM runs on the 16-wave kernel, and a PRENORM launch of
+    STORE/CONV matrices of 256 x 7 or 256 x 8 tiles on the 7- or 8-wave one."""
     tiles = 0
     for e, (q, q2, out, kind) in enumerate(mats):
         m = params.mats[e]
@@ -98,5 +99,11 @@ def launch_qmv(pkg, dev, K, M, params, mats, wide=True):
         grid = max(1, (tiles + pkg.QMV_WIDE_TILES - 1) // pkg.QMV_WIDE_TILES)
         dev.dispatch(name + "_wide", params, (grid,), (pkg.QMV_WIDE_THREADS,))
         return params.ksplit, grid
+    nw = tiles // pkg.QMV_WIDE_GROUPS
+    if (wide and K == 5120 and params.pro_mode == pkg.PRO_PRENORM and kinds <= {pkg.EPI_STORE, pkg.EPI_CONV}
+            and not params.am_val and tiles % pkg.QMV_WIDE_GROUPS == 0 and nw in (7, 8)):
+        # the runner's in-projection launch: one tile per wave, one workgroup per CU
+        dev.dispatch(f"{name}_wide{nw}", params, (pkg.QMV_WIDE_GROUPS,), (64 * nw,))
+        return params.ksplit, pkg.QMV_WIDE_GROUPS
     dev.dispatch(name, params, (grid,), (256,))
     return params.ksplit, grid

@@ -45,7 +45,8 @@ def test_no_kernel_spills_to_scratch():
     meta = kernel_metadata()
     for k in ("lisa_q4_gemm", "lisa_q4_gemm_wide", "lisa_qmv_k5120_m1_prenorm_gateup", "lisa_qmv_k17408_m1_x",
               "lisa_gdn_recurrence_m1", "lisa_attn_partial_m1", "lisa_qmv_k5120_m1_prenorm_gateup_wide",
-              "lisa_qmv_k5120_m3_prenorm_gateup_wide"):
+              "lisa_qmv_k5120_m3_prenorm_gateup_wide", "lisa_qmv_k5120_m1_prenorm_wide7",
+              "lisa_qmv_k5120_m1_prenorm_wide8", "lisa_qmv_k5120_m3_prenorm_wide7", "lisa_qmv_k5120_m3_prenorm_wide8"):
         assert k in meta
     spilled = {k: v for k, v in meta.items() if v}
     assert not spilled, spilled
@@ -60,10 +61,13 @@ def test_python_launch_sizes_match_the_kernels():
     for m in (1, 3):
         assert wg[f"lisa_attn_partial_m{m}"] == pkg.ATT_PARTIAL_THREADS[m]
         assert wg[f"lisa_qmv_k5120_m{m}_prenorm_gateup_wide"] == pkg.QMV_WIDE_THREADS
+        for nw in (7, 8):
+            assert wg[f"lisa_qmv_k5120_m{m}_prenorm_wide{nw}"] == 64 * nw
     assert wg["lisa_q4_gemm_wide"] == pkg.GEMM_THREADS_WIDE
     hdr = (Path(pkg.PKG_DIR).parent / "include" / "lisa_kernels.h").read_text()
     assert int(re.search(r"#define LISA_QMV_WIDE_TILES (\d+)", hdr).group(1)) == pkg.QMV_WIDE_TILES
     assert int(re.search(r"#define LISA_QMV_WIDE_THREADS (\d+)", hdr).group(1)) == pkg.QMV_WIDE_THREADS
+    assert int(re.search(r"#define LISA_QMV_WIDE_GROUPS (\d+)", hdr).group(1)) == pkg.QMV_WIDE_GROUPS
 
 
 STRUCTS = {  # Python mirror -> C typedef (include/lisa_kernels.h, include/lisa_hip.h)
@@ -103,3 +107,57 @@ def test_python_structs_match_the_headers(tmp_path):
         key, val = line.rsplit(" ", 1)
         got[key] = int(val)
     assert got == want
+
+
+ENUMS = {"PRO_": "LISA_PRO_", "EPI_": "LISA_EPI_", "FILL_": "LISA_FILL_"}
+
+
+def test_python_enums_match_the_headers(tmp_path):
+    """The package's prologue, epilogue and fill-kind constants equal the C
+    enums (a fill kind off by one writes 4-byte elements into a buffer sized
+    for 2-byte ones)."""
+    pkg = load_pkg()
+    inc = Path(pkg.PKG_DIR).parent / "include"
+    lines = ['#include <cstdio>', '#include "lisa_kernels.h"', '#include "lisa_synth.h"', "int main() {"]
+    want = {}
+    for py, c in ENUMS.items():
+        for name in dir(pkg):
+            if name.startswith(py) and isinstance(getattr(pkg, name), int):
+                lines.append(f'  std::printf("{name} %d\\n", (int){c}{name[len(py):]});')
+                want[name] = getattr(pkg, name)
+    for name in ("DIST_BITS", "DIST_UNIFORM", "DIST_NORMAL"):
+        lines.append(f'  std::printf("{name} %d\\n", (int)LISA_{name});')
+        want[name] = getattr(pkg, name)
+    lines += ["  return 0;", "}"]
+    src, exe = tmp_path / "enums.cpp", tmp_path / "enums"
+    src.write_text("\n".join(lines) + "\n")
+    subprocess.run(["g++", "-std=c++17", f"-I{inc}", str(src), "-o", str(exe)], check=True, capture_output=True)
+    got = {}
+    for line in subprocess.run([str(exe)], check=True, capture_output=True, text=True).stdout.splitlines():
+        key, val = line.rsplit(" ", 1)
+        got[key] = int(val)
+    assert len(want) >= 20 and got == want
+
+
+def test_synth_fill_refuses_overruns():
+    """Device.synth_fill checks the element count against the buffer on the
+    host before any dispatch."""
+    pkg = load_pkg()
+
+    class Dev:  # the check runs before self.dispatch
+        dispatch = None
+
+    class Buf:
+        nbytes, ptr = 1024, 0
+
+    fill = pkg.Device.synth_fill
+    with pytest.raises(ValueError):
+        fill(Dev(), Buf(), 512, pkg.FILL_SB, 1)  # 2048 bytes
+    with pytest.raises(ValueError):
+        fill(Dev(), Buf(), 513, pkg.FILL_BF16, 1)
+    with pytest.raises(ValueError):
+        fill(Dev(), Buf(), 4 * 256, pkg.FILL_KV, 1, capacity=1, filled=1)  # 2048 bytes
+    with pytest.raises(ValueError):
+        fill(Dev(), Buf(), 4 * 256, pkg.FILL_KV, 1, capacity=0, filled=1)
+    with pytest.raises(ValueError):
+        fill(Dev(), Buf(), 4, 7, 1)

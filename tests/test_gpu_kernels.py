@@ -229,6 +229,71 @@ def test_qmv_wide_gateup_equals_four_wave(pkg, orc, dev, M, N):
         assert np.array_equal(runs[0][0], orc.silu_mul(g, u))
 
 
+@pytest.mark.parametrize("M", [1, 3])
+@pytest.mark.parametrize("layer", ["gdn", "attn"])
+def test_qmv_wide_inproj_equals_four_wave(pkg, orc, dev, M, layer):
+    """The in-projection launches under PRENORM on one workgroup per CU, one
+    tile per wave: GDN (qkv 10240 CONV + z 6144 rows = 2048 tiles = 256 x 8
+    waves, with the a/b gate contributions) and attention (q 12288 + k 1024 +
+    v 1024 = 1792 tiles = 256 x 7). Every output (projections, conv state and
+    history slots, gate contributions) equals the four-wave kernel's bit for
+    bit, and the projections and causal conv equal the oracle's
+    (x = RMSNorm(h), gdn.metal:163-170)."""
+    rng = np.random.default_rng(300 + M + (0 if layer == "gdn" else 7))
+    K = 5120
+    shapes = ([("qkv", 10240, pkg.EPI_CONV), ("z", 6144, pkg.EPI_STORE)] if layer == "gdn" else
+              [("q", 12288, pkg.EPI_STORE), ("k", 1024, pkg.EPI_STORE), ("v", 1024, pkg.EPI_STORE)])
+    mats = {n: rand_q4(rng, rows, K) for n, rows, _ in shapes}
+    qd = {n: DevQ4(dev, *mats[n]) for n in mats}
+    h = bf16((rng.standard_normal((M, K)) * 4).astype(np.float32))
+    nw = bf16(rng.uniform(0.9, 1.1, K).astype(np.float32))
+    hb, nb = dev.upload(h), dev.upload(nw)
+    if layer == "gdn":
+        gate = [DevQ4(dev, *rand_q4(rng, 48, K)) for _ in range(2)]
+        conv_w = bf16(rng.uniform(-0.5, 0.5, 10240 * 4).astype(np.float32))
+        conv_state = bf16(rng.standard_normal(3 * 10240).astype(np.float32))
+        cwb = dev.upload(conv_w)
+    runs = []
+    for wide in (True, False):
+        outs = {n: dev.buffer(M * rows * 4) for n, rows, _ in shapes}
+        p = pkg.QmvParams()
+        p.pro_mode = pkg.PRO_PRENORM
+        p.h_in, p.norm_w = hb.ptr, nb.ptr
+        if layer == "gdn":
+            csb, cslot = dev.upload(conv_state), dev.upload(np.zeros(2 * 3 * 10240, np.uint16))
+            gab = dev.upload(np.zeros(M * 48 * 192, np.float32))
+            p.conv_w, p.conv_state, p.conv_slots, p.conv_slot_stride = cwb.ptr, csb.ptr, cslot.ptr, 3 * 10240
+            p.capture = 1 if M == 3 else 0
+            p.gate_a_w, p.gate_a_sb = gate[0].wbuf.ptr, gate[0].sbbuf.ptr
+            p.gate_b_w, p.gate_b_sb = gate[1].wbuf.ptr, gate[1].sbbuf.ptr
+            p.gate_ab = gab.ptr
+        _, grid = launch_qmv(pkg, dev, K, M, p, [(qd[n], None, outs[n].ptr, kind) for n, _, kind in shapes], wide=wide)
+        run = {n: outs[n].read(np.float32, M * rows).reshape(M, rows) for n, rows, _ in shapes}
+        if layer == "gdn":
+            run["conv_state"] = csb.read(np.uint16, 3 * 10240)
+            run["conv_slots"] = cslot.read(np.uint16, 2 * 3 * 10240)
+            run["gate_ab"] = gab.read(np.uint32, M * 48 * 192)
+        runs.append((grid, run))
+    tiles = sum(rows // 8 for _, rows, _ in shapes)
+    assert runs[0][0] == pkg.QMV_WIDE_GROUPS and tiles == pkg.QMV_WIDE_GROUPS * (8 if layer == "gdn" else 7)
+    assert runs[1][0] == tiles // 4
+    for key, got in runs[0][1].items():
+        assert np.array_equal(got.view(np.uint32) if got.dtype == np.float32 else got,
+                              runs[1][1][key].view(np.uint32) if got.dtype == np.float32 else runs[1][1][key]), key
+    wide = runs[0][1]
+    x = np.stack([orc.rms_norm_tiles(h[m], nw) for m in range(M)])
+    for n, rows, kind in shapes:
+        y = orc.q4_linear(x, *mats[n], rows, K, M, 1)
+        if kind == pkg.EPI_CONV:
+            conv_out, cs_want, cslots = orc.gdn_conv(y, conv_w, conv_state, M, slots=True)
+            assert same_bits(wide[n], conv_out)
+            assert np.array_equal(wide["conv_state"], cs_want)
+            if M == 3:
+                assert np.array_equal(wide["conv_slots"], cslots[:2 * 3 * 10240])
+        else:
+            assert same_bits(wide[n], y), n
+
+
 # ---------------------------------------------------------------- config 1
 @pytest.mark.parametrize("M", [1, 3])
 def test_gdn_layer_config1(pkg, orc, dev, M):
