@@ -1882,13 +1882,200 @@ DEV void slice_pv3(const float* pb3, const uint16_t* Vt, int n, int dp, float (&
 // rows' raw key and value, and then every K and V row of the slice, clamped
 // below the capacity, before the position is known. The queries are normalized
 // and rotated, and the appended rows written, while the slice is in flight.
-// Scores: one wave per pair of heads; P.V: thread (dp, hg) = (tid % 128,
-// tid / 128) owns dimensions 2dp, 2dp+1 of heads 3hg..3hg+2.
-// NT threads: 256 for one row, 512 for three (the three rows' score items
-// and P.V groups then take two passes, not three).
+// The slice's q.k runs on 12 M items (row, head pair, class d mod 4), one per
+// wave: each is one of the four accumulators of attention.metal:550-604's dot
+// (an ascending fma chain over d = r, r + 4, ..), read from K and q stored
+// class-major in LDS (element d of a row at (d & 3) 64 + (d >> 2), rows padded
+// to 264 entries); after a barrier, one wave per (row, head pair) forms
+// ((a0 + a1) + (a2 + a3)) / 16 and the slice softmax statistics. P.V: thread
+// (d, item) owns dimension d of three heads, chains over the tokens in order.
+// One row: spreading q.k over twelve waves instead of three, 59.2 -> 55.4 us
+// at ctx 32768 and 16.1 -> 15.9 us at ctx 4096 (partial + merge). Three rows
+// keep attn_partial_pairs below (one wave per row and head pair, all four
+// accumulators; 387 against 408 us per verify).
 typedef uint32_t lisa_u32x4 __attribute__((ext_vector_type(4)));
-template <int M, int NT = 256>
+template <int M, int NT>
 DEV void attn_partial_body(const LisaAttnParams& p) {
+  constexpr int T = LISA_ATT_SLICE, HD = LISA_ATT_HD, KP = HD + 8, NW = NT / 64;
+  const int s = blockIdx.x, kvh = blockIdx.y;
+  const uint32_t t0 = (uint32_t)s * T;
+  __shared__ __attribute__((aligned(16))) uint16_t Kc[T * KP];
+  __shared__ __attribute__((aligned(16))) uint16_t Vt[T * HD];
+  __shared__ __attribute__((aligned(16))) float qc[M * 6 * HD];
+  __shared__ __attribute__((aligned(16))) float pb[M * 6 * T];
+  __shared__ __attribute__((aligned(16))) float sc[M * 6 * 4 * T];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const size_t cache_base = (size_t)kvh * p.capacity * HD;
+  const uint32_t pos_v = vload_u32(p.pos);
+  constexpr int QP = (6 * M + NW - 1) / NW;
+  float qraw[QP][4], qw[QP][4];
+#pragma unroll
+  for (int j = 0; j < QP; ++j) {
+    const int pr = min(wave + NW * j, 6 * M - 1), t = pr / 6, i = pr % 6;
+    hnr_load(p.q_proj + (size_t)t * LISA_ATT_Q_OUT + (kvh * 6 + i) * 512, p.q_norm_w, lane, qraw[j], qw[j]);
+  }
+  float inv_freq = 0.0f;
+#pragma unroll
+  for (int j = 0; j < LISA_ROPE_PAIRS; ++j) inv_freq = (lane & 31) == j ? kRopeInvFreq[j] : inv_freq;
+  const int wr = min(wave, M - 1);
+  float nkraw[4], nkw[4], nvraw[4];
+  hnr_load(p.k_raw + (size_t)wr * LISA_ATT_KV_OUT + kvh * HD, p.k_norm_w, lane, nkraw, nkw);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) nvraw[j] = p.v_raw[(size_t)wr * LISA_ATT_KV_OUT + kvh * HD + lane + 64 * j];
+  __builtin_amdgcn_sched_barrier(0);
+  constexpr int R = T * (HD / 8) / NT;
+  lisa_u32x4 kr[R], vr[R];
+#pragma unroll
+  for (int i = 0; i < R; ++i) {
+    const int c = tid + NT * i, row = c / (HD / 8), col = (c % (HD / 8)) * 8;
+    const size_t off = cache_base + (size_t)min(t0 + row, p.capacity - 1) * HD + col;
+    kr[i] = *reinterpret_cast<const lisa_u32x4*>(p.key_cache + off);
+    vr[i] = *reinterpret_cast<const lisa_u32x4*>(p.value_cache + off);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  const uint32_t base = __builtin_amdgcn_readfirstlane(pos_v);
+  if (t0 >= base + M) return;
+  float rs[M], rc[M];
+#pragma unroll
+  for (int t = 0; t < M; ++t) rope_sincos_f(base + t, inv_freq, rs[t], rc[t]);
+  // queries, class-major: element d of head (t, i) at qc[(t 6 + i) 256 + (d & 3) 64 + (d >> 2)]
+#pragma unroll
+  for (int j = 0; j < QP; ++j) {
+    const int pr = wave + NW * j;
+    if (pr >= 6 * M) break;
+    const int t = pr / 6, i = pr % 6;
+    float qo[4];
+    hnr_finish(qraw[j], qw[j], rs[t], rc[t], lane, qo);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) qc[(t * 6 + i) * HD + (lane & 3) * 64 + (lane >> 2) + 16 * e] = qo[e];
+  }
+  if (wave < M) {
+    const uint32_t pos = base + wave;
+    if (pos >= t0 && pos < t0 + T && pos < p.capacity) {
+      float kn[4];
+      hnr_finish(nkraw, nkw, rs[wave], rc[wave], lane, kn);
+      const int row = (int)(pos - t0);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int d = lane + 64 * j;
+        const uint16_t kb = lisa_f32_to_bf16(kn[j]);
+        const uint16_t vb = lisa_f32_to_bf16(nvraw[j]);
+        Kc[row * KP + (lane & 3) * 64 + (lane >> 2) + 16 * j] = kb;
+        Vt[row * HD + d] = vb;
+        p.key_cache[cache_base + (size_t)pos * HD + d] = kb;
+        p.value_cache[cache_base + (size_t)pos * HD + d] = vb;
+      }
+    }
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  // K class-major: the chunk's elements col + e and col + e + 4 (class e) are
+  // entries 2 (c % 32), 2 (c % 32) + 1 of class e of the row
+#pragma unroll
+  for (int i = 0; i < R; ++i) {
+    const int c = tid + NT * i, row = c / (HD / 8), cc = c % (HD / 8), col = cc * 8;
+    if (t0 + row < base) {
+      const lisa_u32x4 k = kr[i];
+      uint32_t* kd = reinterpret_cast<uint32_t*>(&Kc[row * KP + 2 * cc]);
+      kd[0] = (k.x & 0xffffu) | (k.z << 16);
+      kd[32] = (k.x >> 16) | (k.z & 0xffff0000u);
+      kd[64] = (k.y & 0xffffu) | (k.w << 16);
+      kd[96] = (k.y >> 16) | (k.w & 0xffff0000u);
+      *reinterpret_cast<lisa_u32x4*>(&Vt[row * HD + col]) = vr[i];
+    }
+  }
+  __syncthreads();
+  // 5a. item (row t, head pair, class r): lane = token, the class-r accumulator
+  // of heads 2 pair and 2 pair + 1 (an ascending fma chain over d = r, r + 4, ..)
+  for (int it = wave; it < 12 * M; it += NW) {
+    const int t = it / 12, pr = (it % 12) >> 2, r = it & 3, i = 2 * pr;
+    const uint32_t ctx = base + t + 1;
+    if (ctx <= t0) continue;
+    const int n = (int)min((uint32_t)T, ctx - t0);
+    if (lane < n) {
+      const uint16_t* kk = Kc + lane * KP + r * 64;
+      const float* qa = qc + (t * 6 + i) * HD + r * 64;
+      const float* qb = qa + HD;
+      float a = 0.0f, b = 0.0f;
+#pragma unroll 2
+      for (int j = 0; j < 64; j += 8) {
+        const uint4 k8 = *reinterpret_cast<const uint4*>(kk + j);
+        const float4 xa = *reinterpret_cast<const float4*>(qa + j), ya = *reinterpret_cast<const float4*>(qa + j + 4);
+        const float4 xb = *reinterpret_cast<const float4*>(qb + j), yb = *reinterpret_cast<const float4*>(qb + j + 4);
+        const float k0 = lo_bf(k8.x), k1 = hi_bf(k8.x), k2 = lo_bf(k8.y), k3 = hi_bf(k8.y);
+        const float k4 = lo_bf(k8.z), k5 = hi_bf(k8.z), k6 = lo_bf(k8.w), k7 = hi_bf(k8.w);
+        a = lisa_fma(xa.x, k0, a); b = lisa_fma(xb.x, k0, b);
+        a = lisa_fma(xa.y, k1, a); b = lisa_fma(xb.y, k1, b);
+        a = lisa_fma(xa.z, k2, a); b = lisa_fma(xb.z, k2, b);
+        a = lisa_fma(xa.w, k3, a); b = lisa_fma(xb.w, k3, b);
+        a = lisa_fma(ya.x, k4, a); b = lisa_fma(yb.x, k4, b);
+        a = lisa_fma(ya.y, k5, a); b = lisa_fma(yb.y, k5, b);
+        a = lisa_fma(ya.z, k6, a); b = lisa_fma(yb.z, k6, b);
+        a = lisa_fma(ya.w, k7, a); b = lisa_fma(yb.w, k7, b);
+      }
+      sc[((t * 6 + i) * 4 + r) * T + lane] = a;
+      sc[((t * 6 + i + 1) * 4 + r) * T + lane] = b;
+    }
+  }
+  __syncthreads();
+  // 5b. item (row t, head pair): scores ((a0 + a1) + (a2 + a3)) / 16 and the
+  // slice softmax statistics, as slice_scores2
+  for (int it = wave; it < 3 * M; it += NW) {
+    const int t = it / 3, i = 2 * (it % 3), h = kvh * 6 + i;
+    const uint32_t ctx = base + t + 1;
+    if (ctx <= t0) continue;
+    const int n = (int)min((uint32_t)T, ctx - t0);
+    float sa = -INFINITY, sb = -INFINITY;
+    if (lane < n) {
+      const float* ca = sc + (t * 6 + i) * 4 * T + lane;
+      const float* cb = ca + 4 * T;
+      sa = ((ca[0] + ca[T]) + (ca[2 * T] + ca[3 * T])) * 0.0625f;
+      sb = ((cb[0] + cb[T]) + (cb[2 * T] + cb[3 * T])) * 0.0625f;
+    }
+    const float ma = max64(sa), mb = max64(sb);
+    const float pa = (lane < n) ? lisa_exp2f(1.4426950408889634f * (sa - ma)) : 0.0f;
+    const float pbv = (lane < n) ? lisa_exp2f(1.4426950408889634f * (sb - mb)) : 0.0f;
+    const float da = tree64(pa), db = tree64(pbv);
+    pb[(t * 6 + i) * T + lane] = pa;
+    pb[(t * 6 + i + 1) * T + lane] = pbv;
+    if (lane == 0) {
+      float* ml = p.part_ml + (((size_t)t * LISA_ATT_QH + h) * p.s_max + s) * 2;
+      ml[0] = ma;
+      ml[1] = da;
+      ml[(size_t)p.s_max * 2] = mb;
+      ml[(size_t)p.s_max * 2 + 1] = db;
+    }
+  }
+  __syncthreads();
+  // 6. P.V: thread (d, item) = (tid % 256, tid / 256): dimension d of heads
+  // 3 hg .. 3 hg + 2 of row t (item = 2 t + hg), chains over the tokens in order
+  const int d = tid & 255;
+  for (int item = tid >> 8; item < 2 * M; item += NT / 256) {
+    const int t = item >> 1, hg = item & 1;
+    const uint32_t ctx = base + t + 1;
+    if (ctx <= t0) continue;
+    const int n = (int)min((uint32_t)T, ctx - t0);
+    const float* p3 = pb + (t * 6 + 3 * hg) * T;
+    float acc0 = 0.0f, acc1 = 0.0f, acc2 = 0.0f;
+#pragma unroll 4
+    for (int tok = 0; tok < n; ++tok) {
+      const float v = bf2f(Vt[tok * HD + d]);
+      acc0 = lisa_fma(p3[tok], v, acc0);
+      acc1 = lisa_fma(p3[T + tok], v, acc1);
+      acc2 = lisa_fma(p3[2 * T + tok], v, acc2);
+    }
+    float* po = p.part_o + (((size_t)t * LISA_ATT_QH + kvh * 6 + 3 * hg) * p.s_max + s) * HD + d;
+    po[0] = acc0;
+    po[(size_t)p.s_max * HD] = acc1;
+    po[(size_t)2 * p.s_max * HD] = acc2;
+  }
+}
+
+// Three rows: the same stages with q.k as one item per (row, head pair), lane =
+// token, all four accumulators in one lane (slice_scores2), and P.V thread
+// (dp, hg) = (tid % 128, tid / 128) owning dimensions 2dp, 2dp+1 of heads
+// 3hg..3hg+2 (slice_pv3); K and q row-major in LDS.
+template <int M, int NT>
+DEV void attn_partial_pairs(const LisaAttnParams& p) {
   constexpr int T = LISA_ATT_SLICE, HD = LISA_ATT_HD, KP = HD + 8, NW = NT / 64;
   const int s = blockIdx.x, kvh = blockIdx.y;
   const uint32_t t0 = (uint32_t)s * T;
@@ -2065,7 +2252,7 @@ extern "C" __global__ __launch_bounds__(LISA_ATT_PARTIAL_THREADS(1)) void lisa_a
   attn_partial_body<1, LISA_ATT_PARTIAL_THREADS(1)>(p);
 }
 extern "C" __global__ __launch_bounds__(LISA_ATT_PARTIAL_THREADS(3)) void lisa_attn_partial_m3(LisaAttnParams p) {
-  attn_partial_body<3, LISA_ATT_PARTIAL_THREADS(3)>(p);
+  attn_partial_pairs<3, LISA_ATT_PARTIAL_THREADS(3)>(p);
 }
 extern "C" __global__ __launch_bounds__(256) void lisa_attn_merge_m1(LisaAttnParams p) { attn_merge_body<1>(p); }
 extern "C" __global__ __launch_bounds__(256) void lisa_attn_merge_m3(LisaAttnParams p) { attn_merge_body<3>(p); }
