@@ -459,7 +459,7 @@ def attention_case(pkg, orc, dev, M, ctx, seed):
     return got, want, bufs["kc"].read(np.uint16, 4 * cap * 256), kc_w, bufs["vc"].read(np.uint16, 4 * cap * 256), vc_w
 
 
-@pytest.mark.parametrize("M,ctx", [(1, 4096), (3, 4096), (1, 1), (3, 3), (1, 65), (3, 130), (1, 32768)])
+@pytest.mark.parametrize("M,ctx", [(1, 4096), (3, 4096), (1, 1), (3, 3), (1, 65), (1, 100), (3, 130), (1, 32768)])
 def test_attention_config2(pkg, orc, dev, M, ctx):
     """Gated GQA decode attention: q/k RMSNorm + partial RoPE, KV append,
     split-K over 64-token slices, flash merge, sigmoid output gate; exact
