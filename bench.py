@@ -167,8 +167,11 @@ def kernel_configs(pkg, copies=8, reps=40):
         m.w, m.sb, m.out, m.rows, m.kind = ws[c].ptr, sbs[c].ptr, y.ptr, N, pkg.EPI_STORE
         p.tile_start[0], p.tile_start[1], p.n_mats, p.ksplit = 0, tiles, 1, 1
         params.append(p)
-    us = timed(pkg, dev, lambda i: dev.dispatch("lisa_qmv_k5120_m1_x", params[i % copies], ((tiles + 3) // 4,),
-                                                (256,), wait=False), reps)
+    # the runner's launch for a one-row plain-x projection of 2176 tiles: one
+    # nine-wave workgroup per CU (lisa_qmv_k5120_m1_x_wide9)
+    xw = pkg.QMV_X_WIDE_WAVES
+    us = timed(pkg, dev, lambda i: dev.dispatch("lisa_qmv_k5120_m1_x_wide9", params[i % copies],
+                                                ((tiles + xw - 1) // xw,), (64 * xw,), wait=False), reps)
     qbytes = N * K * 0.5625 + K * 2 + N * 4
     out["config0_qmv"] = {"shape": "M=1 K=5120 N=17408", "us": round(us, 2), "bytes": int(qbytes),
                           "gbps": round(qbytes / us / 1e3, 1), "frac": round(qbytes / us / 1e3 / HBM_PEAK_GBS, 4)}

@@ -44,6 +44,12 @@
  * the four-wave lisa_qmv_k5120_m{1,3}_prenorm. */
 #define LISA_QMV_WIDE_GROUPS 256
 
+/* lisa_qmv_k5120_m1_x_wide9: a one-row LOADX launch of STORE matrices of
+ * (8 x 256, 9 x 256] tiles (the config-0 GEMV: 2176 tiles) on workgroups of
+ * 64 x LISA_QMV_X_WIDE_WAVES threads, one tile per wave; grid ceil(tiles / 9).
+ * Outputs are the bits of the four-wave lisa_qmv_k5120_m1_x. */
+#define LISA_QMV_X_WIDE_WAVES 9
+
 enum {
   LISA_PRO_LOADX = 0,   /* x = bf16 x_in[M][K] */
   LISA_PRO_RESNORM = 1, /* r = bf16(h_in + bf16(o_in)); x = RMSNorm(r, norm_w) */

@@ -1206,8 +1206,32 @@ DEV void prenorm_wide(const LisaQmvParams& p, unsigned char* lds, const uint4 (&
 // group iterations are issued before the prologue, DEPTH are in flight during
 // the loop. Launch 64 NW threads per workgroup and tiles / (NW + XT)
 // workgroups.
-template <int M, int NW, int XT, int EPI, int EARLY, int DEPTH>
+// x of a LOADX launch over NT threads: thread t stages chunks t, t + NT, ..
+// (< 640) of every row, each chunk and its group's X_g as the 256-thread
+// prologue forms them (x_process), so the staged rows are the same bits.
+template <int M, int NT>
+DEV void loadx_wide(unsigned char* lds, const uint4 (&xa)[kWideChunks<NT>][M]) {
+  using C = QmvCfg<LISA_HIDDEN, M>;
+  float* gsum = reinterpret_cast<float*>(lds + C::XBYTES);
+  const int tid = threadIdx.x;
+#pragma unroll
+  for (int i = 0; i < kWideChunks<NT>; ++i) {
+    const int c = tid + NT * i;
+    const bool valid = c < kSegChunks;
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+      float x[8];
+      unpack_bf8(xa[i][m], x);
+      if (valid) put_chunk<LISA_HIDDEN, M>(lds, m, 8 * c, x);
+      put_gsum<LISA_HIDDEN, M>(gsum, m, 8 * c, valid, x);
+    }
+  }
+  __syncthreads();
+}
+
+template <int M, int NW, int XT, int EPI, int EARLY, int DEPTH, int PRO = LISA_PRO_PRENORM>
 DEV void qmv_wide(const LisaQmvParams& p, unsigned char* lds) {
+  static_assert(PRO == LISA_PRO_PRENORM || PRO == LISA_PRO_LOADX, "wide prologues");
   constexpr int K = LISA_HIDDEN, NT = 64 * NW, TPW = NW + XT, CH = kWideChunks<NT>;
   using C = QmvCfg<K, M>;
   using W = WideCfg<M>;
@@ -1229,13 +1253,15 @@ DEV void qmv_wide(const LisaQmvParams& p, unsigned char* lds) {
   const bool tile_ok = tile < tiles;
   const bool xwave = XT > 0 && wv < C::IMAX;  // runs iteration wv of the extra tile
 
+  // PRENORM: residual rows and norm weights; LOADX: the x rows (in ha)
   uint4 ha[CH][M], hw[CH];
 #pragma unroll
   for (int i = 0; i < CH; ++i) {
     const int c = min(tid + NT * i, kSegChunks - 1);
-    hw[i] = reinterpret_cast<const uint4*>(p.norm_w)[c];
+    if constexpr (PRO == LISA_PRO_PRENORM) hw[i] = reinterpret_cast<const uint4*>(p.norm_w)[c];
 #pragma unroll
-    for (int m = 0; m < M; ++m) ha[i][m] = reinterpret_cast<const uint4*>(p.h_in + (size_t)m * LISA_HIDDEN)[c];
+    for (int m = 0; m < M; ++m)
+      ha[i][m] = reinterpret_cast<const uint4*>((PRO == LISA_PRO_PRENORM ? p.h_in : p.x_in) + (size_t)m * LISA_HIDDEN)[c];
   }
   __builtin_amdgcn_sched_barrier(0);
   const TileRef tr = tile_ref<K>(p, tile_ok ? tile : tiles - 1, rp);
@@ -1247,7 +1273,8 @@ DEV void qmv_wide(const LisaQmvParams& p, unsigned char* lds) {
     load_unit_off<K, 1>(xu, xr, wv, wv + 1, li, 0, 1);
   }
   __builtin_amdgcn_sched_barrier(0);
-  prenorm_wide<M, NT>(p, lds, ha, hw);
+  if constexpr (PRO == LISA_PRO_PRENORM) prenorm_wide<M, NT>(p, lds, ha, hw);
+  else loadx_wide<M, NT>(lds, ha);
   __builtin_amdgcn_sched_barrier(0);
   // waves 0..4 first run the extra tile's iteration wv (its weights were
   // issued with the prologue's loads) and issue the tile's further iterations
@@ -1388,6 +1415,15 @@ LISA_QMV_INPROJ_WIDE(1, 8)
 LISA_QMV_INPROJ_WIDE(3, 7)
 LISA_QMV_INPROJ_WIDE(3, 8)
 #undef LISA_QMV_INPROJ_WIDE
+
+// A one-row LOADX launch of STORE matrices of 2049..2304 tiles (the 17408-row
+// projection of the config-0 GEMV: 2176 tiles): one workgroup of nine waves per
+// CU, one tile per wave, x staged once per CU; both pipelined iterations go
+// ahead of the staging, which only converts x.
+extern "C" __global__ __launch_bounds__(576) void lisa_qmv_k5120_m1_x_wide9(LisaQmvParams p) {
+  __shared__ __attribute__((aligned(16))) unsigned char lds[WideCfg<1>::BYTES];
+  qmv_wide<1, 9, 0, LISA_EPI_STORE, 2, 2, LISA_PRO_LOADX>(p, lds);
+}
 
 // ===========================================================================
 // GDN recurrence (gdn.metal:245-328) + gates (gdn.metal:170-205) + gated

@@ -123,6 +123,7 @@ struct LisaRunner {
   LisaFunction *qmv_epi[2][7][5] = {};  // K = 5120 with a fixed epilogue: [m3][prologue][epilogue]
   LisaFunction *qmv_gateup_wide[2] = {};  // MLP gate/up, PRENORM: 17 tiles per 16-wave workgroup [m3]
   LisaFunction *qmv_inproj_wide[2][2] = {};  // in-projections, PRENORM: one tile per wave [m3][NW 7, 8]
+  LisaFunction *qmv_x_wide = nullptr;  // one-row LOADX STORE launches of 2049..2304 tiles, 9 waves
   LisaFunction *gdn[2] = {}, *attn_part[2] = {}, *attn_merge[2] = {}, *finalize = nullptr, *synth = nullptr;
   // batched prefill
   LisaFunction *gemm = nullptr, *gemm_wide = nullptr, *gemm_swiglu = nullptr, *rows = nullptr, *conv_rows = nullptr, *gdn_prep_rows = nullptr, *gdn_scan_rows = nullptr,
@@ -629,6 +630,14 @@ int launch_qmv(LisaRunner* r, int m_rows, uint32_t K, LisaQmvParams& p, const st
       tiles % LISA_QMV_WIDE_GROUPS == 0 && (nw == 7 || nw == 8))
     return lisa_launch(r->dev, r->qmv_inproj_wide[m_rows == 3 ? 1 : 0][nw - 7], &p, sizeof p, LISA_QMV_WIDE_GROUPS,
                        1, 1, 64 * nw, 1, 1);
+  // a one-row plain-x launch of 2049..2304 tiles (a 17408-row projection):
+  // one workgroup of nine waves per CU
+  bool all_store = true;
+  for (const MatSpec& s : mats) all_store = all_store && s.kind == LISA_EPI_STORE;
+  constexpr uint32_t XW = LISA_QMV_X_WIDE_WAVES;
+  if (K == LISA_HIDDEN && m_rows == 1 && p.pro_mode == LISA_PRO_LOADX && all_store && !p.am_val && !p.gate_ab &&
+      tiles > (XW - 1) * LISA_QMV_WIDE_GROUPS && tiles <= XW * LISA_QMV_WIDE_GROUPS)
+    return lisa_launch(r->dev, r->qmv_x_wide, &p, sizeof p, (tiles + XW - 1) / XW, 1, 1, 64 * XW, 1, 1);
   const uint32_t grid = std::max<uint32_t>(1, qmv_grid(K, tiles));
   return lisa_launch(r->dev, fn, &p, sizeof p, grid, 1, 1, 256, 1, 1);
 }
@@ -1065,6 +1074,7 @@ int runner_init(const LisaRunnerConfig* cfg, std::unique_ptr<LisaRunner>& out) {
     for (int wi = 0; wi < 2; ++wi)
       LISA_TRY(lisa_function_get(r->mod, (std::string("lisa_qmv_k5120") + sfx + "_prenorm_wide" + (wi ? "8" : "7")).c_str(),
                                  &r->qmv_inproj_wide[mi][wi]));
+    if (mi == 0) LISA_TRY(lisa_function_get(r->mod, "lisa_qmv_k5120_m1_x_wide9", &r->qmv_x_wide));
   }
   LISA_TRY(lisa_function_get(r->mod, "lisa_step_finalize", &r->finalize));
   LISA_TRY(lisa_function_get(r->mod, "lisa_synth_fill", &r->synth));
@@ -1247,7 +1257,7 @@ extern "C" void lisa_runner_free(LisaRunner* r) {
       for (LisaFunction* f : b) delete f;
   for (LisaFunction* f : {r->gdn[0], r->gdn[1], r->attn_part[0], r->attn_part[1], r->attn_merge[0], r->attn_merge[1],
                           r->qmv_gateup_wide[0], r->qmv_gateup_wide[1], r->qmv_inproj_wide[0][0],
-                          r->qmv_inproj_wide[0][1], r->qmv_inproj_wide[1][0], r->qmv_inproj_wide[1][1],
+                          r->qmv_inproj_wide[0][1], r->qmv_inproj_wide[1][0], r->qmv_inproj_wide[1][1], r->qmv_x_wide,
                           r->finalize, r->synth, r->gemm, r->gemm_wide, r->gemm_swiglu, r->rows, r->conv_rows, r->gdn_prep_rows, r->gdn_scan_rows, r->gdn_out_rows, r->attn_store_rows,
                           r->attn_partial_rows, r->attn_merge_rows})
     delete f;

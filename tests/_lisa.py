@@ -70,8 +70,10 @@ def launch_qmv(pkg, dev, K, M, params, mats, wide=True):
     (DevQ4, DevQ4-or-None, out_ptr, kind). One 8-row tile per wave (K = 5120,
     four tiles per workgroup) or per workgroup with the group iterations split
     over its four waves (every other K); unless wide=False, the MLP gate/up
-    alone under PRENORM runs on the 16-wave kernel, and a PRENORM launch of
-    STORE/CONV matrices of 256 x 7 or 256 x 8 tiles on the 7- or 8-wave one."""
+    alone under PRENORM runs on the 16-wave kernel, a PRENORM launch of
+    STORE/CONV matrices of 256 x 7 or 256 x 8 tiles on the 7- or 8-wave one,
+    and a one-row LOADX launch of STORE matrices of 2049..2304 tiles on the
+    9-wave one."""
     tiles = 0
     for e, (q, q2, out, kind) in enumerate(mats):
         m = params.mats[e]
@@ -105,5 +107,13 @@ def launch_qmv(pkg, dev, K, M, params, mats, wide=True):
         # the runner's in-projection launch: one tile per wave, one workgroup per CU
         dev.dispatch(f"{name}_wide{nw}", params, (pkg.QMV_WIDE_GROUPS,), (64 * nw,))
         return params.ksplit, pkg.QMV_WIDE_GROUPS
+    xw = pkg.QMV_X_WIDE_WAVES
+    if (wide and K == 5120 and M == 1 and params.pro_mode == pkg.PRO_LOADX and kinds == {pkg.EPI_STORE}
+            and not params.am_val and not params.gate_ab
+            and (xw - 1) * pkg.QMV_WIDE_GROUPS < tiles <= xw * pkg.QMV_WIDE_GROUPS):
+        # the runner's one-row plain-x launch of a 17408-row projection
+        grid = (tiles + xw - 1) // xw
+        dev.dispatch(f"{name}_wide{xw}", params, (grid,), (64 * xw,))
+        return params.ksplit, grid
     dev.dispatch(name, params, (grid,), (256,))
     return params.ksplit, grid

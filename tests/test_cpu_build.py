@@ -46,7 +46,8 @@ def test_no_kernel_spills_to_scratch():
     for k in ("lisa_q4_gemm", "lisa_q4_gemm_wide", "lisa_qmv_k5120_m1_prenorm_gateup", "lisa_qmv_k17408_m1_x",
               "lisa_gdn_recurrence_m1", "lisa_attn_partial_m1", "lisa_qmv_k5120_m1_prenorm_gateup_wide",
               "lisa_qmv_k5120_m3_prenorm_gateup_wide", "lisa_qmv_k5120_m1_prenorm_wide7",
-              "lisa_qmv_k5120_m1_prenorm_wide8", "lisa_qmv_k5120_m3_prenorm_wide7", "lisa_qmv_k5120_m3_prenorm_wide8"):
+              "lisa_qmv_k5120_m1_prenorm_wide8", "lisa_qmv_k5120_m3_prenorm_wide7", "lisa_qmv_k5120_m3_prenorm_wide8",
+              "lisa_qmv_k5120_m1_x_wide9"):
         assert k in meta
     spilled = {k: v for k, v in meta.items() if v}
     assert not spilled, spilled
@@ -63,11 +64,13 @@ def test_python_launch_sizes_match_the_kernels():
         assert wg[f"lisa_qmv_k5120_m{m}_prenorm_gateup_wide"] == pkg.QMV_WIDE_THREADS
         for nw in (7, 8):
             assert wg[f"lisa_qmv_k5120_m{m}_prenorm_wide{nw}"] == 64 * nw
+    assert wg["lisa_qmv_k5120_m1_x_wide9"] == 64 * pkg.QMV_X_WIDE_WAVES
     assert wg["lisa_q4_gemm_wide"] == pkg.GEMM_THREADS_WIDE
     hdr = (Path(pkg.PKG_DIR).parent / "include" / "lisa_kernels.h").read_text()
     assert int(re.search(r"#define LISA_QMV_WIDE_TILES (\d+)", hdr).group(1)) == pkg.QMV_WIDE_TILES
     assert int(re.search(r"#define LISA_QMV_WIDE_THREADS (\d+)", hdr).group(1)) == pkg.QMV_WIDE_THREADS
     assert int(re.search(r"#define LISA_QMV_WIDE_GROUPS (\d+)", hdr).group(1)) == pkg.QMV_WIDE_GROUPS
+    assert int(re.search(r"#define LISA_QMV_X_WIDE_WAVES (\d+)", hdr).group(1)) == pkg.QMV_X_WIDE_WAVES
 
 
 STRUCTS = {  # Python mirror -> C typedef (include/lisa_kernels.h, include/lisa_hip.h)

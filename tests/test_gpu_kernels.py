@@ -229,6 +229,33 @@ def test_qmv_wide_gateup_equals_four_wave(pkg, orc, dev, M, N):
         assert np.array_equal(runs[0][0], orc.silu_mul(g, u))
 
 
+@pytest.mark.parametrize("N", [17408, 17411, 18000])
+def test_qmv_x_wide9_equals_four_wave(pkg, orc, dev, N):
+    """The one-row plain-x launch of 2049..2304 tiles on nine-wave workgroups
+    (x staged once per CU) against the four-wave kernel, bit for bit, and the
+    oracle: the config-0 shape (2176 tiles, 242 workgroups, the last with 7
+    tiles), a ragged last tile (17411 rows) and 2250 full tiles."""
+    rng = np.random.default_rng(500 + N)
+    K = 5120
+    w, s, b = rand_q4(rng, N, K)
+    q = DevQ4(dev, w, s, b)
+    x = bf16(rng.standard_normal((1, K)).astype(np.float32))
+    xb = dev.upload(x)
+    runs = []
+    for wide in (True, False):
+        out = dev.buffer(N * 4)
+        p = pkg.QmvParams()
+        p.pro_mode = pkg.PRO_LOADX
+        p.x_in = xb.ptr
+        _, grid = launch_qmv(pkg, dev, K, 1, p, [(q, None, out.ptr, pkg.EPI_STORE)], wide=wide)
+        runs.append((grid, out.read(np.float32, N)))
+    tiles = (N + 7) // 8
+    assert runs[0][0] == (tiles + pkg.QMV_X_WIDE_WAVES - 1) // pkg.QMV_X_WIDE_WAVES
+    assert runs[1][0] == (tiles + 3) // 4
+    assert same_bits(runs[0][1], runs[1][1])
+    assert same_bits(runs[0][1], orc.q4_linear(x, w, s, b, N, K, 1, 1)[0])
+
+
 @pytest.mark.parametrize("M", [1, 3])
 @pytest.mark.parametrize("layer", ["gdn", "attn"])
 def test_qmv_wide_inproj_equals_four_wave(pkg, orc, dev, M, layer):
