@@ -172,7 +172,7 @@ typedef struct LisaGdnParams {
 /* ---- split-K decode attention --------------------------------------------
  * Kernels: lisa_attn_partial_m{1,3} grid (s_max, 4) x LISA_ATT_PARTIAL_THREADS(M),
  *          lisa_attn_merge_m{1,3}   grid (24, M) x 256. */
-/* threads of lisa_attn_partial_m<M>: 256 for one row, 512 for three */
+/* threads of lisa_attn_partial_m<M>: sixteen waves for one row and for three */
 #define LISA_ATT_PARTIAL_THREADS(M) ((M) == 3 ? 1024 : 1024)
 typedef struct LisaAttnParams {
   const float* q_proj; /* [M][12288] raw */
