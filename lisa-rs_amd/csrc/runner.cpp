@@ -29,6 +29,7 @@
 #include "lisa_hip.h"
 #include "loader.h"
 #include "lisa_kernels.h"
+#include "qmv_launch.h"
 #include "lisa_model.h"
 #include "lisa_numerics.h"
 #include "lisa_synth.h"
@@ -590,11 +591,6 @@ int launch_qmv(LisaRunner* r, int m_rows, uint32_t K, LisaQmvParams& p, const st
     if (LisaFunction* f = r->qmv_epi[m_rows == 3 ? 1 : 0][p.pro_mode][mats[0].kind]) fn = f;
   }
   if (!fn) return lisa_fail(LISA_E_ARG, "no q4 kernel for K=%u M=%d prologue %u", K, m_rows, p.pro_mode);
-  // the MLP gate/up alone under the PRENORM prologue: one 16-wave workgroup per
-  // 17 tiles (the 4352 tiles of the model's pair are 256 x 17), the bits of
-  // the four-wave kernel
-  const bool wide = K == LISA_HIDDEN && mats.size() == 1 && mats[0].kind == LISA_EPI_GATEUP &&
-                    p.pro_mode == LISA_PRO_PRENORM && !p.gate_ab && !p.am_val;
   p.n_mats = (uint32_t)mats.size();
   uint32_t tiles = 0, rows_total = 0;
   for (size_t e = 0; e < mats.size(); ++e) {
@@ -616,30 +612,18 @@ int launch_qmv(LisaRunner* r, int m_rows, uint32_t K, LisaQmvParams& p, const st
   p.tile_start[mats.size()] = tiles;
   (void)rows_total;
   p.ksplit = qmv_split(K) ? 4 : 1;
-  if (wide) {
-    const uint32_t grid = std::max<uint32_t>(1, (tiles + LISA_QMV_WIDE_TILES - 1) / LISA_QMV_WIDE_TILES);
-    return lisa_launch(r->dev, r->qmv_gateup_wide[m_rows == 3 ? 1 : 0], &p, sizeof p, grid, 1, 1,
-                       LISA_QMV_WIDE_THREADS, 1, 1);
+  uint32_t kinds[LISA_QMV_MAX_MATS];
+  for (size_t e = 0; e < mats.size(); ++e) kinds[e] = mats[e].kind;
+  const LisaQmvShape sh = lisa_qmv_shape(K, m_rows, p.pro_mode, kinds, (int)mats.size(), tiles, p.gate_ab != nullptr,
+                                         p.am_val != nullptr);
+  const int mi = m_rows == 3 ? 1 : 0;
+  switch (sh.family) {
+    case LISA_QMV_GATEUP_WIDE: fn = r->qmv_gateup_wide[mi]; break;
+    case LISA_QMV_INPROJ_WIDE: fn = r->qmv_inproj_wide[mi][sh.nw - 7]; break;
+    case LISA_QMV_X_WIDE: fn = r->qmv_x_wide; break;
+    default: break;
   }
-  // the GDN (2048 tiles) and attention (1792) in-projections under PRENORM:
-  // one workgroup of NW = tiles / 256 waves per CU, one tile per wave
-  bool store_conv = true;
-  for (const MatSpec& s : mats) store_conv = store_conv && (s.kind == LISA_EPI_STORE || s.kind == LISA_EPI_CONV);
-  const uint32_t nw = tiles / LISA_QMV_WIDE_GROUPS;
-  if (K == LISA_HIDDEN && p.pro_mode == LISA_PRO_PRENORM && store_conv && !p.am_val &&
-      tiles % LISA_QMV_WIDE_GROUPS == 0 && (nw == 7 || nw == 8))
-    return lisa_launch(r->dev, r->qmv_inproj_wide[m_rows == 3 ? 1 : 0][nw - 7], &p, sizeof p, LISA_QMV_WIDE_GROUPS,
-                       1, 1, 64 * nw, 1, 1);
-  // a one-row plain-x launch of 2049..2304 tiles (a 17408-row projection):
-  // one workgroup of nine waves per CU
-  bool all_store = true;
-  for (const MatSpec& s : mats) all_store = all_store && s.kind == LISA_EPI_STORE;
-  constexpr uint32_t XW = LISA_QMV_X_WIDE_WAVES;
-  if (K == LISA_HIDDEN && m_rows == 1 && p.pro_mode == LISA_PRO_LOADX && all_store && !p.am_val && !p.gate_ab &&
-      tiles > (XW - 1) * LISA_QMV_WIDE_GROUPS && tiles <= XW * LISA_QMV_WIDE_GROUPS)
-    return lisa_launch(r->dev, r->qmv_x_wide, &p, sizeof p, (tiles + XW - 1) / XW, 1, 1, 64 * XW, 1, 1);
-  const uint32_t grid = std::max<uint32_t>(1, qmv_grid(K, tiles));
-  return lisa_launch(r->dev, fn, &p, sizeof p, grid, 1, 1, 256, 1, 1);
+  return lisa_launch(r->dev, fn, &p, sizeof p, sh.grid, 1, 1, sh.block, 1, 1);
 }
 
 // Consumer of the residual rows: x = RMSNorm(c.H), the statistic from 8-row

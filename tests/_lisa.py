@@ -65,15 +65,36 @@ class DevQ4:
 PROLOGUE_NAMES = ["x", "resnorm", "embed", "cast", "norm", "mtpfc", "prenorm"]
 
 
+QMV_FOUR_WAVE, QMV_GATEUP_WIDE, QMV_INPROJ_WIDE, QMV_X_WIDE = range(4)  # csrc/qmv_launch.h LisaQmvFamily
+
+
+def qmv_shape(pkg, K, M, pro_mode, kinds, tiles, gate_ab, am_val, wide=True):
+    """Restates lisa_qmv_shape of lisa-rs_amd/csrc/qmv_launch.h (the runner's
+    rule): (family, grid, block, waves per workgroup). With wide=False every
+    launch takes the four-wave kernel."""
+    kinds = list(kinds)
+    all_store = bool(kinds) and all(k == pkg.EPI_STORE for k in kinds)
+    store_conv = bool(kinds) and all(k in (pkg.EPI_STORE, pkg.EPI_CONV) for k in kinds)
+    if wide and K == 5120:
+        if (kinds == [pkg.EPI_GATEUP] and pro_mode == pkg.PRO_PRENORM and not gate_ab and not am_val):
+            return QMV_GATEUP_WIDE, max(1, -(-tiles // pkg.QMV_WIDE_TILES)), pkg.QMV_WIDE_THREADS, pkg.QMV_WIDE_THREADS // 64
+        nw = tiles // pkg.QMV_WIDE_GROUPS
+        if (pro_mode == pkg.PRO_PRENORM and store_conv and not am_val and tiles % pkg.QMV_WIDE_GROUPS == 0
+                and nw in (7, 8)):
+            return QMV_INPROJ_WIDE, pkg.QMV_WIDE_GROUPS, 64 * nw, nw
+        xw = pkg.QMV_X_WIDE_WAVES
+        if (M == 1 and pro_mode == pkg.PRO_LOADX and all_store and not am_val and not gate_ab
+                and (xw - 1) * pkg.QMV_WIDE_GROUPS < tiles <= xw * pkg.QMV_WIDE_GROUPS):
+            return QMV_X_WIDE, -(-tiles // xw), 64 * xw, xw
+    return QMV_FOUR_WAVE, max(1, -(-tiles // 4) if K == 5120 else tiles), 256, 4
+
+
 def launch_qmv(pkg, dev, K, M, params, mats, wide=True):
     """Restates launch_qmv of lisa-rs_amd/csrc/runner.cpp. mats: list of
-    (DevQ4, DevQ4-or-None, out_ptr, kind). One 8-row tile per wave (K = 5120,
-    four tiles per workgroup) or per workgroup with the group iterations split
-    over its four waves (every other K); unless wide=False, the MLP gate/up
-    alone under PRENORM runs on the 16-wave kernel, a PRENORM launch of
-    STORE/CONV matrices of 256 x 7 or 256 x 8 tiles on the 7- or 8-wave one,
-    and a one-row LOADX launch of STORE matrices of 2049..2304 tiles on the
-    9-wave one."""
+    (DevQ4, DevQ4-or-None, out_ptr, kind). The launch shape follows qmv_shape;
+    the four-wave kernel owns one 8-row tile per wave (K = 5120, four tiles
+    per workgroup) or one per workgroup with its group iterations split over
+    the four waves (every other K)."""
     tiles = 0
     for e, (q, q2, out, kind) in enumerate(mats):
         m = params.mats[e]
@@ -89,31 +110,18 @@ def launch_qmv(pkg, dev, K, M, params, mats, wide=True):
     params.tile_start[len(mats)] = tiles
     params.n_mats = len(mats)
     params.ksplit = 1 if K == 5120 else 4
-    grid = max(1, tiles if params.ksplit == 4 else (tiles + 3) // 4)
+    kinds = [kind for _, _, _, kind in mats]
+    family, grid, block, nw = qmv_shape(pkg, K, M, params.pro_mode, kinds, tiles, bool(params.gate_ab),
+                                        bool(params.am_val), wide)
     name = f"lisa_qmv_k{K}_m{M}_{PROLOGUE_NAMES[params.pro_mode]}"
-    kinds = {kind for _, _, _, kind in mats}
-    if K == 5120 and params.pro_mode in (pkg.PRO_RESNORM, pkg.PRO_PRENORM) and kinds in ({pkg.EPI_GATEUP},
-                                                                                    {pkg.EPI_ARGMAX}):
-        name += "_gateup" if kinds == {pkg.EPI_GATEUP} else "_argmax"  # the runner's specialized kernels
-    if (wide and K == 5120 and len(mats) == 1 and kinds == {pkg.EPI_GATEUP} and params.pro_mode == pkg.PRO_PRENORM
-            and not params.gate_ab and not params.am_val):
-        # the runner's 16-wave gate/up: LISA_QMV_WIDE_TILES tiles per workgroup
-        grid = max(1, (tiles + pkg.QMV_WIDE_TILES - 1) // pkg.QMV_WIDE_TILES)
-        dev.dispatch(name + "_wide", params, (grid,), (pkg.QMV_WIDE_THREADS,))
-        return params.ksplit, grid
-    nw = tiles // pkg.QMV_WIDE_GROUPS
-    if (wide and K == 5120 and params.pro_mode == pkg.PRO_PRENORM and kinds <= {pkg.EPI_STORE, pkg.EPI_CONV}
-            and not params.am_val and tiles % pkg.QMV_WIDE_GROUPS == 0 and nw in (7, 8)):
-        # the runner's in-projection launch: one tile per wave, one workgroup per CU
-        dev.dispatch(f"{name}_wide{nw}", params, (pkg.QMV_WIDE_GROUPS,), (64 * nw,))
-        return params.ksplit, pkg.QMV_WIDE_GROUPS
-    xw = pkg.QMV_X_WIDE_WAVES
-    if (wide and K == 5120 and M == 1 and params.pro_mode == pkg.PRO_LOADX and kinds == {pkg.EPI_STORE}
-            and not params.am_val and not params.gate_ab
-            and (xw - 1) * pkg.QMV_WIDE_GROUPS < tiles <= xw * pkg.QMV_WIDE_GROUPS):
-        # the runner's one-row plain-x launch of a 17408-row projection
-        grid = (tiles + xw - 1) // xw
-        dev.dispatch(f"{name}_wide{xw}", params, (grid,), (64 * xw,))
-        return params.ksplit, grid
-    dev.dispatch(name, params, (grid,), (256,))
+    if family == QMV_GATEUP_WIDE:
+        name += "_gateup_wide"
+    elif family == QMV_INPROJ_WIDE:
+        name += f"_wide{nw}"
+    elif family == QMV_X_WIDE:
+        name += f"_wide{nw}"
+    elif K == 5120 and params.pro_mode in (pkg.PRO_RESNORM, pkg.PRO_PRENORM) and set(kinds) in ({pkg.EPI_GATEUP},
+                                                                                          {pkg.EPI_ARGMAX}):
+        name += "_gateup" if set(kinds) == {pkg.EPI_GATEUP} else "_argmax"  # the runner's specialized kernels
+    dev.dispatch(name, params, (grid,), (block,))
     return params.ksplit, grid

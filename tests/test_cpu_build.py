@@ -164,3 +164,44 @@ def test_synth_fill_refuses_overruns():
         fill(Dev(), Buf(), 4 * 256, pkg.FILL_KV, 1, capacity=0, filled=1)
     with pytest.raises(ValueError):
         fill(Dev(), Buf(), 4, 7, 1)
+
+
+def test_python_launch_rule_matches_the_runner(tmp_path):
+    """tests/_lisa.py's qmv_shape (the launch shape the GPU tests dispatch)
+    equals lisa_qmv_shape of csrc/qmv_launch.h, which the runner applies, on
+    the model's q4 launches and the edges of each rule."""
+    import _lisa
+    pkg = load_pkg()
+    root = Path(pkg.PKG_DIR).parent
+    S, G, C, A, R = pkg.EPI_STORE, pkg.EPI_GATEUP, pkg.EPI_CONV, pkg.EPI_ARGMAX, pkg.EPI_RESID
+    cases = []
+    for m in (1, 3):
+        cases += [(5120, m, pkg.PRO_PRENORM, [G], 4352, 0, 0), (5120, m, pkg.PRO_PRENORM, [G], 251, 0, 0),
+                  (5120, m, pkg.PRO_PRENORM, [G], 4352, 1, 0), (5120, m, pkg.PRO_RESNORM, [G], 4352, 0, 0),
+                  (5120, m, pkg.PRO_PRENORM, [C, S], 2048, 1, 0), (5120, m, pkg.PRO_PRENORM, [S, S, S], 1792, 0, 0),
+                  (5120, m, pkg.PRO_PRENORM, [S], 2047, 0, 0), (5120, m, pkg.PRO_PRENORM, [S], 1536, 0, 0),
+                  (5120, m, pkg.PRO_PRENORM, [A], 31040, 0, 1), (5120, m, pkg.PRO_PRENORM, [R, S], 2048, 0, 0),
+                  (5120, m, pkg.PRO_EMBED, [C, S], 2048, 1, 0), (5120, m, pkg.PRO_CAST, [S, S, S], 1792, 0, 0),
+                  (5120, m, pkg.PRO_LOADX, [S], 2176, 0, 0), (5120, m, pkg.PRO_LOADX, [S], 2048, 0, 0),
+                  (5120, m, pkg.PRO_LOADX, [S], 2049, 0, 0), (5120, m, pkg.PRO_LOADX, [S], 2304, 0, 0),
+                  (5120, m, pkg.PRO_LOADX, [S], 2305, 0, 0), (5120, m, pkg.PRO_LOADX, [S, S], 2176, 0, 0),
+                  (5120, m, pkg.PRO_LOADX, [C], 2176, 0, 0), (17408, m, pkg.PRO_LOADX, [R], 640, 0, 0),
+                  (6144, m, pkg.PRO_LOADX, [R], 640, 0, 0), (10240, m, pkg.PRO_MTPFC, [S], 640, 0, 0),
+                  (1024, m, pkg.PRO_LOADX, [S], 3, 0, 0), (5120, m, pkg.PRO_PRENORM, [S, S], 6, 0, 0)]
+    lines = ["#include <cstdio>", '#include "qmv_launch.h"', "int main() {"]
+    for K, m, pro, kinds, tiles, gab, amv in cases:
+        ks = ", ".join(str(k) for k in kinds)
+        lines.append(f"  {{ const uint32_t k[] = {{{ks}}}; const LisaQmvShape s = lisa_qmv_shape({K}, {m}, {pro}, k, "
+                     f"{len(kinds)}, {tiles}, {'true' if gab else 'false'}, {'true' if amv else 'false'}); "
+                     'std::printf("%d %u %u %u\\n", s.family, s.grid, s.block, s.nw); }')
+    lines += ["  return 0;", "}"]
+    src, exe = tmp_path / "shape.cpp", tmp_path / "shape"
+    src.write_text("\n".join(lines) + "\n")
+    subprocess.run(["g++", "-std=c++17", f"-I{root / 'include'}", f"-I{root / 'lisa-rs_amd' / 'csrc'}", str(src),
+                    "-o", str(exe)], check=True, capture_output=True)
+    got = [tuple(int(v) for v in line.split())
+           for line in subprocess.run([str(exe)], check=True, capture_output=True, text=True).stdout.splitlines()]
+    want = [_lisa.qmv_shape(pkg, K, m, pro, kinds, tiles, bool(gab), bool(amv)) for K, m, pro, kinds, tiles, gab, amv in cases]
+    assert got == want
+    families = {w[0] for w in want}
+    assert families == {0, 1, 2, 3}
