@@ -292,8 +292,9 @@ typedef struct LisaRowsParams {
 } LisaRowsParams;
 
 /* lisa_attn_partial_rows takes LISA_ATT_ROWS_PER_WG rows per workgroup:
- * grid (s_max, 4, ceil(m / LISA_ATT_ROWS_PER_WG)) x 256. */
+ * grid (s_max, 4, ceil(m / LISA_ATT_ROWS_PER_WG)) x LISA_ATT_ROWS_THREADS. */
 #define LISA_ATT_ROWS_PER_WG 8
+#define LISA_ATT_ROWS_THREADS 1024
 
 /* lisa_gdn_conv_rows: causal conv + SiLU over m rows per channel with the
  * carried history, grid (ceil(10240/256), ceil(m/64)) x 256. */

@@ -112,6 +112,7 @@ QMV_WIDE_THREADS = 1024  # lisa_qmv_k5120_m{1,3}_prenorm_gateup_wide workgroup s
 QMV_WIDE_TILES = 17  # 8-row tiles per workgroup of that kernel (LISA_QMV_WIDE_TILES)
 QMV_WIDE_GROUPS = 256  # workgroups of a lisa_qmv_k5120_m{1,3}_prenorm_wide{7,8} launch (LISA_QMV_WIDE_GROUPS)
 QMV_X_WIDE_WAVES = 9  # waves of lisa_qmv_k5120_m1_x_wide9 (LISA_QMV_X_WIDE_WAVES)
+ATT_ROWS_THREADS = 1024  # workgroup size of lisa_attn_partial_rows (LISA_ATT_ROWS_THREADS)
 
 
 class RowsParams(C.Structure):

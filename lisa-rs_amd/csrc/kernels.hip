@@ -2711,11 +2711,13 @@ extern "C" __global__ __launch_bounds__(256) void lisa_attn_store_rows(LisaAttnP
   }
 }
 
-// 2. slice partials: grid (s_max, 4, ceil(m / ATT_RB)); a workgroup takes one
-//    64-token slice of one KV head for ATT_RB rows.
+// 2. slice partials: grid (s_max, 4, ceil(m / ATT_RB)); a workgroup of sixteen
+//    waves takes one 64-token slice of one KV head for ATT_RB rows (its LDS
+//    allows one workgroup per CU, so the waves that interleave the score and
+//    P.V loops are all in it).
 constexpr int ATT_RB = LISA_ATT_ROWS_PER_WG;
-extern "C" __global__ __launch_bounds__(256) void lisa_attn_partial_rows(LisaAttnParams p) {
-  constexpr int T = LISA_ATT_SLICE, HD = LISA_ATT_HD, KP = HD + 8;
+extern "C" __global__ __launch_bounds__(LISA_ATT_ROWS_THREADS) void lisa_attn_partial_rows(LisaAttnParams p) {
+  constexpr int T = LISA_ATT_SLICE, HD = LISA_ATT_HD, KP = HD + 8, NT = LISA_ATT_ROWS_THREADS, NW = NT / 64;
   const uint32_t base = *p.pos;
   const int s = blockIdx.x, kvh = blockIdx.y, r0 = blockIdx.z * ATT_RB;
   const int nr = min(ATT_RB, (int)p.m_rows - r0);
@@ -2728,19 +2730,19 @@ extern "C" __global__ __launch_bounds__(256) void lisa_attn_partial_rows(LisaAtt
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const size_t cache_base = (size_t)kvh * p.capacity * HD;
   const int nrows = (int)min((uint32_t)T, base + (uint32_t)(r0 + nr) - t0);
-  for (int c = tid; c < nrows * (HD / 8); c += 256) {
+  for (int c = tid; c < nrows * (HD / 8); c += NT) {
     const int row = c / (HD / 8), col = (c % (HD / 8)) * 8;
     const size_t off = cache_base + (size_t)(t0 + row) * HD + col;
     *reinterpret_cast<uint4*>(&Kt[row * KP + col]) = *reinterpret_cast<const uint4*>(p.key_cache + off);
     *reinterpret_cast<uint4*>(&Vt[row * HD + col]) = *reinterpret_cast<const uint4*>(p.value_cache + off);
   }
-  for (int e = tid; e < nr * 6 * HD; e += 256) {
+  for (int e = tid; e < nr * 6 * HD; e += NT) {
     const int tt = e / (6 * HD), i = (e / HD) % 6, d = e % HD;
     qv[e] = bf2f(p.query[((size_t)(r0 + tt) * LISA_ATT_QH + kvh * 6 + i) * HD + d]);
   }
   __syncthreads();
   // scores: item (row tt, head pair) per wave, as the decode partial
-  for (int it = wave; it < nr * 3; it += 4) {
+  for (int it = wave; it < nr * 3; it += NW) {
     const int tt = it / 3, i = 2 * (it % 3), h = kvh * 6 + i, t = r0 + tt;
     const uint32_t ctx = base + t + 1;
     if (ctx <= t0) continue;
@@ -2751,9 +2753,10 @@ extern "C" __global__ __launch_bounds__(256) void lisa_attn_partial_rows(LisaAtt
                   ml + (size_t)p.s_max * 2);
   }
   __syncthreads();
-  // P.V: thread (dp, hg) owns dimensions 2dp, 2dp+1 of heads 3hg..3hg+2
-  const int dp = tid & 127, hg = tid >> 7;
-  for (int tt = 0; tt < nr; ++tt) {
+  // P.V: thread (dp, hg, rr) owns dimensions 2dp, 2dp+1 of heads 3hg..3hg+2
+  // of rows rr, rr + NT / 256, ..
+  const int dp = tid & 127, hg = (tid >> 7) & 1;
+  for (int tt = tid >> 8; tt < nr; tt += NT / 256) {
     const int t = r0 + tt;
     const uint32_t ctx = base + t + 1;
     if (ctx <= t0) continue;

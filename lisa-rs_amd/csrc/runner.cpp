@@ -1880,7 +1880,7 @@ int prefill_attention(LisaRunner* r, uint32_t m, uint32_t base, const uint16_t* 
     b.m_rows = ms;
     const uint32_t slices = (base + r0 + ms + LISA_ATT_SLICE - 1) / LISA_ATT_SLICE;
     LISA_TRY(lisa_launch(r->dev, r->attn_partial_rows, &b, sizeof b, slices, LISA_ATT_KVH,
-                         (ms + LISA_ATT_ROWS_PER_WG - 1) / LISA_ATT_ROWS_PER_WG, 256, 1, 1));
+                         (ms + LISA_ATT_ROWS_PER_WG - 1) / LISA_ATT_ROWS_PER_WG, LISA_ATT_ROWS_THREADS, 1, 1));
     LISA_TRY(lisa_launch(r->dev, r->attn_merge_rows, &b, sizeof b, LISA_ATT_QH, ms, 1, 256, 1, 1));
   }
   return LISA_OK;

@@ -65,12 +65,14 @@ def test_python_launch_sizes_match_the_kernels():
         for nw in (7, 8):
             assert wg[f"lisa_qmv_k5120_m{m}_prenorm_wide{nw}"] == 64 * nw
     assert wg["lisa_qmv_k5120_m1_x_wide9"] == 64 * pkg.QMV_X_WIDE_WAVES
+    assert wg["lisa_attn_partial_rows"] == pkg.ATT_ROWS_THREADS
     assert wg["lisa_q4_gemm_wide"] == pkg.GEMM_THREADS_WIDE
     hdr = (Path(pkg.PKG_DIR).parent / "include" / "lisa_kernels.h").read_text()
     assert int(re.search(r"#define LISA_QMV_WIDE_TILES (\d+)", hdr).group(1)) == pkg.QMV_WIDE_TILES
     assert int(re.search(r"#define LISA_QMV_WIDE_THREADS (\d+)", hdr).group(1)) == pkg.QMV_WIDE_THREADS
     assert int(re.search(r"#define LISA_QMV_WIDE_GROUPS (\d+)", hdr).group(1)) == pkg.QMV_WIDE_GROUPS
     assert int(re.search(r"#define LISA_QMV_X_WIDE_WAVES (\d+)", hdr).group(1)) == pkg.QMV_X_WIDE_WAVES
+    assert int(re.search(r"#define LISA_ATT_ROWS_THREADS (\d+)", hdr).group(1)) == pkg.ATT_ROWS_THREADS
 
 
 STRUCTS = {  # Python mirror -> C typedef (include/lisa_kernels.h, include/lisa_hip.h)

@@ -209,7 +209,7 @@ def test_attention_rows_bit_exact(pkg, orc, dev):
                        query=query.ptr, m_rows=m)
     dev.dispatch("lisa_attn_store_rows", p, (m, 7), (256,))
     rb = pkg.ATT_ROWS_PER_WG
-    dev.dispatch("lisa_attn_partial_rows", p, ((base + m + 63) // 64, 4, (m + rb - 1) // rb), (256,))
+    dev.dispatch("lisa_attn_partial_rows", p, ((base + m + 63) // 64, 4, (m + rb - 1) // rb), (pkg.ATT_ROWS_THREADS,))
     dev.dispatch("lisa_attn_merge_rows", p, (24, m), (256,))
     want, kc2, vc2 = orc.attention(q_proj, k_raw, v_raw, qn, kn, kc, vc, cap, base, m)
     assert np.array_equal(bufs["kc"].read(np.uint16, kc.size), kc2)
