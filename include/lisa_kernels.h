@@ -240,6 +240,7 @@ typedef struct LisaSynthParams {
  * k multiple of 64. lisa_q4_gemm_wide: same contract, 256 x LISA_GEMM_TILE_N_WIDE
  * tiles, LISA_GEMM_THREADS_WIDE threads. */
 #define LISA_GEMM_TILE_M 256
+#define LISA_GEMM_TILE_M_SMALL 128 /* lisa_q4_gemm_m128: 128 x LISA_GEMM_TILE_N tiles, 256 threads */
 #define LISA_GEMM_TILE_N 128
 #define LISA_GEMM_TILE_N_WIDE 256
 #define LISA_GEMM_THREADS_WIDE 512

@@ -103,6 +103,7 @@ class GemmParams(C.Structure):
 
 ROWS_EMBED, ROWS_NORM, ROWS_RESNORM, ROWS_SILU, ROWS_ARGMAX = range(5)
 GEMM_TILE_M, GEMM_TILE_N = 256, 128  # lisa_q4_gemm output tile (LISA_GEMM_TILE_M/N)
+GEMM_TILE_M_SMALL = 128  # lisa_q4_gemm_m128 output tile rows (LISA_GEMM_TILE_M_SMALL)
 GEMM_TILE_N_WIDE = 256  # lisa_q4_gemm_wide (LISA_GEMM_TILE_N_WIDE)
 GEMM_THREADS_WIDE = 512  # lisa_q4_gemm_wide workgroup size (LISA_GEMM_THREADS_WIDE)
 QMV_MAX_MATS = 4  # matrices per q4 launch (LISA_QMV_MAX_MATS)

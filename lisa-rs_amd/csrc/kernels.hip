@@ -2316,21 +2316,22 @@ typedef uint32_t lisa_u32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int GEMM_BM = LISA_GEMM_TILE_M, GEMM_PAD = 72;
 
-// NT threads (4 or 8 waves): waves split the 256 x BN tile WM x WN; each wave
-// owns a 128 x BN/WN block as 4 x NB MFMA blocks.
-template <int BN, int NT>
+// NT threads (4 or 8 waves): waves split the BM x BN tile 2 x WN; each wave
+// owns a BM/2 x BN/WN block as AB x NB MFMA blocks.
+template <int BN, int NT, int BM = GEMM_BM>
 struct GemmCfg {
   static constexpr int WAVES = NT / 64;
   static constexpr int WN = WAVES / 2;                 // waves along N (2 or 4)
-  static constexpr int RA = GEMM_BM * 8 / NT;          // A chunks per thread and K step
+  static constexpr int AB = BM / 64;                   // 32-row A blocks per wave
+  static constexpr int RA = BM * 8 / NT;               // A chunks per thread and K step
   static constexpr int RW = BN * 2 / NT;               // W 16 B chunks per thread and K step
   static constexpr int NB = BN / WN / 32;              // 32-wide N blocks per wave
-  static_assert(RA % 4 == 0 && RW >= 1 && NB >= 1, "tile");
+  static_assert(RA % 4 == 0 && RW >= 1 && NB >= 1 && AB >= 1 && (32 * RW) % (AB * NB) == 0, "tile");
 };
 
-template <int BN, int NT>
+template <int BN, int NT, int BM>
 DEV void gemm_lstore(uint16_t* as, uint16_t* ws, int tid, const lisa_u32x4* a, const lisa_u32x4* w, uint32_t sb) {
-  using G = GemmCfg<BN, NT>;
+  using G = GemmCfg<BN, NT, BM>;
 #pragma unroll
   for (int i = 0; i < G::RA; ++i) {
     const int u = tid + NT * i;
@@ -2354,34 +2355,34 @@ DEV void gemm_lstore(uint16_t* as, uint16_t* ws, int tid, const lisa_u32x4* a, c
   }
 }
 
-template <int BN, int NT>
-DEV void gemm_frags(const uint16_t* as, const uint16_t* ws, int wm, int wn, int lane, int ks, lisa_bf16x8 (&af)[4],
-                    lisa_bf16x8 (&bf)[GemmCfg<BN, NT>::NB]) {
-  using G = GemmCfg<BN, NT>;
+template <int BN, int NT, int BM>
+DEV void gemm_frags(const uint16_t* as, const uint16_t* ws, int wm, int wn, int lane, int ks,
+                    lisa_bf16x8 (&af)[GemmCfg<BN, NT, BM>::AB], lisa_bf16x8 (&bf)[GemmCfg<BN, NT, BM>::NB]) {
+  using G = GemmCfg<BN, NT, BM>;
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < G::AB; ++i)
     af[i] = *reinterpret_cast<const lisa_bf16x8*>(
-        &as[(wm * 128 + i * 32 + (lane & 31)) * GEMM_PAD + ks * 16 + 8 * (lane >> 5)]);
+        &as[(wm * (BM / 2) + i * 32 + (lane & 31)) * GEMM_PAD + ks * 16 + 8 * (lane >> 5)]);
 #pragma unroll
   for (int j = 0; j < G::NB; ++j)
     bf[j] = *reinterpret_cast<const lisa_bf16x8*>(
         &ws[(wn * (BN / G::WN) + j * 32 + (lane & 31)) * GEMM_PAD + ks * 16 + 8 * (lane >> 5)]);
 }
 
-template <int BN, int NT>
+template <int BN, int NT, int BM>
 DEV void gemm_step(const uint16_t* as_r, const uint16_t* ws_r, uint16_t* as_w, uint16_t* ws_w, int tid, int wm, int wn,
                    int lane, const lisa_u32x4* a, const lisa_u32x4* w, uint32_t sb,
-                   lisa_f32x16 (&acc)[4][GemmCfg<BN, NT>::NB]) {
-  using G = GemmCfg<BN, NT>;
-  lisa_bf16x8 af[2][4], bf[2][G::NB];
-  gemm_frags<BN, NT>(as_r, ws_r, wm, wn, lane, 0, af[0], bf[0]);
+                   lisa_f32x16 (&acc)[GemmCfg<BN, NT, BM>::AB][GemmCfg<BN, NT, BM>::NB]) {
+  using G = GemmCfg<BN, NT, BM>;
+  lisa_bf16x8 af[2][G::AB], bf[2][G::NB];
+  gemm_frags<BN, NT, BM>(as_r, ws_r, wm, wn, lane, 0, af[0], bf[0]);
   const float sc = lo_bf(sb), bi = hi_bf(sb);
 #pragma unroll
   for (int ks = 0; ks < 4; ++ks) {
     const int c = ks & 1;
-    if (ks + 1 < 4) gemm_frags<BN, NT>(as_r, ws_r, wm, wn, lane, ks + 1, af[c ^ 1], bf[c ^ 1]);
+    if (ks + 1 < 4) gemm_frags<BN, NT, BM>(as_r, ws_r, wm, wn, lane, ks + 1, af[c ^ 1], bf[c ^ 1]);
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < G::AB; ++i)
 #pragma unroll
       for (int j = 0; j < G::NB; ++j)
         acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[c][i], bf[c][j], acc[i][j], 0, 0, 0);
@@ -2401,11 +2402,11 @@ DEV void gemm_step(const uint16_t* as_r, const uint16_t* ws_r, uint16_t* as_w, u
       const int u = tid + NT * i;
       *reinterpret_cast<lisa_u32x4*>(&as_w[(u >> 3) * GEMM_PAD + (u & 7) * 8]) = a[i];
     }
-    if (ks + 1 < 4) __builtin_amdgcn_sched_group_barrier(0x100, 4 + G::NB, 0);
+    if (ks + 1 < 4) __builtin_amdgcn_sched_group_barrier(0x100, G::AB + G::NB, 0);
 #pragma unroll
-    for (int q = 0; q < 4 * G::NB; ++q) {
+    for (int q = 0; q < G::AB * G::NB; ++q) {
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x002, 32 * G::RW / (4 * G::NB) + 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x002, 32 * G::RW / (G::AB * G::NB) + 1, 0);
     }
     __builtin_amdgcn_sched_group_barrier(0x200, G::RA / 4 + G::RW, 0);
   }
@@ -2416,13 +2417,13 @@ DEV void gemm_step(const uint16_t* as_r, const uint16_t* ws_r, uint16_t* as_w, u
 // 1 up) of columns n0 + wn * 32 + (0..31); the epilogue then finds the gate
 // and up sums of an output in the same lane and writes bf16(silu(bf16 g) *
 // bf16 u) (mlp.metal:11-16) instead of the two f32 outputs.
-template <int BN, int NT, bool SWIGLU = false>
-DEV void q4_gemm_body(const LisaGemmParams& p, uint16_t (*As)[GEMM_BM * GEMM_PAD], uint16_t (*Ws)[BN * GEMM_PAD]) {
-  using G = GemmCfg<BN, NT>;
+template <int BN, int NT, bool SWIGLU = false, int BM = GEMM_BM>
+DEV void q4_gemm_body(const LisaGemmParams& p, uint16_t (*As)[BM * GEMM_PAD], uint16_t (*Ws)[BN * GEMM_PAD]) {
+  using G = GemmCfg<BN, NT, BM>;
   static_assert(!SWIGLU || G::NB == 2, "the gate/up tile pairs two 32-wide blocks per wave");
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave / G::WN, wn = wave % G::WN;
-  const uint32_t m0 = blockIdx.y * GEMM_BM, n0 = blockIdx.x * (SWIGLU ? BN / 2 : BN);
+  const uint32_t m0 = blockIdx.y * BM, n0 = blockIdx.x * (SWIGLU ? BN / 2 : BN);
   const uint32_t K = p.k, nk = K / 64;
 
   const lisa_u32x4* asrc[G::RA];
@@ -2443,9 +2444,9 @@ DEV void q4_gemm_body(const LisaGemmParams& p, uint16_t (*As)[GEMM_BM * GEMM_PAD
   const lisa_u32x4* wsrc = reinterpret_cast<const lisa_u32x4*>(wmat + (size_t)wrow * (K / 8)) + ((G::RW * tid) & 1);
   const uint32_t* sbsrc = sbmat + (size_t)wrow * (K / 64);
 
-  lisa_f32x16 acc[4][G::NB];
+  lisa_f32x16 acc[G::AB][G::NB];
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < G::AB; ++i)
 #pragma unroll
     for (int j = 0; j < G::NB; ++j)
 #pragma unroll
@@ -2462,7 +2463,7 @@ DEV void q4_gemm_body(const LisaGemmParams& p, uint16_t (*As)[GEMM_BM * GEMM_PAD
   uint32_t sb0, sb1;
   GEMM_GLOAD(a0, w0, sb0, 0);
   GEMM_GLOAD(a1, w1, sb1, 1);
-  gemm_lstore<BN, NT>(As[0], Ws[0], tid, a0, w0, sb0);
+  gemm_lstore<BN, NT, BM>(As[0], Ws[0], tid, a0, w0, sb0);
   __syncthreads();
   // Pairs of K steps. With an odd number of steps the second half of the
   // last pair is a phantom step past K whose scale and bias words are zero, so
@@ -2471,20 +2472,20 @@ DEV void q4_gemm_body(const LisaGemmParams& p, uint16_t (*As)[GEMM_BM * GEMM_PAD
   // matrix registers (the eight-wave tile then spills).
   for (uint32_t step = 0; step < nk; step += 2) {
     GEMM_GLOAD(a0, w0, sb0, step + 2);
-    gemm_step<BN, NT>(As[0], Ws[0], As[1], Ws[1], tid, wm, wn, lane, a1, w1, sb1, acc);
+    gemm_step<BN, NT, BM>(As[0], Ws[0], As[1], Ws[1], tid, wm, wn, lane, a1, w1, sb1, acc);
     __syncthreads();
     GEMM_GLOAD(a1, w1, sb1, step + 3);
-    gemm_step<BN, NT>(As[1], Ws[1], As[0], Ws[0], tid, wm, wn, lane, a0, w0, sb0, acc);
+    gemm_step<BN, NT, BM>(As[1], Ws[1], As[0], Ws[0], tid, wm, wn, lane, a0, w0, sb0, acc);
     __syncthreads();
   }
 #undef GEMM_GLOAD
   if constexpr (SWIGLU) {
     const uint32_t col = n0 + wn * 32 + (lane & 31);
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < G::AB; ++i)
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const uint32_t row = m0 + wm * 128 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+        const uint32_t row = m0 + wm * (BM / 2) + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
         if (row < p.m && col < p.n) {
           const float a = lisa_bf16r(lisa_silu_exp2(lisa_bf16r(acc[i][0][r])) * lisa_bf16r(acc[i][1][r]));
           p.act[(size_t)row * p.ldc + col] = lisa_f32_to_bf16(a);
@@ -2492,13 +2493,13 @@ DEV void q4_gemm_body(const LisaGemmParams& p, uint16_t (*As)[GEMM_BM * GEMM_PAD
       }
   } else {
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < G::AB; ++i)
 #pragma unroll
       for (int j = 0; j < G::NB; ++j) {
         const uint32_t col = n0 + wn * (BN / G::WN) + j * 32 + (lane & 31);
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-          const uint32_t row = m0 + wm * 128 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+          const uint32_t row = m0 + wm * (BM / 2) + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
           if (row < p.m && col < p.n) p.c[(size_t)row * p.ldc + col] = acc[i][j][r];
         }
       }
@@ -2514,6 +2515,15 @@ extern "C" __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(
   __shared__ __attribute__((aligned(16))) uint16_t As[2][GEMM_BM * GEMM_PAD];
   __shared__ __attribute__((aligned(16))) uint16_t Ws[2][LISA_GEMM_TILE_N * GEMM_PAD];
   q4_gemm_body<LISA_GEMM_TILE_N, 256>(p, As, Ws);
+}
+// Small projections (few tiles against the CUs): the 128 x 128 tile on four
+// waves, each a 64 x 64 block of 2 x 2 MFMA blocks; two workgroups fit per CU.
+// Every output takes the same MFMA sequence as in the 256 x 128 tile.
+extern "C" __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void lisa_q4_gemm_m128(
+    LisaGemmParams p) {
+  __shared__ __attribute__((aligned(16))) uint16_t As[2][LISA_GEMM_TILE_M_SMALL * GEMM_PAD];
+  __shared__ __attribute__((aligned(16))) uint16_t Ws[2][LISA_GEMM_TILE_N * GEMM_PAD];
+  q4_gemm_body<LISA_GEMM_TILE_N, 256, false, LISA_GEMM_TILE_M_SMALL>(p, As, Ws);
 }
 extern "C" __global__ __launch_bounds__(LISA_GEMM_THREADS_WIDE) __attribute__((amdgpu_waves_per_eu(2, 2))) void lisa_q4_gemm_wide(
     LisaGemmParams p) {

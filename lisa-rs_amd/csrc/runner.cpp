@@ -127,7 +127,7 @@ struct LisaRunner {
   LisaFunction *qmv_x_wide = nullptr;  // one-row LOADX STORE launches of 2049..2304 tiles, 9 waves
   LisaFunction *gdn[2] = {}, *attn_part[2] = {}, *attn_merge[2] = {}, *finalize = nullptr, *synth = nullptr;
   // batched prefill
-  LisaFunction *gemm = nullptr, *gemm_wide = nullptr, *gemm_swiglu = nullptr, *rows = nullptr, *conv_rows = nullptr, *gdn_prep_rows = nullptr, *gdn_scan_rows = nullptr,
+  LisaFunction *gemm = nullptr, *gemm_m128 = nullptr, *gemm_wide = nullptr, *gemm_swiglu = nullptr, *rows = nullptr, *conv_rows = nullptr, *gdn_prep_rows = nullptr, *gdn_scan_rows = nullptr,
                *gdn_out_rows = nullptr, *attn_store_rows = nullptr,
                *attn_partial_rows = nullptr, *attn_merge_rows = nullptr;
   // memory
@@ -1064,6 +1064,7 @@ int runner_init(const LisaRunnerConfig* cfg, std::unique_ptr<LisaRunner>& out) {
   LISA_TRY(lisa_function_get(r->mod, "lisa_synth_fill", &r->synth));
   LISA_TRY(lisa_function_get(r->mod, "lisa_q4_gemm", &r->gemm));
   LISA_TRY(lisa_function_get(r->mod, "lisa_q4_gemm_wide", &r->gemm_wide));
+  LISA_TRY(lisa_function_get(r->mod, "lisa_q4_gemm_m128", &r->gemm_m128));
   LISA_TRY(lisa_function_get(r->mod, "lisa_q4_gemm_swiglu", &r->gemm_swiglu));
   LISA_TRY(lisa_function_get(r->mod, "lisa_rows", &r->rows));
   LISA_TRY(lisa_function_get(r->mod, "lisa_gdn_conv_rows", &r->conv_rows));
@@ -1242,7 +1243,7 @@ extern "C" void lisa_runner_free(LisaRunner* r) {
   for (LisaFunction* f : {r->gdn[0], r->gdn[1], r->attn_part[0], r->attn_part[1], r->attn_merge[0], r->attn_merge[1],
                           r->qmv_gateup_wide[0], r->qmv_gateup_wide[1], r->qmv_inproj_wide[0][0],
                           r->qmv_inproj_wide[0][1], r->qmv_inproj_wide[1][0], r->qmv_inproj_wide[1][1], r->qmv_x_wide,
-                          r->finalize, r->synth, r->gemm, r->gemm_wide, r->gemm_swiglu, r->rows, r->conv_rows, r->gdn_prep_rows, r->gdn_scan_rows, r->gdn_out_rows, r->attn_store_rows,
+                          r->finalize, r->synth, r->gemm, r->gemm_m128, r->gemm_wide, r->gemm_swiglu, r->rows, r->conv_rows, r->gdn_prep_rows, r->gdn_scan_rows, r->gdn_out_rows, r->attn_store_rows,
                           r->attn_partial_rows, r->attn_merge_rows})
     delete f;
   lisa_buffer_free(r->pf.buf);
@@ -1806,6 +1807,11 @@ int launch_gemm(LisaRunner* r, const uint16_t* a, uint32_t m, const Q4Dev& w, fl
   const uint32_t gw = (w.n + LISA_GEMM_TILE_N_WIDE - 1) / LISA_GEMM_TILE_N_WIDE;
   const uint32_t cus = r->dev->cu_count > 0 ? (uint32_t)r->dev->cu_count : 256;
   const uint32_t rn = (gn * gm + cus - 1) / cus, rw = (gw * gm + cus - 1) / cus;
+  // a projection whose 256-row tiles would fill at most half the CUs (the GDN
+  // a and b, attention k and v): 128-row tiles, twice the workgroups
+  if (gn * gm * 2 <= cus)
+    return lisa_launch(r->dev, r->gemm_m128, &g, sizeof g, gn, (m + LISA_GEMM_TILE_M_SMALL - 1) / LISA_GEMM_TILE_M_SMALL,
+                       1, 256, 1, 1);
   if (rw * 3 <= rn * 2) return lisa_launch(r->dev, r->gemm_wide, &g, sizeof g, gw, gm, 1, LISA_GEMM_THREADS_WIDE, 1, 1);
   return lisa_launch(r->dev, r->gemm, &g, sizeof g, gn, gm, 1, 256, 1, 1);
 }

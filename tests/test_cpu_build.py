@@ -47,7 +47,7 @@ def test_no_kernel_spills_to_scratch():
               "lisa_gdn_recurrence_m1", "lisa_attn_partial_m1", "lisa_qmv_k5120_m1_prenorm_gateup_wide",
               "lisa_qmv_k5120_m3_prenorm_gateup_wide", "lisa_qmv_k5120_m1_prenorm_wide7",
               "lisa_qmv_k5120_m1_prenorm_wide8", "lisa_qmv_k5120_m3_prenorm_wide7", "lisa_qmv_k5120_m3_prenorm_wide8",
-              "lisa_qmv_k5120_m1_x_wide9"):
+              "lisa_qmv_k5120_m1_x_wide9", "lisa_q4_gemm_m128"):
         assert k in meta
     spilled = {k: v for k, v in meta.items() if v}
     assert not spilled, spilled
@@ -66,6 +66,7 @@ def test_python_launch_sizes_match_the_kernels():
             assert wg[f"lisa_qmv_k5120_m{m}_prenorm_wide{nw}"] == 64 * nw
     assert wg["lisa_qmv_k5120_m1_x_wide9"] == 64 * pkg.QMV_X_WIDE_WAVES
     assert wg["lisa_attn_partial_rows"] == pkg.ATT_ROWS_THREADS
+    assert wg["lisa_q4_gemm_m128"] == 256
     assert wg["lisa_q4_gemm_wide"] == pkg.GEMM_THREADS_WIDE
     hdr = (Path(pkg.PKG_DIR).parent / "include" / "lisa_kernels.h").read_text()
     assert int(re.search(r"#define LISA_QMV_WIDE_TILES (\d+)", hdr).group(1)) == pkg.QMV_WIDE_TILES
@@ -73,6 +74,7 @@ def test_python_launch_sizes_match_the_kernels():
     assert int(re.search(r"#define LISA_QMV_WIDE_GROUPS (\d+)", hdr).group(1)) == pkg.QMV_WIDE_GROUPS
     assert int(re.search(r"#define LISA_QMV_X_WIDE_WAVES (\d+)", hdr).group(1)) == pkg.QMV_X_WIDE_WAVES
     assert int(re.search(r"#define LISA_ATT_ROWS_THREADS (\d+)", hdr).group(1)) == pkg.ATT_ROWS_THREADS
+    assert int(re.search(r"#define LISA_GEMM_TILE_M_SMALL (\d+)", hdr).group(1)) == pkg.GEMM_TILE_M_SMALL
 
 
 STRUCTS = {  # Python mirror -> C typedef (include/lisa_kernels.h, include/lisa_hip.h)

@@ -30,14 +30,14 @@ def dev(pkg):
     return pkg.Device(0)
 
 
-GEMM_KERNELS = ["lisa_q4_gemm", "lisa_q4_gemm_wide"]
+GEMM_KERNELS = ["lisa_q4_gemm", "lisa_q4_gemm_wide", "lisa_q4_gemm_m128"]
 
 
 def gemm(pkg, dev, a_bf16, q, m, kernel="lisa_q4_gemm"):
     out = dev.buffer(m * q.n * 4)
     ab = dev.upload(a_bf16)
     p = pkg.GemmParams(ab.ptr, q.wbuf.ptr, q.sbbuf.ptr, out.ptr, m, q.n, q.k, q.n)
-    tm = pkg.GEMM_TILE_M
+    tm = pkg.GEMM_TILE_M_SMALL if kernel.endswith("_m128") else pkg.GEMM_TILE_M
     wide = kernel.endswith("_wide")
     tn = pkg.GEMM_TILE_N_WIDE if wide else pkg.GEMM_TILE_N
     dev.dispatch(kernel, p, ((q.n + tn - 1) // tn, (m + tm - 1) // tm), (pkg.GEMM_THREADS_WIDE if wide else 256,))
@@ -71,6 +71,18 @@ def test_gemm_exact_integer_case(pkg, orc, dev, kernel, K):
     b = bf16(rng.choice(np.array([-8.0, -4.0, 0.0, 1.0], np.float32), size=(N, K // 64)))
     got = gemm(pkg, dev, a, DevQ4(dev, w, s, b), M, kernel)
     assert np.array_equal(got, orc.q4_gemm(a, w, s, b, N, K, M))
+
+
+@pytest.mark.parametrize("M,N,K", [(2048, 48, 5120), (2048, 1024, 5120), (300, 130, 192), (37, 200, 1024)])
+def test_gemm_m128_equals_256_row_tile(pkg, dev, M, N, K):
+    """The 128-row tile (the small projections: GDN a/b, attention k/v) gives
+    every output the same MFMA sequence as the 256-row tile: equal bits."""
+    rng = np.random.default_rng(M + 3 * N + K)
+    q = DevQ4(dev, *rand_q4(rng, N, K))
+    a = bf16(rng.standard_normal((M, K)).astype(np.float32))
+    got = gemm(pkg, dev, a, q, M, "lisa_q4_gemm_m128")
+    ref = gemm(pkg, dev, a, q, M, "lisa_q4_gemm")
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
 
 
 @pytest.mark.parametrize("M,N,K", [(300, 600, 1024), (37, 256, 5120), (260, 130, 192)])
