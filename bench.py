@@ -373,6 +373,18 @@ def gemm_phase(pkg, reps=10):
             "note": "dequantized q4 weights; peak = dense bf16 MFMA of MI355X"}
 
 
+def top2_logits(logits):
+    """(top-1 index, top-1 logit, top-2 logit, the row) of one oracle logit row;
+    ties go to the lowest index, as in the argmax kernels."""
+    v = np.asarray(logits, np.float32)
+    i1 = int(np.argmax(v))
+    v1 = float(v[i1])
+    v[i1] = -np.inf
+    v2 = float(v.max())
+    v[i1] = v1
+    return i1, v1, v2, v
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -453,7 +465,12 @@ def main():
         if list(rep_tokens) != list(tokens):
             raise SystemExit("bench.py: a repeat of the timed region produced different tokens")
     repeats = {"n": len(rep_tok_s), "median_tok_s": round(float(np.median(rep_tok_s)), 3),
-               "min_tok_s": round(min(rep_tok_s), 3), "max_tok_s": round(max(rep_tok_s), 3)}
+               "min_tok_s": round(min(rep_tok_s), 3), "max_tok_s": round(max(rep_tok_s), 3),
+               "first_tok_s": round(rep_tok_s[0], 3)}
+    # the reported value is the median of the repeated timed regions
+    tok_s = float(np.median(rep_tok_s))
+    ms_per_step = 1e3 / tok_s
+    gbps = bpt * tok_s / 1e9
 
     # per-launch profile (eager, hipEvents around every launch)
     runner.fill_state(CTX, CTX_SEED)
@@ -541,12 +558,13 @@ def main():
         model.fill_state(CTX, CTX_SEED)
         print(f"[bench] oracle model built in {time.time() - t0:.1f}s", file=sys.stderr, flush=True)
         tok = FIRST_TOKEN
-        cpu_tokens = []
+        cpu_tokens, cpu_top2 = [], []
         t_cpu = time.perf_counter()
         for _ in range(args.cpu_steps):
-            am, _ = model.forward([tok])
+            am, _, logits = model.forward([tok], want_logits=True)
             tok = int(am[0])
             cpu_tokens.append(tok)
+            cpu_top2.append(top2_logits(logits[0]))
         cpu_s = time.perf_counter() - t_cpu
         model.close()
         cpu_tok_s = args.cpu_steps / cpu_s
@@ -562,6 +580,14 @@ def main():
         gpu_head = [int(t) for t in tokens[:n_cmp]]
         result["exact_match"] = bool(n_cmp > 0 and gpu_head == cpu_tokens[:n_cmp])
         result["exact_match_tokens"] = n_cmp
+        first = next((i for i in range(n_cmp) if gpu_head[i] != cpu_tokens[i]), None)
+        if first is not None:
+            # the greedy margin at the first divergence (tests/spec_diag.rs:79-103)
+            i1, v1, v2, lg = cpu_top2[first]
+            result["mismatch"] = {"step": first, "gpu_token": gpu_head[first], "oracle_token": i1,
+                                  "oracle_top2_margin": v1 - v2,
+                                  "oracle_logit_gap_of_gpu_token": v1 - float(lg[gpu_head[first]])}
+            print(f"[bench] greedy mismatch: {result['mismatch']}", file=sys.stderr, flush=True)
         if "speculative" in result:
             # the speculative stream starts from the same state and first token
             spec_head = result["speculative"].pop("_tokens")[:n_cmp]

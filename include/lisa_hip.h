@@ -231,7 +231,9 @@ LisaDevice* lisa_runner_device(LisaRunner* r);
 uint32_t lisa_runner_position(LisaRunner* r);
 uint64_t lisa_runner_weight_bytes(LisaRunner* r);
 
-/* reset_state (runner.rs:423-444): zero GDN/conv state and KV, position 0. */
+/* QwenRunner::reset_state (runner.rs:423-444): zero the target's GDN/conv
+ * state and K/V caches, position 0. The drafter's caches and position are
+ * kept (MtpRunner::reset_state below clears those). */
 int lisa_runner_reset_state(LisaRunner* r);
 /* Synthetic context: GDN state N(0,0.01), conv history N(0,1), KV rows
  * [0,filled) N(0,1) (target and drafter), position = filled. */
@@ -325,6 +327,10 @@ int lisa_mtp_upload_cond(LisaRunner* r, const uint16_t* hidden);
 int lisa_mtp_read_normalized(LisaRunner* r, uint16_t* out);
 uint32_t lisa_mtp_position(LisaRunner* r);
 int lisa_mtp_trim_state(LisaRunner* r, int32_t count);
+/* MtpRunner::reset_state (runner.rs:2508-2520): zero the drafter's K/V caches,
+ * drafter position 0; the target's state is kept. LISA_E_STATE without a
+ * drafter. */
+int lisa_mtp_reset_state(LisaRunner* r);
 
 /* Device-resident conditioning by (buffer, byte offset), as speculative/mod.rs
  * passes it: the target's hidden row `row` sits at lisa_runner_hidden_offset(row)

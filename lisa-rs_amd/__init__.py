@@ -255,6 +255,7 @@ _SIGS = {
     "lisa_mtp_read_normalized": (C.c_int, [_P, _P]),
     "lisa_mtp_position": (C.c_uint32, [_P]),
     "lisa_mtp_trim_state": (C.c_int, [_P, C.c_int32]),
+    "lisa_mtp_reset_state": (C.c_int, [_P]),
     "lisa_runner_hidden_offset": (C.c_uint64, [C.c_int32]),
     "lisa_mtp_normalized_offset": (C.c_uint64, []),
     "lisa_mtp_resolve_cond": (C.c_int, [C.c_int32, C.c_uint64, C.POINTER(C.c_int32), C.POINTER(C.c_int32)]),
@@ -535,6 +536,7 @@ class Runner:
         return lib().lisa_runner_weight_bytes(self.h)
 
     def reset_state(self) -> None:
+        """QwenRunner::reset_state: the target's state only."""
         _check(lib().lisa_runner_reset_state(self.h))
 
     def fill_state(self, filled: int, seed: int) -> None:
@@ -652,6 +654,10 @@ class Runner:
 
     def mtp_trim_state(self, count: int) -> None:
         _check(lib().lisa_mtp_trim_state(self.h, count))
+
+    def mtp_reset_state(self) -> None:
+        """MtpRunner::reset_state: the drafter's K/V and position only."""
+        _check(lib().lisa_mtp_reset_state(self.h))
 
     def mtp_forward_device(self, token: int, cond_is_target: bool, cond_off: int):
         """forward_position_decode_device addressed by (buffer, byte offset):

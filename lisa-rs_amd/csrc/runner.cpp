@@ -1124,6 +1124,9 @@ int check_geometry(int32_t layers, int32_t vocab) {
   return LISA_OK;
 }
 
+// Clears the target's and the drafter's state (defined with the reset entry points).
+int reset_all(LisaRunner* r);
+
 }  // namespace
 
 extern "C" int lisa_runner_create(const LisaRunnerConfig* cfg, LisaRunner** out) {
@@ -1131,7 +1134,7 @@ extern "C" int lisa_runner_create(const LisaRunnerConfig* cfg, LisaRunner** out)
   std::unique_ptr<LisaRunner> r;
   LISA_TRY(runner_init(cfg, r));
   LISA_TRY(generate_weights(r.get()));
-  LISA_TRY(lisa_runner_reset_state(r.get()));
+  LISA_TRY(reset_all(r.get()));
   *out = r.release();
   return LISA_OK;
 }
@@ -1177,7 +1180,7 @@ extern "C" int lisa_runner_load(const char* target_snapshot, const char* mtp_sna
   LISA_TRY(runner_init(&c, r));
   LISA_TRY(upload_catalogue(r.get(), tgt.get(), target_catalogue(r.get())));
   if (drf) LISA_TRY(upload_catalogue(r.get(), drf.get(), mtp_catalogue(r.get())));
-  LISA_TRY(lisa_runner_reset_state(r.get()));
+  LISA_TRY(reset_all(r.get()));
   *out = r.release();
   return LISA_OK;
 }
@@ -1261,24 +1264,61 @@ extern "C" LisaDevice* lisa_runner_device(LisaRunner* r) { return r ? r->dev : n
 extern "C" uint32_t lisa_runner_position(LisaRunner* r) { return r ? r->position : 0; }
 extern "C" uint64_t lisa_runner_weight_bytes(LisaRunner* r) { return r && r->weights ? r->weights->len : 0; }
 
-extern "C" int lisa_runner_reset_state(LisaRunner* r) {
-  if (!r) return lisa_fail(LISA_E_ARG, "null runner");
-  LISA_TRY(lisa_hip_check(hipMemsetAsync(r->state->ptr, 0, r->state->len, r->dev->stream), "memset state"));
-  if (r->mtp_state)
-    LISA_TRY(lisa_hip_check(hipMemsetAsync(r->mtp_state->ptr, 0, r->mtp_state->len, r->dev->stream), "memset MTP KV"));
+namespace {
+
+// The target's recurrent state, verify slots and K/V caches: one contiguous
+// range of the state arena (plan_state), zeroed and the position rewound.
+int clear_target(LisaRunner* r) {
+  const size_t kv = (size_t)r->attn_layers * LISA_ATT_KVH * (size_t)r->cfg.capacity * LISA_ATT_HD;
+  char* lo = reinterpret_cast<char*>(r->gdn_state);
+  char* hi = reinterpret_cast<char*>(r->value_cache + kv);
+  LISA_TRY(lisa_hip_check(hipMemsetAsync(lo, 0, (size_t)(hi - lo), r->dev->stream), "memset state"));
   LISA_TRY(write_pos(r, r->tgt, 0));
-  LISA_TRY(write_pos(r, r->drf, 0));
-  LISA_TRY(sync(r));
   r->position = 0;
-  r->mtp_position = 0;
   r->verify_base = -1;
   return LISA_OK;
+}
+
+// The drafter's K/V caches (in the state arena of a runner created with the
+// drafter, in their own arena after lisa_mtp_load) and its position.
+int clear_drafter(LisaRunner* r) {
+  const size_t kv = (size_t)LISA_ATT_KVH * (size_t)r->cfg.capacity * LISA_ATT_HD * sizeof(uint16_t);
+  LISA_TRY(lisa_hip_check(hipMemsetAsync(r->mtp_key, 0, kv, r->dev->stream), "memset MTP keys"));
+  LISA_TRY(lisa_hip_check(hipMemsetAsync(r->mtp_value, 0, kv, r->dev->stream), "memset MTP values"));
+  LISA_TRY(write_pos(r, r->drf, 0));
+  r->mtp_position = 0;
+  return LISA_OK;
+}
+
+// Both halves: a new runner, a loaded one, a synthetic context.
+int reset_all(LisaRunner* r) {
+  LISA_TRY(clear_target(r));
+  if (r->cfg.with_mtp) LISA_TRY(clear_drafter(r));
+  return sync(r);
+}
+
+}  // namespace
+
+// QwenRunner::reset_state (runner.rs:423-444) clears the target's GDN, conv
+// and K/V state only; the drafter keeps its caches and position.
+extern "C" int lisa_runner_reset_state(LisaRunner* r) {
+  if (!r) return lisa_fail(LISA_E_ARG, "null runner");
+  LISA_TRY(clear_target(r));
+  return sync(r);
+}
+
+// MtpRunner::reset_state (runner.rs:2508-2520): the drafter's K/V and position.
+extern "C" int lisa_mtp_reset_state(LisaRunner* r) {
+  if (!r) return lisa_fail(LISA_E_ARG, "null runner");
+  if (!r->cfg.with_mtp) return lisa_fail(LISA_E_STATE, "runner holds no MTP drafter");
+  LISA_TRY(clear_drafter(r));
+  return sync(r);
 }
 
 extern "C" int lisa_runner_fill_state(LisaRunner* r, uint32_t filled, uint64_t seed) {
   if (!r) return lisa_fail(LISA_E_ARG, "null runner");
   if (filled > (uint32_t)r->cfg.capacity) return lisa_fail(LISA_E_CAPACITY, "fill beyond KV capacity");
-  LISA_TRY(lisa_runner_reset_state(r));
+  LISA_TRY(reset_all(r));
   const uint32_t cap = (uint32_t)r->cfg.capacity;
   for (int i = 0; i < r->cfg.layers; ++i) {
     const LayerDev& l = r->layers[i];

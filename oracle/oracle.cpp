@@ -1281,6 +1281,22 @@ int orc_model_tensor(OrcModel* M, int scope, int kind, int part, void** ptr, siz
   }
   if (scope < 1 || scope > M->layers) return -4;
   OrcLayer& l = M->L[scope - 1];
+  // a layer's slice of the recurrent state and of the K/V caches
+  auto span = [&](void* base, size_t nbytes) -> int {
+    if (part != 0) return -1;
+    *ptr = base;
+    *bytes = nbytes;
+    return 0;
+  };
+  if (!l.attention && kind == LISA_T_GDN_STATE)
+    return span(&M->gdn_state[(size_t)l.state_index * LISA_GDN_STATE], sizeof(float) * LISA_GDN_STATE);
+  if (!l.attention && kind == LISA_T_CONV_STATE)
+    return span(&M->conv_state[(size_t)l.state_index * 3 * LISA_GDN_CONV_DIM], 2 * 3 * LISA_GDN_CONV_DIM);
+  if (l.attention && (kind == LISA_T_KEY_CACHE || kind == LISA_T_VALUE_CACHE)) {
+    const size_t n = (size_t)LISA_ATT_KVH * M->capacity * LISA_ATT_HD;
+    std::vector<uint16_t>& c = kind == LISA_T_KEY_CACHE ? M->key_cache : M->value_cache;
+    return span(&c[(size_t)l.cache_index * n], 2 * n);
+  }
   switch (kind) {
     case LISA_T_INPUT_NORM: return vec(l.input_norm);
     case LISA_T_POST_NORM: return vec(l.post_norm);

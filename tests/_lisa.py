@@ -125,3 +125,23 @@ def launch_qmv(pkg, dev, K, M, params, mats, wide=True):
         name += "_gateup" if set(kinds) == {pkg.EPI_GATEUP} else "_argmax"  # the runner's specialized kernels
     dev.dispatch(name, params, (grid,), (block,))
     return params.ksplit, grid
+
+
+def top2(logits):
+    """(top-1 index, top-1 value, top-2 value) of a logit row, ties to the
+    lowest index as the argmax kernels break them."""
+    v = np.asarray(logits, np.float32)
+    i1 = int(np.argmax(v))
+    rest = v.copy()
+    rest[i1] = -np.inf
+    return i1, float(v[i1]), float(rest.max())
+
+
+def mismatch_diagnostic(step, gpu_token, oracle_logits):
+    """The report of a greedy mismatch (tests/spec_diag.rs:79-103): the step,
+    both tokens, the oracle's top-2 logit margin, and how far below the
+    oracle's top logit the GPU's token scored."""
+    i1, v1, v2 = top2(oracle_logits)
+    return (f"greedy mismatch at step {step}: gpu token {gpu_token}, oracle token {i1}; "
+            f"oracle top-2 margin {v1 - v2:.6g}; oracle logit of the gpu token "
+            f"{float(oracle_logits[gpu_token]):.6g} ({v1 - float(oracle_logits[gpu_token]):.6g} below the top)")

@@ -106,6 +106,8 @@ def test_drafter_loaded_after_the_target(loaded):
         assert d0 == w0
         assert np.array_equal(r.mtp_normalized(), wn0)
         r.reset_state()
+        assert r.position == 0 and r.mtp_position == 41  # the drafter kept its position
+        r.mtp_reset_state()
         assert r.mtp_position == 0
     finally:
         r.close()

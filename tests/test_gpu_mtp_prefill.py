@@ -40,6 +40,41 @@ def test_host_hidden_drafter_step_bit_exact(pair):
     assert r.mtp_position == m.mtp_position == 35
 
 
+def test_reset_halves_are_independent(pair):
+    """QwenRunner::reset_state (runner.rs:423-444) clears the target only and
+    MtpRunner::reset_state (runner.rs:2508-2520) the drafter only, as
+    src/cli/run.rs:74-82 and src/serve/mod.rs:209-234 call them."""
+    pkg, orc, r, m = pair
+    rng = np.random.default_rng(21)
+    r.fill_state(33, CTX_SEED)
+    m.fill_state(33, CTX_SEED)
+    r.reset_state()
+    assert (r.position, r.mtp_position) == (0, 33)
+    # the drafter's K/V survived the target reset: its step attends rows 0..33
+    h = rng.standard_normal(5120).astype(np.float32)
+    am, xn = r.mtp_forward_position_decode(41, h)
+    wam, wxn = m.mtp_forward(41, orc.f32_to_bf16_trunc(h))
+    assert am == wam and np.array_equal(xn, orc.bf16_bits_to_f32(wxn))
+    # the target restarts from zero state at position 0
+    m.reset()
+    tam, thid = r.forward_token_decode(7, want_hidden=True)
+    wtam, wthid = m.forward([7])
+    assert tam == int(wtam[0]) and np.array_equal(thid.view(np.uint32), wthid[0].view(np.uint32))
+    assert (r.position, r.mtp_position) == (1, 34)
+    r.mtp_reset_state()
+    assert (r.position, r.mtp_position) == (1, 0)
+    # the drafter restarts at position 0 (the oracle's drafter is at 0 after reset)
+    h = rng.standard_normal(5120).astype(np.float32)
+    am, xn = r.mtp_forward_position_decode(9, h)
+    wam, wxn = m.mtp_forward(9, orc.f32_to_bf16_trunc(h))
+    assert am == wam and np.array_equal(xn, orc.bf16_bits_to_f32(wxn))
+    # and the target kept its state and position through the drafter reset
+    tam, thid = r.forward_token_decode(8, want_hidden=True)
+    wtam, wthid = m.forward([8])
+    assert tam == int(wtam[0]) and np.array_equal(thid.view(np.uint32), wthid[0].view(np.uint32))
+    assert (r.position, r.mtp_position, m.position, m.mtp_position) == (2, 1, 2, 1)
+
+
 def test_device_addressing_equals_row_selection(pair):
     pkg, orc, r, m = pair
     r.fill_state(20, CTX_SEED)
@@ -86,6 +121,7 @@ def test_prefill_prompt_then_speculation(pair):
     rng = np.random.default_rng(77)
     prompt = rng.integers(0, VOCAB, 24).astype(np.uint32)
     r.reset_state()
+    r.mtp_reset_state()
     bonus, th, (seed_tok, seed_h) = r.prefill_prompt(prompt)
     assert r.position == r.mtp_position == len(prompt)
     # the same orchestration from the oracle's pieces
@@ -104,6 +140,7 @@ def test_prefill_prompt_then_speculation(pair):
     assert np.sqrt(np.mean((seed_h - ws) ** 2) / np.mean(ws ** 2)) < 3e-2
     # short prompts take the M=1 path (fewer than 4 tokens)
     r.reset_state()
+    r.mtp_reset_state()
     b3, th3, (s3, sh3) = r.prefill_prompt(prompt[:3])
     m.reset()
     seq = [m.forward([int(t)]) for t in prompt[:3]]
@@ -111,6 +148,7 @@ def test_prefill_prompt_then_speculation(pair):
     assert np.array_equal(th3.view(np.uint32), seq[-1][1][0].view(np.uint32))
     # speculative decoding from the prompt state emits the target's greedy stream
     r.reset_state()
+    r.mtp_reset_state()
     bonus, th, (seed_tok, seed_h) = r.prefill_prompt(prompt)
     ck = r.checkpoint_state()
     mck = r.mtp_checkpoint_state()

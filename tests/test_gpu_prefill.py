@@ -105,6 +105,41 @@ def test_gemm_swiglu_equals_separate_gemms(pkg, orc, dev, M, N, K):
     assert np.array_equal(act.read(np.uint16, M * N).reshape(M, N), orc.silu_mul(g, u).reshape(M, N))
 
 
+@pytest.mark.timeout(300)
+def test_gemm_full_model_shapes(pkg, orc, dev):
+    """The config-3 prefill's largest GEMMs at their real shapes against the
+    oracle: the MLP down (2048 x 5120 x 17408) and the gate and up projections
+    (2048 x 17408 x 5120) on the eight-wave 256-wide tile, each within the
+    GEMM tolerance of the smaller shapes; and the gate/up pair with the
+    SwiGLU epilogue (2 x 17408 interleaved outputs) bit-equal to
+    bf16(silu(bf16 g) * bf16 u) of those two GEMMs' outputs."""
+    rng = np.random.default_rng(2048)
+    M, H, I = 2048, 5120, 17408
+
+    def check(got, want, k):
+        rms = np.sqrt(np.mean(want.astype(np.float64) ** 2))
+        assert np.max(np.abs(got - want)) <= 1e-5 * np.sqrt(k / 64) * rms
+        assert np.mean(got.view(np.uint32) == want.view(np.uint32)) >= 0.95
+
+    a = bf16(rng.standard_normal((M, I)).astype(np.float32))
+    dq = DevQ4(dev, *rand_q4(rng, H, I))
+    check(gemm(pkg, dev, a, dq, M, "lisa_q4_gemm_wide"), orc.q4_gemm(a, dq.w, dq.s, dq.b, H, I, M), I)
+    del dq, a
+
+    x = bf16(rng.standard_normal((M, H)).astype(np.float32))
+    gq, uq = DevQ4(dev, *rand_q4(rng, I, H)), DevQ4(dev, *rand_q4(rng, I, H))
+    g = gemm(pkg, dev, x, gq, M, "lisa_q4_gemm_wide")
+    check(g, orc.q4_gemm(x, gq.w, gq.s, gq.b, I, H, M), H)
+    u = gemm(pkg, dev, x, uq, M, "lisa_q4_gemm_wide")
+    check(u, orc.q4_gemm(x, uq.w, uq.s, uq.b, I, H, M), H)
+    xb, act = dev.upload(x), dev.buffer(M * I * 2)
+    p = pkg.GemmParams(a=xb.ptr, w=gq.wbuf.ptr, sb=gq.sbbuf.ptr, m=M, n=I, k=H, ldc=I, w2=uq.wbuf.ptr,
+                       sb2=uq.sbbuf.ptr, act=act.ptr)
+    dev.dispatch("lisa_q4_gemm_swiglu", p, ((I + 127) // 128, (M + pkg.GEMM_TILE_M - 1) // pkg.GEMM_TILE_M),
+                 (pkg.GEMM_THREADS_WIDE,))
+    assert np.array_equal(act.read(np.uint16, M * I), orc.silu_mul(g, u))
+
+
 def rows(pkg, dev, p, gx, m):
     dev.dispatch("lisa_rows", p, (gx, m), (256,))
 
