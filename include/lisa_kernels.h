@@ -128,7 +128,7 @@ typedef struct LisaQmvParams {
  * Kernels: lisa_gdn_recurrence_m{1,3}; grid 48 workgroups x 512 threads, or
  * 48 + 8 n with the L2 prefetch workgroups (pf_* below).
  * Prefill over m rows: lisa_gdn_prep_rows grid (m, 9) x 256, then
- * lisa_gdn_scan_rows grid (48, 4) x 256 (y_out required), then lisa_gdn_out_rows
+ * lisa_gdn_scan_rows grid (48, 8) x 256 (y_out required), then lisa_gdn_out_rows
  * grid (m, 48) x 128; together they equal the decode kernel applied row by row. */
 typedef struct LisaGdnParams {
   const float* conv_out; /* [M][10240] */

@@ -1643,13 +1643,13 @@ DEV void gdn_body(const LisaGdnParams& p) {
 // Prefill over rows, in three launches with the arithmetic of gdn_body:
 // lisa_gdn_prep_rows (grid (m, 9) x 256): normalized q and k of every row and
 //   key head into qk [m][2][2048], beta and decay into gates [m][48][2];
-// lisa_gdn_scan_rows (grid (48, 4) x 256, 32 state rows per workgroup, eight
-//   lanes per row with 16 elements each): the sequential delta-rule scan, with
-//   no barrier in the time loop (each state row only needs the precomputed
-//   inputs), each row's inputs loaded eight rows ahead. A step costs the LDS
-//   bytes that bring every lane its k and q values (1 KB per state row) and
-//   the VALU work of the lane's elements, so the head is spread over four
-//   workgroups and each row over eight lanes;
+// lisa_gdn_scan_rows (grid (48, 8) x 256, 16 state rows per workgroup,
+//   sixteen lanes per row with one run of 8 elements each): the sequential
+//   delta-rule scan, with no barrier in the time loop (each state row only
+//   needs the precomputed inputs), each row's inputs loaded eight rows ahead
+//   and staged eight rows at a time. A step is a chain of dependent VALU work
+//   per row, so the rows are spread over every CU and each lane carries one
+//   run;
 //   readout y (bf16 values) into y_out [m][6144];
 // lisa_gdn_out_rows (grid (m, 48) x 128): gated RMSNorm of y into gated.
 extern "C" __global__ __launch_bounds__(256) void lisa_gdn_prep_rows(LisaGdnParams p) {
@@ -1691,75 +1691,112 @@ DEV void gdn_row_load(const LisaGdnParams& p, int t, int h, int kh, int v, int l
   in.v = p.conv_out[(size_t)t * LISA_GDN_CONV_DIM + 2 * LISA_GDN_KEY_DIM + h * 128 + v];
 }
 
-// Row dot of the scan over a lane's 16 elements (runs 2o, 2o+1 of its row;
-// lane o = 0..7 of the row): the lane adds its two runs, which is
-// (r_4j + r_4j+1) or (r_4j+2 + r_4j+3) of quarter j = o / 2; xor 1 forms the
-// quarter, xor 2 (Q0 + Q1) or (Q2 + Q3), xor 4 the row.
-DEV float gdn_dot16(const float (&S)[16], const float* vec) {
-  float ra = S[0] * vec[0], rb = S[8] * vec[8];
+// Row dot of the scan over a lane's 8 elements (run o of its row; lane o =
+// 0..15 of the row): xor 1 adds the run pairs (r_4j + r_4j+1), xor 2 forms
+// quarter j, then (Q0 + Q1) / (Q2 + Q3) and the row. Each level leaves its
+// groups of 2, 4 and 8 lanes holding one value, so the last two levels take
+// the half-row mirror (lane i <- 7 - i within 8) and the row mirror (lane
+// i <- 15 - i), DPP moves that bring each lane the other group's value as
+// xor 4 and xor 8 do.
+DEV float gdn_dot8(const float (&S)[8], const float* vec) {
+  float r = S[0] * vec[0];
 #pragma unroll
-  for (int e = 1; e < 8; ++e) {
-    ra = lisa_fma(S[e], vec[e], ra);
-    rb = lisa_fma(S[8 + e], vec[8 + e], rb);
-  }
-  float r = ra + rb;
+  for (int e = 1; e < 8; ++e) r = lisa_fma(S[e], vec[e], r);
   r = r + xor_lane<1>(r);
   r = r + xor_lane<2>(r);
-  return r + xor_lane<4>(r);
+  r = r + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(r), 0x141 /* row_half_mirror */, 0xf, 0xf,
+                                                     false));
+  return r + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(r), 0x140 /* row_mirror */, 0xf, 0xf, false));
 }
 
 extern "C" __global__ __launch_bounds__(256) void lisa_gdn_scan_rows(LisaGdnParams p) {
   const int rows = (int)p.m_rows;
   const int h = blockIdx.x, kh = h / (LISA_GDN_VH / LISA_GDN_KH);
-  const int tid = threadIdx.x, v = blockIdx.y * 32 + (tid >> 3), o = tid & 7, lane = tid & 63, wave = tid >> 6;
-  // each wave stages the row's k and q in its own LDS slot (a wave reads only
-  // what it wrote, so no workgroup barrier is needed)
-  __shared__ lisa_f32x4 kqs[4][64];
-  float* srow = p.state + (size_t)h * 128 * 128 + (size_t)v * 128 + 16 * o;
-  float S[16];
+  // sixteen lanes per state row, lane o owning run o (elements 8o .. 8o + 7)
+  const int tid = threadIdx.x, v = blockIdx.y * 16 + (tid >> 4), o = tid & 15, lane = tid & 63, wave = tid >> 6;
+  constexpr int D = 8;
+  // each wave stages D rows' k and q at a time in its own LDS ring (a wave
+  // reads only what it wrote, so no workgroup barrier is needed)
+  __shared__ lisa_f32x4 kqs[4][D][64];
+  float* srow = p.state + (size_t)h * 128 * 128 + (size_t)v * 128 + 8 * o;
+  float S[8];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
+  for (int i = 0; i < 2; ++i) {
     const float4 f = reinterpret_cast<const float4*>(srow)[i];
     S[4 * i] = f.x; S[4 * i + 1] = f.y; S[4 * i + 2] = f.z; S[4 * i + 3] = f.w;
   }
-  auto step = [&](const GdnRowIn& in, int t) {
-    kqs[wave][lane] = in.kq;
-    float kv[16], qv[16];
+  // one row: the state update, and the readout y = q . S, which the next
+  // row's update does not wait for (in a block without branches the compiler
+  // interleaves it with the next row's k . S chain)
+  auto step = [&](int j, lisa_f32x2 g, float vin) -> float {
+    float kv[8], qv[8];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const lisa_f32x4 k4 = kqs[wave][4 * o + i], q4 = kqs[wave][32 + 4 * o + i];
+    for (int i = 0; i < 2; ++i) {
+      const lisa_f32x4 k4 = kqs[wave][j][2 * o + i], q4 = kqs[wave][j][32 + 2 * o + i];
       kv[4 * i] = k4.x; kv[4 * i + 1] = k4.y; kv[4 * i + 2] = k4.z; kv[4 * i + 3] = k4.w;
       qv[4 * i] = q4.x; qv[4 * i + 1] = q4.y; qv[4 * i + 2] = q4.z; qv[4 * i + 3] = q4.w;
     }
-    // the time step on the lane's 16 elements
 #pragma unroll
-    for (int k = 0; k < 16; ++k) S[k] = S[k] * in.g.y;
-    const float pk = gdn_dot16(S, kv);
-    const float delta = (in.v - pk) * in.g.x;
+    for (int k = 0; k < 8; ++k) S[k] = S[k] * g.y;
+    const float pk = gdn_dot8(S, kv);
+    const float delta = (vin - pk) * g.x;
 #pragma unroll
-    for (int k = 0; k < 16; ++k) S[k] = lisa_fma(delta, kv[k], S[k]);
-    const float py = gdn_dot16(S, qv);
-    if (o == 0) p.y_out[(size_t)t * LISA_GDN_VALUE_DIM + h * 128 + v] = lisa_bf16r(py);
+    for (int k = 0; k < 8; ++k) S[k] = lisa_fma(delta, kv[k], S[k]);
+    return lisa_bf16r(gdn_dot8(S, qv));
   };
-  // a ring of eight input sets: row t's inputs are loaded eight rows ahead, so
-  // the scan never waits on a memory round trip
-  constexpr int D = 8;
   GdnRowIn in[D];
 #pragma unroll
   for (int j = 0; j < D; ++j) gdn_row_load(p, min(j, rows - 1), h, kh, v, lane, in[j]);
-  const int full = rows / D * D;
-  for (int t0 = 0; t0 < full; t0 += D) {
+  // a block's readouts are stored at the start of the next block, ahead of
+  // its wait for the inputs, so that wait does not include the stores (loads
+  // and stores share the wave's counter, in issue order)
+  float yo = 0.0f;
+  int ny = 0, ty = 0;
+  auto store_y = [&]() {
+    if ((o & 7) < ny) p.y_out[(size_t)(ty + (o & 7)) * LISA_GDN_VALUE_DIM + h * 128 + v] = yo;
+  };
+  for (int t0 = 0; t0 < rows; t0 += D) {
+    // the previous block (whole: only the last block can be short, and it is
+    // stored after the loop): one store per lane on every path, so the wait
+    // below can count it; the first block has no predecessor and writes into
+    // the lane's own state element, which the final state store overwrites
+    {
+      float* dst = ny == D ? p.y_out + (size_t)(ty + (o & 7)) * LISA_GDN_VALUE_DIM + h * 128 + v : srow;
+      *dst = ny == D ? yo : S[0];
+    }
+    lisa_f32x2 g[D];
+    float vin[D];
 #pragma unroll
     for (int j = 0; j < D; ++j) {
-      step(in[j], t0 + j);
-      gdn_row_load(p, min(t0 + j + D, rows - 1), h, kh, v, lane, in[j]);
+      kqs[wave][j][lane] = in[j].kq;
+      g[j] = in[j].g;
+      vin[j] = in[j].v;
     }
+    wave_lds_fence();
+#pragma unroll
+    for (int j = 0; j < D; ++j) gdn_row_load(p, min(t0 + D + j, rows - 1), h, kh, v, lane, in[j]);
+    const int n = min(D, rows - t0);
+    float y[D];
+    if (n == D) {
+#pragma unroll
+      for (int j = 0; j < D; ++j) y[j] = step(j, g[j], vin[j]);
+    } else {
+#pragma unroll
+      for (int j = 0; j < D; ++j)
+        if (j < n) y[j] = step(j, g[j], vin[j]);
+    }
+    wave_lds_fence();
+    // lanes o and o + 8 of the row store row o % 8's readout (every lane of
+    // the row holds the row's values; the pair writes the same value)
+    yo = y[0];
+#pragma unroll
+    for (int j = 1; j < D; ++j) yo = (o & 7) == j ? y[j] : yo;
+    ny = n;
+    ty = t0;
   }
+  store_y();
 #pragma unroll
-  for (int j = 0; j < D - 1; ++j)
-    if (full + j < rows) step(in[j], full + j);
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < 2; ++i)
     reinterpret_cast<float4*>(srow)[i] = make_float4(S[4 * i], S[4 * i + 1], S[4 * i + 2], S[4 * i + 3]);
 }
 

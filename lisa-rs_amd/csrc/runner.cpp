@@ -2039,7 +2039,7 @@ int prefill_chunk(LisaRunner* r, uint32_t m) {
       g.gates = P.gdn_gates;
       g.y_out = P.gdn_y;
       LISA_TRY(lisa_launch(r->dev, r->gdn_prep_rows, &g, sizeof g, m, 9, 1, 256, 1, 1));
-      LISA_TRY(lisa_launch(r->dev, r->gdn_scan_rows, &g, sizeof g, LISA_GDN_VH, 4, 1, 256, 1, 1));
+      LISA_TRY(lisa_launch(r->dev, r->gdn_scan_rows, &g, sizeof g, LISA_GDN_VH, 8, 1, 256, 1, 1));
       LISA_TRY(lisa_launch(r->dev, r->gdn_out_rows, &g, sizeof g, m, LISA_GDN_VH, 1, 128, 1, 1));
       LISA_TRY(launch_gemm(r, P.gated, m, l.out, P.B));
     } else {

@@ -202,9 +202,10 @@ def test_gdn_conv_rows_bit_exact(pkg, orc, dev, m):
     assert np.array_equal(sb.read(np.uint16, 3 * CV), want_state)
 
 
-def test_gdn_rows_bit_exact(pkg, orc, dev):
-    rng = np.random.default_rng(6)
-    m, CV, VH, HD = 40, 10240, 48, 128
+@pytest.mark.parametrize("m", [40, 43, 5])  # whole, ragged and short blocks of the scan's eight-row staging
+def test_gdn_rows_bit_exact(pkg, orc, dev, m):
+    rng = np.random.default_rng(6 + m)
+    CV, VH, HD = 10240, 48, 128
     qkv = rng.standard_normal((m, CV)).astype(np.float32)
     conv_w = bf16(rng.uniform(-0.5, 0.5, CV * 4).astype(np.float32))
     state = bf16(rng.standard_normal(3 * CV).astype(np.float32))
@@ -228,7 +229,7 @@ def test_gdn_rows_bit_exact(pkg, orc, dev):
                       state=stb.ptr, gated=gb.ptr, y_out=yb.ptr, q_scale=float(np.float32(inv * inv)),
                       k_scale=float(np.float32(inv)), m_rows=m, qk=qkb.ptr, gates=gtb.ptr)
     dev.dispatch("lisa_gdn_prep_rows", p, (m, 9), (256,))
-    dev.dispatch("lisa_gdn_scan_rows", p, (VH, 4), (256,))
+    dev.dispatch("lisa_gdn_scan_rows", p, (VH, 8), (256,))
     dev.dispatch("lisa_gdn_out_rows", p, (m, VH), (128,))
     gated, st, y, _ = orc.gdn_recurrence(co, z, a, b, a_log, dt_bias, nw, s0, m)
     assert np.array_equal(gb.read(np.uint16, m * VH * HD).reshape(m, -1), gated)
