@@ -188,9 +188,10 @@ typedef struct LisaAttnParams {
   uint16_t* gated;     /* [M][6144] bf16 */
   uint32_t capacity;
   uint32_t s_max;
-  /* *_rows (prefill) kernels: normalized rotated queries bf16 [m][24][256]
-   * written by lisa_attn_store_rows, and the row count */
-  uint16_t* query;
+  /* *_rows (prefill) kernels: normalized rotated queries [m][24][256], the
+   * bf16-rounded values as f32, written by lisa_attn_store_rows, and the row
+   * count */
+  float* query;
   uint32_t m_rows;
   uint32_t pad0;
 } LisaAttnParams;
@@ -294,7 +295,7 @@ typedef struct LisaRowsParams {
 
 /* lisa_attn_partial_rows takes LISA_ATT_ROWS_PER_WG rows per workgroup:
  * grid (s_max, 4, ceil(m / LISA_ATT_ROWS_PER_WG)) x LISA_ATT_ROWS_THREADS. */
-#define LISA_ATT_ROWS_PER_WG 8
+#define LISA_ATT_ROWS_PER_WG 16
 #define LISA_ATT_ROWS_THREADS 1024
 
 /* lisa_gdn_conv_rows: causal conv + SiLU over m rows per channel with the

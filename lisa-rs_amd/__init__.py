@@ -107,7 +107,7 @@ GEMM_TILE_M_SMALL = 128  # lisa_q4_gemm_m128 output tile rows (LISA_GEMM_TILE_M_
 GEMM_TILE_N_WIDE = 256  # lisa_q4_gemm_wide (LISA_GEMM_TILE_N_WIDE)
 GEMM_THREADS_WIDE = 512  # lisa_q4_gemm_wide workgroup size (LISA_GEMM_THREADS_WIDE)
 QMV_MAX_MATS = 4  # matrices per q4 launch (LISA_QMV_MAX_MATS)
-ATT_ROWS_PER_WG = 8  # lisa_attn_partial_rows rows per workgroup (LISA_ATT_ROWS_PER_WG)
+ATT_ROWS_PER_WG = 16  # lisa_attn_partial_rows rows per workgroup (LISA_ATT_ROWS_PER_WG)
 ATT_PARTIAL_THREADS = {1: 1024, 3: 1024}  # lisa_attn_partial_m{1,3} workgroup size (LISA_ATT_PARTIAL_THREADS)
 QMV_WIDE_THREADS = 1024  # lisa_qmv_k5120_m{1,3}_prenorm_gateup_wide workgroup size (LISA_QMV_WIDE_THREADS)
 QMV_WIDE_TILES = 17  # 8-row tiles per workgroup of that kernel (LISA_QMV_WIDE_TILES)

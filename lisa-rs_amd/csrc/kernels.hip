@@ -2754,7 +2754,7 @@ extern "C" __global__ __launch_bounds__(256) void lisa_attn_store_rows(LisaAttnP
     const int h = (grp - 1) * 4 + wave;
     head_norm_rope_wave(p.q_proj + (size_t)t * LISA_ATT_Q_OUT + h * 512, p.q_norm_w, pos, lane, o);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) p.query[((size_t)t * LISA_ATT_QH + h) * HD + lane + 64 * j] = lisa_f32_to_bf16(o[j]);
+    for (int j = 0; j < 4; ++j) p.query[((size_t)t * LISA_ATT_QH + h) * HD + lane + 64 * j] = lisa_bf16r(o[j]);
   }
 }
 
@@ -2762,6 +2762,52 @@ extern "C" __global__ __launch_bounds__(256) void lisa_attn_store_rows(LisaAttnP
 //    waves takes one 64-token slice of one KV head for ATT_RB rows (its LDS
 //    allows one workgroup per CU, so the waves that interleave the score and
 //    P.V loops are all in it).
+//
+// The score items take their query values (the same for every lane, lane =
+// token) as scalar operands of the fmas rather than as broadcast LDS reads,
+// which bounded the loop: the query rows are read through the constant
+// address space, whose wave-uniform loads the compiler issues as scalar loads
+// (and waits for itself). The rows are written by the previous launch and not
+// written here.
+typedef __attribute__((address_space(4))) const float* lisa_cfloat_ptr;
+
+// slice_scores2 with the two heads' query rows qa, qb read by scalar loads;
+// the same accumulators, chains and softmax statistics.
+DEV void slice_scores2_sq(lisa_cfloat_ptr qa, lisa_cfloat_ptr qb, const uint16_t* Kt, int kp, int n, int lane,
+                          float* pba, float* pbb, float* mla, float* mlb) {
+  const uint16_t* kr = Kt + lane * kp;
+  float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
+  float b0 = 0.0f, b1 = 0.0f, b2 = 0.0f, b3 = 0.0f;
+#pragma unroll 4
+  for (int d = 0; d < LISA_ATT_HD; d += 8) {
+    const uint4 kk = *reinterpret_cast<const uint4*>(kr + d);
+    const float k0 = lo_bf(kk.x), k1 = hi_bf(kk.x), k2 = lo_bf(kk.y), k3 = hi_bf(kk.y);
+    const float k4 = lo_bf(kk.z), k5 = hi_bf(kk.z), k6 = lo_bf(kk.w), k7 = hi_bf(kk.w);
+    a0 = lisa_fma(qa[d], k0, a0); a1 = lisa_fma(qa[d + 1], k1, a1); a2 = lisa_fma(qa[d + 2], k2, a2);
+    a3 = lisa_fma(qa[d + 3], k3, a3);
+    b0 = lisa_fma(qb[d], k0, b0); b1 = lisa_fma(qb[d + 1], k1, b1); b2 = lisa_fma(qb[d + 2], k2, b2);
+    b3 = lisa_fma(qb[d + 3], k3, b3);
+    a0 = lisa_fma(qa[d + 4], k4, a0); a1 = lisa_fma(qa[d + 5], k5, a1); a2 = lisa_fma(qa[d + 6], k6, a2);
+    a3 = lisa_fma(qa[d + 7], k7, a3);
+    b0 = lisa_fma(qb[d + 4], k4, b0); b1 = lisa_fma(qb[d + 5], k5, b1); b2 = lisa_fma(qb[d + 6], k6, b2);
+    b3 = lisa_fma(qb[d + 7], k7, b3);
+  }
+  const float sa = lane < n ? ((a0 + a1) + (a2 + a3)) * 0.0625f : -INFINITY;
+  const float sb = lane < n ? ((b0 + b1) + (b2 + b3)) * 0.0625f : -INFINITY;
+  const float ma = max64(sa), mb = max64(sb);
+  const float pa = (lane < n) ? lisa_exp2f(1.4426950408889634f * (sa - ma)) : 0.0f;
+  const float pbv = (lane < n) ? lisa_exp2f(1.4426950408889634f * (sb - mb)) : 0.0f;
+  const float da = tree64(pa), db = tree64(pbv);
+  pba[lane] = pa;
+  pbb[lane] = pbv;
+  if (lane == 0) {
+    mla[0] = ma;
+    mla[1] = da;
+    mlb[0] = mb;
+    mlb[1] = db;
+  }
+}
+
 constexpr int ATT_RB = LISA_ATT_ROWS_PER_WG;
 extern "C" __global__ __launch_bounds__(LISA_ATT_ROWS_THREADS) void lisa_attn_partial_rows(LisaAttnParams p) {
   constexpr int T = LISA_ATT_SLICE, HD = LISA_ATT_HD, KP = HD + 8, NT = LISA_ATT_ROWS_THREADS, NW = NT / 64;
@@ -2772,9 +2818,8 @@ extern "C" __global__ __launch_bounds__(LISA_ATT_ROWS_THREADS) void lisa_attn_pa
   if (nr <= 0 || t0 >= base + (uint32_t)(r0 + nr)) return;
   __shared__ __attribute__((aligned(16))) uint16_t Kt[T * KP];
   __shared__ __attribute__((aligned(16))) uint16_t Vt[T * HD];
-  __shared__ __attribute__((aligned(16))) float qv[ATT_RB * 6 * HD];
   __shared__ float pb[ATT_RB * 6 * T];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const size_t cache_base = (size_t)kvh * p.capacity * HD;
   const int nrows = (int)min((uint32_t)T, base + (uint32_t)(r0 + nr) - t0);
   for (int c = tid; c < nrows * (HD / 8); c += NT) {
@@ -2783,10 +2828,6 @@ extern "C" __global__ __launch_bounds__(LISA_ATT_ROWS_THREADS) void lisa_attn_pa
     *reinterpret_cast<uint4*>(&Kt[row * KP + col]) = *reinterpret_cast<const uint4*>(p.key_cache + off);
     *reinterpret_cast<uint4*>(&Vt[row * HD + col]) = *reinterpret_cast<const uint4*>(p.value_cache + off);
   }
-  for (int e = tid; e < nr * 6 * HD; e += NT) {
-    const int tt = e / (6 * HD), i = (e / HD) % 6, d = e % HD;
-    qv[e] = bf2f(p.query[((size_t)(r0 + tt) * LISA_ATT_QH + kvh * 6 + i) * HD + d]);
-  }
   __syncthreads();
   // scores: item (row tt, head pair) per wave, as the decode partial
   for (int it = wave; it < nr * 3; it += NW) {
@@ -2794,10 +2835,10 @@ extern "C" __global__ __launch_bounds__(LISA_ATT_ROWS_THREADS) void lisa_attn_pa
     const uint32_t ctx = base + t + 1;
     if (ctx <= t0) continue;
     const int n = (int)min((uint32_t)T, ctx - t0);
-    const float* qa = qv + (tt * 6 + i) * HD;
+    const lisa_cfloat_ptr qa = (lisa_cfloat_ptr)(p.query + ((size_t)t * LISA_ATT_QH + h) * HD);
     float* ml = p.part_ml + (((size_t)t * LISA_ATT_QH + h) * p.s_max + s) * 2;
-    slice_scores2(qa, qa + HD, Kt, KP, n, lane, pb + (tt * 6 + i) * T, pb + (tt * 6 + i + 1) * T, ml,
-                  ml + (size_t)p.s_max * 2);
+    slice_scores2_sq(qa, qa + HD, Kt, KP, n, lane, pb + (tt * 6 + i) * T, pb + (tt * 6 + i + 1) * T, ml,
+                     ml + (size_t)p.s_max * 2);
   }
   __syncthreads();
   // P.V: thread (dp, hg, rr) owns dimensions 2dp, 2dp+1 of heads 3hg..3hg+2

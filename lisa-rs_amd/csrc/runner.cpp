@@ -153,7 +153,8 @@ struct LisaRunner {
     LisaBuffer* buf = nullptr;
     uint32_t att_rows = 0;  // rows per attention sub-block (bounds the slice partials)
     uint32_t *tokens = nullptr, *argmax = nullptr, *pos = nullptr;
-    uint16_t *H = nullptr, *X = nullptr, *gated = nullptr, *act = nullptr, *query = nullptr;
+    uint16_t *H = nullptr, *X = nullptr, *gated = nullptr, *act = nullptr;
+    float* query = nullptr;
     float *B = nullptr, *qkv = nullptr, *conv_out = nullptr, *z = nullptr, *a = nullptr, *b = nullptr;
     float *q_proj = nullptr, *k_raw = nullptr, *v_raw = nullptr, *logits = nullptr;
     float *part_o = nullptr, *part_ml = nullptr;
@@ -1800,7 +1801,7 @@ void plan_prefill(LisaRunner* r, Arena& A) {
   P.q_proj = A.take<float>(c * LISA_ATT_Q_OUT);
   P.k_raw = A.take<float>(c * LISA_ATT_KV_OUT);
   P.v_raw = A.take<float>(c * LISA_ATT_KV_OUT);
-  P.query = A.take<uint16_t>(c * LISA_ATT_OUT);
+  P.query = A.take<float>(c * LISA_ATT_OUT);
   P.act = A.take<uint16_t>(c * LISA_INTER);
   P.logits = A.take<float>(c * (size_t)r->cfg.vocab);
   P.gdn_qk = A.take<float>(c * 2 * LISA_GDN_KEY_DIM);

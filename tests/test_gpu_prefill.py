@@ -237,9 +237,9 @@ def test_gdn_rows_bit_exact(pkg, orc, dev, m):
     assert np.array_equal(yb.read(np.float32, m * VH * HD).reshape(m, -1).view(np.uint32), y.view(np.uint32))
 
 
-def test_attention_rows_bit_exact(pkg, orc, dev):
-    rng = np.random.default_rng(8)
-    m, cap, base = 70, 200, 90
+@pytest.mark.parametrize("m,cap,base", [(70, 200, 90), (33, 64, 0), (16, 300, 200)])
+def test_attention_rows_bit_exact(pkg, orc, dev, m, cap, base):
+    rng = np.random.default_rng(8 + m)
     q_proj = (rng.standard_normal((m, 12288)) * 2).astype(np.float32)
     k_raw = rng.standard_normal((m, 1024)).astype(np.float32)
     v_raw = rng.standard_normal((m, 1024)).astype(np.float32)
@@ -249,7 +249,7 @@ def test_attention_rows_bit_exact(pkg, orc, dev):
     s_max = (cap + 63) // 64
     bufs = {n: dev.upload(x) for n, x in dict(q=q_proj, k=k_raw, v=v_raw, qn=qn, kn=kn, kc=kc, vc=vc,
                                               pos=np.array([base], np.uint32)).items()}
-    query, gated = dev.buffer(m * 6144 * 2), dev.buffer(m * 6144 * 2)
+    query, gated = dev.buffer(m * 6144 * 4), dev.buffer(m * 6144 * 2)
     po, pml = dev.buffer(m * 24 * s_max * 256 * 4), dev.buffer(m * 24 * s_max * 2 * 4)
     p = pkg.AttnParams(q_proj=bufs["q"].ptr, k_raw=bufs["k"].ptr, v_raw=bufs["v"].ptr, q_norm_w=bufs["qn"].ptr,
                        k_norm_w=bufs["kn"].ptr, key_cache=bufs["kc"].ptr, value_cache=bufs["vc"].ptr, part_o=po.ptr,
