@@ -140,10 +140,18 @@ struct LisaRunner {
   MtpDev mtp{};
   int gdn_layers = 0, attn_layers = 0;
   uint32_t s_max = 0;
+  // GDN and conv state in three rotating buffers: buffer `live` holds the
+  // state, the other two (in index order) receive a verification's rows 1
+  // and 2, and committing one or two rows makes that buffer the live one
+  // instead of copying it back (the derived pointers follow set_live)
+  float* gdn_buf[3] = {};
+  uint16_t* conv_buf[3] = {};
+  int live = 0;
   float* gdn_state = nullptr;
   uint16_t* conv_state = nullptr;
-  float* gdn_slots = nullptr;
+  float* gdn_slots = nullptr;  // slot 0; slot 1 is gdn_slot_stride floats further
   uint16_t* conv_slots = nullptr;
+  uint64_t gdn_slot_stride = 0, conv_slot_stride = 0;
   uint16_t *key_cache = nullptr, *value_cache = nullptr;
   uint16_t *mtp_key = nullptr, *mtp_value = nullptr;
   Ctx tgt{}, drf{};
@@ -519,12 +527,30 @@ int upload_catalogue(LisaRunner* r, const LisaWeightIndex* idx, const std::vecto
 
 void plan_mtp_state(LisaRunner* r, Arena& A);
 
+// The verification slots of live buffer k: the other two buffers, in index order.
+int slot_buf(int k, int row) { return row == 0 ? (k == 0 ? 1 : 0) : (k == 2 ? 1 : 2); }
+
+void set_live(LisaRunner* r, int k) {
+  const int s0 = slot_buf(k, 0), s1 = slot_buf(k, 1);
+  r->live = k;
+  r->gdn_state = r->gdn_buf[k];
+  r->conv_state = r->conv_buf[k];
+  r->gdn_slots = r->gdn_buf[s0];
+  r->conv_slots = r->conv_buf[s0];
+  r->gdn_slot_stride = (uint64_t)(s1 - s0) * r->gdn_layers * LISA_GDN_STATE;
+  r->conv_slot_stride = (uint64_t)(s1 - s0) * r->gdn_layers * 3 * LISA_GDN_CONV_DIM;
+}
+
 void plan_state(LisaRunner* r, Arena& A) {
   const size_t cap = (size_t)r->cfg.capacity;
-  r->gdn_state = A.take<float>((size_t)r->gdn_layers * LISA_GDN_STATE);
-  r->conv_state = A.take<uint16_t>((size_t)r->gdn_layers * 3 * LISA_GDN_CONV_DIM);
-  r->gdn_slots = A.take<float>((size_t)2 * r->gdn_layers * LISA_GDN_STATE);
-  r->conv_slots = A.take<uint16_t>((size_t)2 * r->gdn_layers * 3 * LISA_GDN_CONV_DIM);
+  const size_t gs = (size_t)r->gdn_layers * LISA_GDN_STATE, cs = (size_t)r->gdn_layers * 3 * LISA_GDN_CONV_DIM;
+  float* g = A.take<float>(3 * gs);
+  uint16_t* c = A.take<uint16_t>(3 * cs);
+  for (int k = 0; k < 3; ++k) {
+    r->gdn_buf[k] = g ? g + k * gs : nullptr;
+    r->conv_buf[k] = c ? c + k * cs : nullptr;
+  }
+  set_live(r, 0);
   r->key_cache = A.take<uint16_t>((size_t)r->attn_layers * LISA_ATT_KVH * cap * LISA_ATT_HD);
   r->value_cache = A.take<uint16_t>((size_t)r->attn_layers * LISA_ATT_KVH * cap * LISA_ATT_HD);
   if (r->cfg.with_mtp) plan_mtp_state(r, A);
@@ -733,7 +759,7 @@ int encode_target(LisaRunner* r, int m, bool capture, bool feedback, uint32_t sl
       p.conv_w = l.conv_w;
       p.conv_state = r->conv_state + (size_t)si * 3 * LISA_GDN_CONV_DIM;
       p.conv_slots = capture ? r->conv_slots + (size_t)si * 3 * LISA_GDN_CONV_DIM : nullptr;
-      p.conv_slot_stride = (uint64_t)r->gdn_layers * 3 * LISA_GDN_CONV_DIM;
+      p.conv_slot_stride = r->conv_slot_stride;
       p.capture = capture ? 1 : 0;
       // a and b leave the tile list: the first 48 workgroups form their group
       // contributions, which the recurrence sums (512 workgroups, not 515)
@@ -754,7 +780,7 @@ int encode_target(LisaRunner* r, int m, bool capture, bool feedback, uint32_t sl
       g.norm_w = l.gnorm;
       g.state = r->gdn_state + (size_t)si * LISA_GDN_STATE;
       g.slots = capture ? r->gdn_slots + (size_t)si * LISA_GDN_STATE : nullptr;
-      g.slot_stride = (uint64_t)r->gdn_layers * LISA_GDN_STATE;
+      g.slot_stride = r->gdn_slot_stride;
       g.gated = c.gated;
       g.q_scale = inv * inv;
       g.k_scale = inv;
@@ -881,13 +907,16 @@ int cached_graph(LisaRunner* r, std::map<uint32_t, LisaGraph*>& cache, uint32_t 
 // position `pos`: recorded on first use for its slice bucket.
 int step_graph_for(LisaRunner* r, uint32_t pos, LisaGraph** out) {
   const uint32_t slices = att_slices(r, pos, true);
-  return cached_graph(r, r->step_graphs, slices, [&] { return encode_target(r, 1, false, true, slices); }, out);
+  // the captured pointers name the live state buffer: one graph per buffer
+  return cached_graph(r, r->step_graphs, slices * 4 + (uint32_t)r->live,
+                      [&] { return encode_target(r, 1, false, true, slices); }, out);
 }
 
 // The captured M=3 verification whose last row sits at `last_pos`.
 int verify_graph_for(LisaRunner* r, uint32_t last_pos, LisaGraph** out) {
   const uint32_t slices = att_slices(r, last_pos, true);
-  return cached_graph(r, r->verify_graphs, slices, [&] { return encode_target(r, 3, true, false, slices); }, out);
+  return cached_graph(r, r->verify_graphs, slices * 4 + (uint32_t)r->live,
+                      [&] { return encode_target(r, 3, true, false, slices); }, out);
 }
 
 // The captured drafter step at the drafter's position, conditioned on `cond`
@@ -915,9 +944,9 @@ int launch_verify(LisaRunner* r) {
   return LISA_OK;
 }
 
-// commit_verified_prefix's device work (the GDN and conv states of row
-// rows - 1 from their slots) and host position; the caller writes the device
-// position.
+// commit_verified_prefix's host work: the GDN and conv states of row rows - 1
+// are already in their slot buffer, which becomes the live one (no device
+// copy); the caller writes the device position.
 int commit_enqueue(LisaRunner* r, int32_t rows) {
   if (r->verify_base < 0) return lisa_fail(LISA_E_STATE, "no pending block-3 verification");
   if (rows < 1 || rows > 3) {
@@ -926,16 +955,7 @@ int commit_enqueue(LisaRunner* r, int32_t rows) {
   }
   const uint32_t base = (uint32_t)r->verify_base;
   r->verify_base = -1;
-  if (rows < 3) {
-    const size_t gs = (size_t)r->gdn_layers * LISA_GDN_STATE;
-    const size_t cs = (size_t)r->gdn_layers * 3 * LISA_GDN_CONV_DIM;
-    LISA_TRY(lisa_hip_check(hipMemcpyAsync(r->gdn_state, r->gdn_slots + (size_t)(rows - 1) * gs, gs * 4,
-                                           hipMemcpyDeviceToDevice, r->dev->stream),
-                            "D2D gdn slot"));
-    LISA_TRY(lisa_hip_check(hipMemcpyAsync(r->conv_state, r->conv_slots + (size_t)(rows - 1) * cs, cs * 2,
-                                           hipMemcpyDeviceToDevice, r->dev->stream),
-                            "D2D conv slot"));
-  }
+  if (rows < 3) set_live(r, slot_buf(r->live, rows - 1));
   r->position = base + (uint32_t)rows;
   return LISA_OK;
 }
@@ -1271,7 +1291,7 @@ namespace {
 // range of the state arena (plan_state), zeroed and the position rewound.
 int clear_target(LisaRunner* r) {
   const size_t kv = (size_t)r->attn_layers * LISA_ATT_KVH * (size_t)r->cfg.capacity * LISA_ATT_HD;
-  char* lo = reinterpret_cast<char*>(r->gdn_state);
+  char* lo = reinterpret_cast<char*>(r->gdn_buf[0]);
   char* hi = reinterpret_cast<char*>(r->value_cache + kv);
   LISA_TRY(lisa_hip_check(hipMemsetAsync(lo, 0, (size_t)(hi - lo), r->dev->stream), "memset state"));
   LISA_TRY(write_pos(r, r->tgt, 0));

@@ -80,6 +80,38 @@ def test_verify_commit_matches_oracle(pair, rows):
         tok = a1
 
 
+def test_commit_sequence_rotates_state_buffers(pair):
+    """A run of verifications with commits of 1, 2, 1, 3, 2, 2 and 1 rows: a
+    commit of one or two rows makes that row's slot buffer the live GDN/conv
+    state (three rotating buffers, no copy), so the sequence visits every live
+    buffer and every graph captured for one; after each commit the next
+    verification, then the final M=1 steps, match the oracle bit for bit, and
+    so does every GDN layer's state."""
+    pkg, orc, r, m = pair
+    fresh(r, m, filled=50)
+    rng = np.random.default_rng(31)
+    for rows in (1, 2, 1, 3, 2, 2, 1):
+        toks = [int(t) for t in rng.integers(0, VOCAB, 3)]
+        am, hid = r.verify_block3(toks, want_hidden=True)
+        wam, whid = m.forward(toks, capture=True)
+        assert list(am) == list(wam)
+        assert np.array_equal(hid.view(np.uint32), whid.view(np.uint32))
+        r.commit_verified_prefix(rows)
+        m.commit(rows)
+        assert r.position == m.position
+    tok = 77
+    for _ in range(3):
+        a1, h1 = r.forward_token_decode(tok, want_hidden=True)
+        w1, wh1 = m.forward([tok])
+        assert a1 == int(w1[0]) and np.array_equal(h1.view(np.uint32), wh1[0].view(np.uint32))
+        tok = a1
+    for idx in range(LAYERS * 3 // 4):  # GDN layer idx is model layer idx + idx // 3
+        scope = idx + idx // 3 + 1
+        want = m.tensor(scope, orc.T["GDN_STATE"], 0, np.float32)
+        assert np.array_equal(r.gdn_state(idx).view(np.uint32), want.view(np.uint32)), idx
+        assert np.array_equal(r.conv_state(idx), m.tensor(scope, orc.T["CONV_STATE"], 0, np.uint16)), idx
+
+
 def test_verify_row_equals_decode(pair):
     """runner_checkpoint.rs invariant: row t of an M=3 verify equals M=1
     decoding of the same tokens (bit-exact here: identical per-row order)."""
