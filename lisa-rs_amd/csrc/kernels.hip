@@ -1644,12 +1644,12 @@ DEV void gdn_body(const LisaGdnParams& p) {
 // lisa_gdn_prep_rows (grid (m, 9) x 256): normalized q and k of every row and
 //   key head into qk [m][2][2048], beta and decay into gates [m][48][2];
 // lisa_gdn_scan_rows (grid (48, 8) x 256, 16 state rows per workgroup,
-//   sixteen lanes per row with one run of 8 elements each): the sequential
-//   delta-rule scan, with no barrier in the time loop (each state row only
-//   needs the precomputed inputs), each row's inputs loaded eight rows ahead
-//   and staged eight rows at a time. A step is a chain of dependent VALU work
-//   per row, so the rows are spread over every CU and each lane carries one
-//   run;
+//   sixteen lanes per state row with one run of 8 elements each): the
+//   sequential delta-rule scan, with no barrier in the time loop (each state
+//   row only needs the precomputed inputs), each time step's inputs loaded
+//   eight steps ahead and staged eight steps at a time. A step is a chain of
+//   dependent VALU work per state row, so the rows are spread over every CU
+//   and each lane carries one run;
 //   readout y (bf16 values) into y_out [m][6144];
 // lisa_gdn_out_rows (grid (m, 48) x 128): gated RMSNorm of y into gated.
 extern "C" __global__ __launch_bounds__(256) void lisa_gdn_prep_rows(LisaGdnParams p) {
@@ -1673,131 +1673,229 @@ extern "C" __global__ __launch_bounds__(256) void lisa_gdn_prep_rows(LisaGdnPara
 
 // Per-row inputs of the scan as one lane sees them: its 16 B of the row's k
 // (lanes 0-31) or q (lanes 32-63) of the key head, the head's (beta, decay) and
-// the state row's v value.
+// the v values of the lane's R state rows (v0 + 16 r).
 // (native vector types: HIP's float4 struct copies lower to memcpy, which keeps
 // an array of these out of registers)
 typedef float lisa_f32x4 __attribute__((ext_vector_type(4)));
 typedef float lisa_f32x2 __attribute__((ext_vector_type(2)));
+template <int R>
 struct GdnRowIn {
   lisa_f32x4 kq;
   lisa_f32x2 g;
-  float v;
+  float v[R];
 };
 
-DEV void gdn_row_load(const LisaGdnParams& p, int t, int h, int kh, int v, int lane, GdnRowIn& in) {
+// state rows v0 + 16 r, r < R
+template <int R>
+DEV void gdn_row_load(const LisaGdnParams& p, int t, int h, int kh, int v0, int lane, GdnRowIn<R>& in) {
   const int which = lane < 32 ? 1 : 0;  // k, then q
   in.kq = reinterpret_cast<const lisa_f32x4*>(p.qk + ((size_t)t * 2 + which) * LISA_GDN_KEY_DIM + kh * 128)[lane & 31];
   in.g = reinterpret_cast<const lisa_f32x2*>(p.gates)[(size_t)t * LISA_GDN_VH + h];
-  in.v = p.conv_out[(size_t)t * LISA_GDN_CONV_DIM + 2 * LISA_GDN_KEY_DIM + h * 128 + v];
-}
-
-// Row dot of the scan over a lane's 8 elements (run o of its row; lane o =
-// 0..15 of the row): xor 1 adds the run pairs (r_4j + r_4j+1), xor 2 forms
-// quarter j, then (Q0 + Q1) / (Q2 + Q3) and the row. Each level leaves its
-// groups of 2, 4 and 8 lanes holding one value, so the last two levels take
-// the half-row mirror (lane i <- 7 - i within 8) and the row mirror (lane
-// i <- 15 - i), DPP moves that bring each lane the other group's value as
-// xor 4 and xor 8 do.
-DEV float gdn_dot8(const float (&S)[8], const float* vec) {
-  float r = S[0] * vec[0];
+  const float* vr = p.conv_out + (size_t)t * LISA_GDN_CONV_DIM + 2 * LISA_GDN_KEY_DIM + h * 128 + v0;
 #pragma unroll
-  for (int e = 1; e < 8; ++e) r = lisa_fma(S[e], vec[e], r);
-  r = r + xor_lane<1>(r);
-  r = r + xor_lane<2>(r);
-  r = r + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(r), 0x141 /* row_half_mirror */, 0xf, 0xf,
-                                                     false));
-  return r + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(r), 0x140 /* row_mirror */, 0xf, 0xf, false));
+  for (int r = 0; r < R; ++r) in.v[r] = vr[16 * r];
 }
 
+// N row dots of the scan, each over a lane's 8 elements (run o of its row;
+// lane o = 0..15 of the row): xor 1 adds the run pairs (r_4j + r_4j+1), xor 2
+// forms quarter j, then (Q0 + Q1) / (Q2 + Q3) and the row. Each level leaves
+// its groups of 2, 4 and 8 lanes holding one value, so the last two levels
+// take the half-row mirror (lane i <- 7 - i within 8) and the row mirror (lane
+// i <- 15 - i), DPP moves that bring each lane the other group's value as
+// xor 4 and xor 8 do. The N chains are interleaved statement by statement: a
+// wave issues in order, so each chain's dependent-latency gaps hold the
+// others' instructions; each result is the same bits as alone.
+template <int N>
+DEV void gdn_dot8_n(const float (&X)[N][8], const float (&V)[N][8], float (&res)[N]) {
+  float a[N];
+#pragma unroll
+  for (int n = 0; n < N; ++n) a[n] = X[n][0] * V[n][0];
+#pragma unroll
+  for (int e = 1; e < 8; ++e)
+#pragma unroll
+    for (int n = 0; n < N; ++n) a[n] = lisa_fma(X[n][e], V[n][e], a[n]);
+#pragma unroll
+  for (int n = 0; n < N; ++n) a[n] = a[n] + xor_lane<1>(a[n]);
+#pragma unroll
+  for (int n = 0; n < N; ++n) a[n] = a[n] + xor_lane<2>(a[n]);
+#pragma unroll
+  for (int n = 0; n < N; ++n)
+    a[n] = a[n] + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(a[n]), 0x141 /* row_half_mirror */,
+                                                             0xf, 0xf, false));
+#pragma unroll
+  for (int n = 0; n < N; ++n)
+    res[n] = a[n] + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(a[n]), 0x140 /* row_mirror */, 0xf,
+                                                               0xf, false));
+}
+
+// Grid (48 value heads, 8) x 256 threads: sixteen lanes per state row of the
+// head (lane o owning run o, elements 8o .. 8o + 7), four rows per wave, 1536
+// waves. (R rows per lane, v and v + 16, with grid (48, 8 / R) runs each
+// row's arithmetic unchanged; two per lane, one wave per SIMD, measured
+// slower than two one-row waves sharing a SIMD.)
 extern "C" __global__ __launch_bounds__(256) void lisa_gdn_scan_rows(LisaGdnParams p) {
+  constexpr int R = 1, D = 8;
   const int rows = (int)p.m_rows;
   const int h = blockIdx.x, kh = h / (LISA_GDN_VH / LISA_GDN_KH);
-  // sixteen lanes per state row, lane o owning run o (elements 8o .. 8o + 7)
-  const int tid = threadIdx.x, v = blockIdx.y * 16 + (tid >> 4), o = tid & 15, lane = tid & 63, wave = tid >> 6;
-  constexpr int D = 8;
+  const int tid = threadIdx.x, o = tid & 15, lane = tid & 63, wave = tid >> 6;
+  const int v0 = blockIdx.y * 16 * R + (tid >> 4);
   // each wave stages D rows' k and q at a time in its own LDS ring (a wave
   // reads only what it wrote, so no workgroup barrier is needed)
   __shared__ lisa_f32x4 kqs[4][D][64];
-  float* srow = p.state + (size_t)h * 128 * 128 + (size_t)v * 128 + 8 * o;
-  float S[8];
+  float* srow[R];
+  float S[R][8];
 #pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    const float4 f = reinterpret_cast<const float4*>(srow)[i];
-    S[4 * i] = f.x; S[4 * i + 1] = f.y; S[4 * i + 2] = f.z; S[4 * i + 3] = f.w;
-  }
-  // one row: the state update, and the readout y = q . S, which the next
-  // row's update does not wait for (in a block without branches the compiler
-  // interleaves it with the next row's k . S chain)
-  auto step = [&](int j, lisa_f32x2 g, float vin) -> float {
-    float kv[8], qv[8];
+  for (int r = 0; r < R; ++r) {
+    srow[r] = p.state + (size_t)h * 128 * 128 + (size_t)(v0 + 16 * r) * 128 + 8 * o;
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
-      const lisa_f32x4 k4 = kqs[wave][j][2 * o + i], q4 = kqs[wave][j][32 + 2 * o + i];
-      kv[4 * i] = k4.x; kv[4 * i + 1] = k4.y; kv[4 * i + 2] = k4.z; kv[4 * i + 3] = k4.w;
-      qv[4 * i] = q4.x; qv[4 * i + 1] = q4.y; qv[4 * i + 2] = q4.z; qv[4 * i + 3] = q4.w;
+      const float4 f = reinterpret_cast<const float4*>(srow[r])[i];
+      S[r][4 * i] = f.x; S[r][4 * i + 1] = f.y; S[r][4 * i + 2] = f.z; S[r][4 * i + 3] = f.w;
     }
+  }
+  auto rd = [&](int j, int off, float (&dst)[8]) {
 #pragma unroll
-    for (int k = 0; k < 8; ++k) S[k] = S[k] * g.y;
-    const float pk = gdn_dot8(S, kv);
-    const float delta = (vin - pk) * g.x;
-#pragma unroll
-    for (int k = 0; k < 8; ++k) S[k] = lisa_fma(delta, kv[k], S[k]);
-    return lisa_bf16r(gdn_dot8(S, qv));
+    for (int i = 0; i < 2; ++i) {
+      const lisa_f32x4 f = kqs[wave][j][off + 2 * o + i];
+      dst[4 * i] = f.x; dst[4 * i + 1] = f.y; dst[4 * i + 2] = f.z; dst[4 * i + 3] = f.w;
+    }
   };
-  GdnRowIn in[D];
+  // one time step of both rows: the state update and the readout y = q . S
+  auto step = [&](int j, lisa_f32x2 g, const float (&vin)[R], float (&yo)[R]) {
+    float kv[8], qv[8];
+    rd(j, 0, kv);
+    rd(j, 32, qv);
+    float K[R][8], Q[R][8], pk[R];
 #pragma unroll
-  for (int j = 0; j < D; ++j) gdn_row_load(p, min(j, rows - 1), h, kh, v, lane, in[j]);
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        S[r][k] = S[r][k] * g.y;
+        K[r][k] = kv[k];
+        Q[r][k] = qv[k];
+      }
+    gdn_dot8_n<R>(S, K, pk);
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const float delta = (vin[r] - pk[r]) * g.x;
+#pragma unroll
+      for (int k = 0; k < 8; ++k) S[r][k] = lisa_fma(delta, kv[k], S[r][k]);
+    }
+    gdn_dot8_n<R>(S, Q, yo);
+#pragma unroll
+    for (int r = 0; r < R; ++r) yo[r] = lisa_bf16r(yo[r]);
+  };
+  GdnRowIn<R> in[D];
+#pragma unroll
+  for (int j = 0; j < D; ++j) gdn_row_load<R>(p, min(j, rows - 1), h, kh, v0, lane, in[j]);
   // a block's readouts are stored at the start of the next block, ahead of
   // its wait for the inputs, so that wait does not include the stores (loads
-  // and stores share the wave's counter, in issue order)
+  // and stores share the wave's counter, in issue order); lane o stores time
+  // step o % 8's readout of state row v0 + 16 ((o / 8) % R) (at R = 1 lanes o
+  // and o + 8 store the same value)
+  const int sj = o & 7, sr = (o >> 3) % R;
   float yo = 0.0f;
   int ny = 0, ty = 0;
-  auto store_y = [&]() {
-    if ((o & 7) < ny) p.y_out[(size_t)(ty + (o & 7)) * LISA_GDN_VALUE_DIM + h * 128 + v] = yo;
-  };
+  float* ycol = p.y_out + h * 128 + v0 + 16 * sr;
   for (int t0 = 0; t0 < rows; t0 += D) {
     // the previous block (whole: only the last block can be short, and it is
     // stored after the loop): one store per lane on every path, so the wait
     // below can count it; the first block has no predecessor and writes into
     // the lane's own state element, which the final state store overwrites
     {
-      float* dst = ny == D ? p.y_out + (size_t)(ty + (o & 7)) * LISA_GDN_VALUE_DIM + h * 128 + v : srow;
-      *dst = ny == D ? yo : S[0];
+      float* dst = ny == D ? ycol + (size_t)(ty + sj) * LISA_GDN_VALUE_DIM : srow[0];
+      *dst = ny == D ? yo : S[0][0];
     }
     lisa_f32x2 g[D];
-    float vin[D];
+    float vin[D][R];
 #pragma unroll
     for (int j = 0; j < D; ++j) {
       kqs[wave][j][lane] = in[j].kq;
       g[j] = in[j].g;
-      vin[j] = in[j].v;
+#pragma unroll
+      for (int r = 0; r < R; ++r) vin[j][r] = in[j].v[r];
     }
     wave_lds_fence();
 #pragma unroll
-    for (int j = 0; j < D; ++j) gdn_row_load(p, min(t0 + D + j, rows - 1), h, kh, v, lane, in[j]);
+    for (int j = 0; j < D; ++j) gdn_row_load<R>(p, min(t0 + D + j, rows - 1), h, kh, v0, lane, in[j]);
     const int n = min(D, rows - t0);
-    float y[D];
+    float y[D][R];
     if (n == D) {
+      // step() software-pipelined: time step j's k . S chains run beside time
+      // step j - 1's readouts (both read only the state after step j - 1),
+      // and step j + 1's k and step j's q come from LDS while step j computes
+      float kc[8], kn[8], qc[8], qp[8];
+      rd(0, 0, kc);
 #pragma unroll
-      for (int j = 0; j < D; ++j) y[j] = step(j, g[j], vin[j]);
+      for (int j = 0; j < D; ++j) {
+        if (j + 1 < D) rd(j + 1, 0, kn);
+        rd(j, 32, qc);
+        float X[2 * R][8], V[2 * R][8], res[2 * R];
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+#pragma unroll
+          for (int k = 0; k < 8; ++k) {
+            X[R + r][k] = S[r][k];  // the state after step j - 1, for its readout
+            S[r][k] = S[r][k] * g[j].y;
+            X[r][k] = S[r][k];
+            V[r][k] = kc[k];
+            V[R + r][k] = qp[k];
+          }
+        if (j == 0) {
+          float pk[R];
+          float XK[R][8], VK[R][8];
+#pragma unroll
+          for (int r = 0; r < R; ++r)
+#pragma unroll
+            for (int k = 0; k < 8; ++k) { XK[r][k] = X[r][k]; VK[r][k] = V[r][k]; }
+          gdn_dot8_n<R>(XK, VK, pk);
+#pragma unroll
+          for (int r = 0; r < R; ++r) res[r] = pk[r];
+        } else {
+          gdn_dot8_n<2 * R>(X, V, res);
+#pragma unroll
+          for (int r = 0; r < R; ++r) y[j - 1][r] = lisa_bf16r(res[R + r]);
+        }
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+          const float delta = (vin[j][r] - res[r]) * g[j].x;
+#pragma unroll
+          for (int k = 0; k < 8; ++k) S[r][k] = lisa_fma(delta, kc[k], S[r][k]);
+        }
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+          qp[k] = qc[k];
+          if (j + 1 < D) kc[k] = kn[k];
+        }
+      }
+      float Q[R][8], yl[R];
+#pragma unroll
+      for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int k = 0; k < 8; ++k) Q[r][k] = qp[k];
+      gdn_dot8_n<R>(S, Q, yl);
+#pragma unroll
+      for (int r = 0; r < R; ++r) y[D - 1][r] = lisa_bf16r(yl[r]);
     } else {
 #pragma unroll
       for (int j = 0; j < D; ++j)
-        if (j < n) y[j] = step(j, g[j], vin[j]);
+        if (j < n) step(j, g[j], vin[j], y[j]);
     }
     wave_lds_fence();
-    // lanes o and o + 8 of the row store row o % 8's readout (every lane of
-    // the row holds the row's values; the pair writes the same value)
-    yo = y[0];
+    yo = y[0][0];
 #pragma unroll
-    for (int j = 1; j < D; ++j) yo = (o & 7) == j ? y[j] : yo;
+    for (int j = 0; j < D; ++j)
+#pragma unroll
+      for (int r = 0; r < R; ++r) yo = (sj == j && sr == r) ? y[j][r] : yo;
     ny = n;
     ty = t0;
   }
-  store_y();
+  if (sj < ny) ycol[(size_t)(ty + sj) * LISA_GDN_VALUE_DIM] = yo;
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
-    reinterpret_cast<float4*>(srow)[i] = make_float4(S[4 * i], S[4 * i + 1], S[4 * i + 2], S[4 * i + 3]);
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+      reinterpret_cast<float4*>(srow[r])[i] = make_float4(S[r][4 * i], S[r][4 * i + 1], S[r][4 * i + 2], S[r][4 * i + 3]);
 }
 
 extern "C" __global__ __launch_bounds__(128) void lisa_gdn_out_rows(LisaGdnParams p) {
