@@ -2869,40 +2869,65 @@ extern "C" __global__ __launch_bounds__(256) void lisa_attn_store_rows(LisaAttnP
 // written here.
 typedef __attribute__((address_space(4))) const float* lisa_cfloat_ptr;
 
-// slice_scores2 with the two heads' query rows qa, qb read by scalar loads;
-// the same accumulators, chains and softmax statistics.
-DEV void slice_scores2_sq(lisa_cfloat_ptr qa, lisa_cfloat_ptr qb, const uint16_t* Kt, int kp, int n, int lane,
-                          float* pba, float* pbb, float* mla, float* mlb) {
+// The slice scores of all six query heads of a KV head for one row, query
+// values read by scalar loads from q (the six heads' rows, contiguous): each
+// head's four accumulators, chains and softmax statistics are slice_scores2's;
+// one conversion of a K element serves the six heads. pb: [6][T]; the
+// statistics of head i at ml + i * mls.
+DEV void slice_scores6_sq(lisa_cfloat_ptr q, const uint16_t* Kt, int kp, int n, int lane, float* pb, float* ml,
+                          size_t mls) {
+  constexpr int HD = LISA_ATT_HD;
   const uint16_t* kr = Kt + lane * kp;
-  float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
-  float b0 = 0.0f, b1 = 0.0f, b2 = 0.0f, b3 = 0.0f;
-#pragma unroll 4
-  for (int d = 0; d < LISA_ATT_HD; d += 8) {
+  float a[6][4];
+#pragma unroll
+  for (int i = 0; i < 6; ++i) a[i][0] = a[i][1] = a[i][2] = a[i][3] = 0.0f;
+#pragma unroll 2
+  for (int d = 0; d < HD; d += 8) {
     const uint4 kk = *reinterpret_cast<const uint4*>(kr + d);
-    const float k0 = lo_bf(kk.x), k1 = hi_bf(kk.x), k2 = lo_bf(kk.y), k3 = hi_bf(kk.y);
-    const float k4 = lo_bf(kk.z), k5 = hi_bf(kk.z), k6 = lo_bf(kk.w), k7 = hi_bf(kk.w);
-    a0 = lisa_fma(qa[d], k0, a0); a1 = lisa_fma(qa[d + 1], k1, a1); a2 = lisa_fma(qa[d + 2], k2, a2);
-    a3 = lisa_fma(qa[d + 3], k3, a3);
-    b0 = lisa_fma(qb[d], k0, b0); b1 = lisa_fma(qb[d + 1], k1, b1); b2 = lisa_fma(qb[d + 2], k2, b2);
-    b3 = lisa_fma(qb[d + 3], k3, b3);
-    a0 = lisa_fma(qa[d + 4], k4, a0); a1 = lisa_fma(qa[d + 5], k5, a1); a2 = lisa_fma(qa[d + 6], k6, a2);
-    a3 = lisa_fma(qa[d + 7], k7, a3);
-    b0 = lisa_fma(qb[d + 4], k4, b0); b1 = lisa_fma(qb[d + 5], k5, b1); b2 = lisa_fma(qb[d + 6], k6, b2);
-    b3 = lisa_fma(qb[d + 7], k7, b3);
+    const float k[8] = {lo_bf(kk.x), hi_bf(kk.x), lo_bf(kk.y), hi_bf(kk.y),
+                        lo_bf(kk.z), hi_bf(kk.z), lo_bf(kk.w), hi_bf(kk.w)};
+#pragma unroll
+    for (int half = 0; half < 2; ++half)
+#pragma unroll
+      for (int i = 0; i < 6; ++i)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) a[i][e] = lisa_fma(q[i * HD + d + 4 * half + e], k[4 * half + e], a[i][e]);
   }
-  const float sa = lane < n ? ((a0 + a1) + (a2 + a3)) * 0.0625f : -INFINITY;
-  const float sb = lane < n ? ((b0 + b1) + (b2 + b3)) * 0.0625f : -INFINITY;
-  const float ma = max64(sa), mb = max64(sb);
-  const float pa = (lane < n) ? lisa_exp2f(1.4426950408889634f * (sa - ma)) : 0.0f;
-  const float pbv = (lane < n) ? lisa_exp2f(1.4426950408889634f * (sb - mb)) : 0.0f;
-  const float da = tree64(pa), db = tree64(pbv);
-  pba[lane] = pa;
-  pbb[lane] = pbv;
+  float sc[6], mx[6], pv[6], den[6];
+#pragma unroll
+  for (int i = 0; i < 6; ++i) sc[i] = lane < n ? ((a[i][0] + a[i][1]) + (a[i][2] + a[i][3])) * 0.0625f : -INFINITY;
+#pragma unroll
+  for (int i = 0; i < 6; ++i) mx[i] = max64(sc[i]);
+#pragma unroll
+  for (int i = 0; i < 6; ++i) pv[i] = lane < n ? lisa_exp2f(1.4426950408889634f * (sc[i] - mx[i])) : 0.0f;
+#pragma unroll
+  for (int i = 0; i < 6; ++i) den[i] = tree64(pv[i]);
+#pragma unroll
+  for (int i = 0; i < 6; ++i) pb[i * LISA_ATT_SLICE + lane] = pv[i];
   if (lane == 0) {
-    mla[0] = ma;
-    mla[1] = da;
-    mlb[0] = mb;
-    mlb[1] = db;
+#pragma unroll
+    for (int i = 0; i < 6; ++i) {
+      ml[i * mls] = mx[i];
+      ml[i * mls + 1] = den[i];
+    }
+  }
+}
+
+// slice_pv3 over the six heads of a KV head: thread dp owns dimensions 2dp,
+// 2dp + 1 of each head, every chain over the tokens in order as there.
+DEV void slice_pv6(const float* pb6, const uint16_t* Vt, int n, int dp, float (&acc)[6][2]) {
+#pragma unroll
+  for (int i = 0; i < 6; ++i) acc[i][0] = acc[i][1] = 0.0f;
+#pragma unroll 4
+  for (int tok = 0; tok < n; ++tok) {
+    const uint32_t vw = *reinterpret_cast<const uint32_t*>(Vt + tok * LISA_ATT_HD + 2 * dp);
+    const float v0 = lo_bf(vw), v1 = hi_bf(vw);
+#pragma unroll
+    for (int i = 0; i < 6; ++i) {
+      const float pv = pb6[i * LISA_ATT_SLICE + tok];
+      acc[i][0] = lisa_fma(pv, v0, acc[i][0]);
+      acc[i][1] = lisa_fma(pv, v1, acc[i][1]);
+    }
   }
 }
 
@@ -2927,31 +2952,30 @@ extern "C" __global__ __launch_bounds__(LISA_ATT_ROWS_THREADS) void lisa_attn_pa
     *reinterpret_cast<uint4*>(&Vt[row * HD + col]) = *reinterpret_cast<const uint4*>(p.value_cache + off);
   }
   __syncthreads();
-  // scores: item (row tt, head pair) per wave, as the decode partial
-  for (int it = wave; it < nr * 3; it += NW) {
-    const int tt = it / 3, i = 2 * (it % 3), h = kvh * 6 + i, t = r0 + tt;
+  // scores: item (row tt, all six heads of the KV head) per wave
+  for (int tt = wave; tt < nr; tt += NW) {
+    const int t = r0 + tt, h = kvh * 6;
     const uint32_t ctx = base + t + 1;
     if (ctx <= t0) continue;
     const int n = (int)min((uint32_t)T, ctx - t0);
-    const lisa_cfloat_ptr qa = (lisa_cfloat_ptr)(p.query + ((size_t)t * LISA_ATT_QH + h) * HD);
+    const lisa_cfloat_ptr q = (lisa_cfloat_ptr)(p.query + ((size_t)t * LISA_ATT_QH + h) * HD);
     float* ml = p.part_ml + (((size_t)t * LISA_ATT_QH + h) * p.s_max + s) * 2;
-    slice_scores2_sq(qa, qa + HD, Kt, KP, n, lane, pb + (tt * 6 + i) * T, pb + (tt * 6 + i + 1) * T, ml,
-                     ml + (size_t)p.s_max * 2);
+    slice_scores6_sq(q, Kt, KP, n, lane, pb + tt * 6 * T, ml, (size_t)p.s_max * 2);
   }
   __syncthreads();
-  // P.V: thread (dp, hg, rr) owns dimensions 2dp, 2dp+1 of heads 3hg..3hg+2
-  // of rows rr, rr + NT / 256, ..
-  const int dp = tid & 127, hg = (tid >> 7) & 1;
-  for (int tt = tid >> 8; tt < nr; tt += NT / 256) {
+  // P.V: thread (dp, rr) owns dimensions 2dp, 2dp+1 of the six heads of rows
+  // rr, rr + NT / 128, ..
+  const int dp = tid & 127;
+  for (int tt = tid >> 7; tt < nr; tt += NT / 128) {
     const int t = r0 + tt;
     const uint32_t ctx = base + t + 1;
     if (ctx <= t0) continue;
     const int n = (int)min((uint32_t)T, ctx - t0);
-    float acc[3][2];
-    slice_pv3(pb + (tt * 6 + 3 * hg) * T, Vt, n, dp, acc);
+    float acc[6][2];
+    slice_pv6(pb + tt * 6 * T, Vt, n, dp, acc);
 #pragma unroll
-    for (int i = 0; i < 3; ++i) {
-      const int h = kvh * 6 + 3 * hg + i;
+    for (int i = 0; i < 6; ++i) {
+      const int h = kvh * 6 + i;
       *reinterpret_cast<float2*>(p.part_o + (((size_t)t * LISA_ATT_QH + h) * p.s_max + s) * HD + 2 * dp) =
           make_float2(acc[i][0], acc[i][1]);
     }
