@@ -1760,7 +1760,7 @@ extern "C" __global__ __launch_bounds__(256) void lisa_gdn_scan_rows(LisaGdnPara
       dst[4 * i] = f.x; dst[4 * i + 1] = f.y; dst[4 * i + 2] = f.z; dst[4 * i + 3] = f.w;
     }
   };
-  // one time step of both rows: the state update and the readout y = q . S
+  // one time step of the lane's rows: the state update and the readout y = q . S
   auto step = [&](int j, lisa_f32x2 g, const float (&vin)[R], float (&yo)[R]) {
     float kv[8], qv[8];
     rd(j, 0, kv);
